@@ -1,0 +1,154 @@
+"""ctypes binding of libgse.so (include/gse.h), in the style of goethe_engine/gc_c.py:58-77 (bind with an ABI check,
+size-first structs) and gc_c.py:222-227 (a negative return code becomes RuntimeError with the library's last error).
+
+torch is imported before the library is loaded so that libgse.so binds to the HIP runtime torch already mapped (both
+carry the soname libamdhip64.so.7): one runtime, so torch's streams and device pointers are valid in libgse calls.
+"""
+import ctypes as C
+import os
+import threading
+
+import numpy as np
+import torch
+
+ABI_MAJOR, ABI_MINOR = 1, 0
+OK, E_ARG, E_DEVICE, E_UNSUPPORTED, E_CAPACITY = 0, -1, -4, -5, -7
+F32, BF16 = 0, 1
+ROW_TEMP_UNDERFLOW = 1
+BATCH_EXACT = 1
+BATCH_PROFILE = 2
+MAX_LOGPROBS = 64
+P_ = C.POINTER
+
+PATH = os.environ.get("GSE_LIB", os.path.join(os.path.dirname(os.path.abspath(__file__)), "libgse.so"))
+
+# gse_row (72 bytes): the per-row parameter record, built as a numpy structured array and copied to the device.
+ROW = np.dtype({
+    "names": ["temperature", "top_k", "top_p", "min_p", "repetition_penalty", "frequency_penalty",
+              "presence_penalty", "mask_row", "seed", "idx", "hist_begin", "hist_end", "logprobs", "flags"],
+    "formats": [np.float32, np.int32, np.float64, np.float64, np.float32, np.float32, np.float32, np.int32,
+                np.uint64, np.uint64, np.int32, np.int32, np.int32, np.uint32],
+    "offsets": [0, 4, 8, 16, 24, 28, 32, 36, 40, 48, 56, 60, 64, 68],
+    "itemsize": 72})
+
+
+class OpenParams(C.Structure):
+    _fields_ = [("size", C.c_uint32), ("device", C.c_int32), ("max_rows", C.c_uint32), ("max_vocab", C.c_uint32)]
+
+
+class Batch(C.Structure):
+    _fields_ = [("size", C.c_uint32), ("dtype", C.c_uint32), ("rows", C.c_uint32), ("vocab", C.c_uint32),
+                ("ld", C.c_int64), ("logits", C.c_void_p), ("params", C.c_void_p), ("mask", C.c_void_p),
+                ("mask_ld", C.c_int64), ("hist", C.c_void_p), ("uniforms", C.c_void_p), ("stream", C.c_void_p),
+                ("flags", C.c_uint32), ("reserved", C.c_uint32)]
+
+
+class Out(C.Structure):
+    _fields_ = [("size", C.c_uint32), ("reserved", C.c_uint32), ("tokens", C.c_void_p), ("processed", C.c_void_p),
+                ("processed_ld", C.c_int64), ("logprob_ids", C.c_void_p), ("logprobs", C.c_void_p),
+                ("logprobs_ld", C.c_int64)]
+
+
+class MssBatch(C.Structure):
+    _fields_ = [("size", C.c_uint32), ("nodes", C.c_uint32), ("vocab", C.c_uint32), ("max_kids", C.c_uint32),
+                ("p", C.c_void_p), ("p_ld", C.c_int64), ("q", C.c_void_p), ("q_ld", C.c_int64),
+                ("kid_tok", C.c_void_p), ("kid_q", C.c_void_p), ("seed", C.c_void_p), ("idx", C.c_void_p),
+                ("out_token", C.c_void_p), ("out_kid", C.c_void_p), ("stream", C.c_void_p)]
+
+
+SIGNATURES = dict(
+    gse_abi_version=(C.c_uint32, []),
+    gse_open=(C.c_int, [P_(OpenParams), P_(C.c_void_p)]),
+    gse_sample=(C.c_int, [C.c_void_p, P_(Batch), P_(Out)]),
+    gse_dist=(C.c_int, [C.c_void_p, P_(Batch), C.c_void_p, C.c_int64]),
+    gse_draw=(C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p,
+                        C.c_void_p]),
+    gse_mss=(C.c_int, [C.c_void_p, P_(MssBatch)]),
+    gse_pack_mask=(C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_uint32, C.c_uint32, C.c_void_p, C.c_int64,
+                             C.c_void_p]),
+    gse_profile=(C.c_int, [C.c_void_p, P_(C.c_float), C.c_uint32, P_(C.c_uint32)]),
+    gse_last_error=(C.c_char_p, [C.c_void_p]),
+    gse_close=(None, [C.c_void_p]),
+)
+
+
+def bind(path=PATH):
+    """The library at path with its gse.h signatures; refuses a different ABI major or an older minor."""
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built: run __graft_entry__.build() (hipcc --offload-arch=gfx950)")
+    L = C.CDLL(path)
+    for n, (res, args) in SIGNATURES.items():
+        f = getattr(L, n)
+        f.restype, f.argtypes = res, args
+    v = L.gse_abi_version()
+    if v >> 16 != ABI_MAJOR or (v & 0xFFFF) < ABI_MINOR:
+        raise RuntimeError(f"{path}: C ABI {v >> 16}.{v & 0xFFFF}, this module needs {ABI_MAJOR}.{ABI_MINOR}+")
+    return L
+
+
+_lock = threading.Lock()
+_L = None
+_handles = {}
+
+
+def lib():
+    global _L
+    if _L is None:
+        _L = bind()
+    return _L
+
+
+class Handle:
+    """One gse handle on one device, reopened larger when a call needs more rows or a larger vocabulary."""
+
+    def __init__(self, device, rows, vocab):
+        self.L = lib()
+        self.device, self.rows, self.vocab = device, rows, vocab
+        h = C.c_void_p()
+        p = OpenParams(C.sizeof(OpenParams), device, rows, vocab)
+        rc = self.L.gse_open(C.byref(p), C.byref(h))
+        if rc != OK:
+            raise RuntimeError(f"gse_open failed ({rc}): {(self.L.gse_last_error(None) or b'').decode()}")
+        self.h = h
+
+    def ck(self, rc, what):
+        if rc < 0:
+            why = (self.L.gse_last_error(self.h) or b"").decode()
+            raise RuntimeError(f"{what} failed ({rc}): {why}")
+
+    def profile(self):
+        """(calls, total milliseconds per kernel: scan, exact[, dist]) of the calls made with BATCH_PROFILE since the
+        last read; clears the record."""
+        ms = (C.c_float * 4)()
+        calls = C.c_uint32()
+        n = self.L.gse_profile(self.h, ms, 4, C.byref(calls))
+        self.ck(n, "gse_profile")
+        return calls.value, [float(ms[i]) for i in range(n)]
+
+    def close(self):
+        if self.h:
+            self.L.gse_close(self.h)
+            self.h = None
+
+
+def handle(device, rows, vocab):
+    """A handle on device that fits rows x vocab (one per device, grown on demand)."""
+    if not torch.cuda.is_available():
+        raise RuntimeError("goethe-engine_amd needs a HIP device (torch.cuda.is_available() is False)")
+    with _lock:
+        h = _handles.get(device)
+        if h is None or h.rows < rows or h.vocab < vocab:
+            if h is not None:
+                torch.cuda.synchronize(device)
+                h.close()
+            h = Handle(device, max(rows, h.rows if h else 0, 64), max(vocab, h.vocab if h else 0))
+            _handles[device] = h
+        return h
+
+
+def ptr(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def stream_of(device):
+    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)

@@ -1,0 +1,305 @@
+// Host side of the C ABI in include/gse.h: handle, device workspace, argument checks, launches.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+#include <string>
+
+#include "gse_dev.h"
+#include "gse_int.h"
+
+struct gse_handle {
+  int device = 0;
+  uint32_t max_rows = 0, max_vocab = 0, nchmax = 0;
+  gse::ChunkHdr *hdr = nullptr;
+  uint64_t *cand = nullptr;
+  gse::RowInfo *info = nullptr;
+  uint32_t *done = nullptr;
+  hipEvent_t (*ring)[4] = nullptr;  // kernel boundaries of up to GSE_PROFILE_CALLS profiled calls
+  int nring = 0;                    // calls recorded
+  int nprof = 0;                    // kernels per recorded call
+  std::string err;
+};
+
+namespace {
+
+thread_local std::string g_open_err;
+
+int fail(gse_handle *h, int rc, const char *fmt, ...) __attribute__((format(printf, 3, 4)));
+int fail(gse_handle *h, int rc, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (h) h->err = buf;
+  else g_open_err = buf;
+  return rc;
+}
+
+int hip_fail(gse_handle *h, hipError_t e, const char *what) {
+  return fail(h, GSE_E_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Copies min(caller size, own size) bytes of a size-first struct; absent fields stay zero.
+template <typename T>
+bool take(const T *src, T &dst) {
+  memset(&dst, 0, sizeof dst);
+  if (!src) return false;
+  uint32_t n = src->size;
+  if (n < 8) return false;
+  memcpy(&dst, src, n < sizeof(T) ? n : sizeof(T));
+  return true;
+}
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+// The event slot of the next profiled call (kernels per call must stay the same between two reads).
+int prof_slot(gse_handle *h, int kernels, hipEvent_t **ev) {
+  *ev = nullptr;
+  if (!h->ring) {
+    h->ring = new (std::nothrow) hipEvent_t[GSE_PROFILE_CALLS][4];
+    if (!h->ring) return fail(h, GSE_E_DEVICE, "out of host memory");
+    for (int c = 0; c < GSE_PROFILE_CALLS; ++c)
+      for (int i = 0; i < 4; ++i) {
+        hipError_t e = hipEventCreate(&h->ring[c][i]);
+        if (e != hipSuccess) return hip_fail(h, e, "event create");
+      }
+  }
+  if (h->nring > 0 && h->nprof != kernels) h->nring = 0;
+  h->nprof = kernels;
+  if (h->nring >= GSE_PROFILE_CALLS) return GSE_OK;  // record full: later calls run unprofiled until the next read
+  *ev = h->ring[h->nring++];
+  return GSE_OK;
+}
+
+int check_batch(gse_handle *h, const gse_batch &b) {
+  if (!b.logits || !b.params) return fail(h, GSE_E_ARG, "logits and params are required");
+  if (b.dtype != GSE_F32 && b.dtype != GSE_BF16) return fail(h, GSE_E_ARG, "dtype %u is neither f32 nor bf16", b.dtype);
+  if (b.vocab == 0) return fail(h, GSE_E_ARG, "vocab is 0");
+  if (b.ld < (int64_t)b.vocab) return fail(h, GSE_E_ARG, "ld %lld < vocab %u", (long long)b.ld, b.vocab);
+  if (b.rows > h->max_rows)
+    return fail(h, GSE_E_CAPACITY, "%u rows, the handle was opened for %u", b.rows, h->max_rows);
+  if (b.vocab > h->max_vocab)
+    return fail(h, GSE_E_CAPACITY, "vocab %u, the handle was opened for %u", b.vocab, h->max_vocab);
+  if (b.mask && b.mask_ld < (int64_t)((b.vocab + 31) / 32))
+    return fail(h, GSE_E_ARG, "mask_ld %lld < ceil(vocab / 32)", (long long)b.mask_ld);
+  return GSE_OK;
+}
+
+gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
+  gse::ScanArgs a = {};
+  a.logits = b.logits;
+  a.ld = b.ld;
+  a.dtype = (int)b.dtype;
+  a.V = (int)b.vocab;
+  a.rows = (int)b.rows;
+  a.nch = (int)((b.vocab + gse::CH - 1) / gse::CH);
+  a.nchmax = (int)h->nchmax;
+  a.mode = mode;
+  a.force_exact = (b.flags & GSE_BATCH_EXACT) ? 1 : 0;
+  a.params = b.params;
+  a.mask = b.mask;
+  a.mask_ld = b.mask_ld;
+  a.hist = b.hist;
+  a.uni = b.uniforms;
+  a.hdr = h->hdr;
+  a.cand = h->cand;
+  a.info = h->info;
+  a.done = h->done;
+  return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+GSE_API uint32_t gse_abi_version(void) { return GSE_ABI_VERSION; }
+
+GSE_API int gse_open(const gse_open_params *p, gse_handle **out) {
+  gse_open_params o;
+  if (!out || !take(p, o)) return fail(nullptr, GSE_E_ARG, "gse_open: null or short gse_open_params");
+  *out = nullptr;
+  if (o.max_rows == 0 || o.max_vocab == 0) return fail(nullptr, GSE_E_ARG, "max_rows and max_vocab must be > 0");
+  if (o.max_vocab > (1u << 21)) return fail(nullptr, GSE_E_CAPACITY, "max_vocab %u > 2^21", o.max_vocab);
+  int ndev = 0;
+  hipError_t e = hipGetDeviceCount(&ndev);
+  if (e != hipSuccess || ndev == 0) return fail(nullptr, GSE_E_DEVICE, "no HIP device: %s", hipGetErrorString(e));
+  if (o.device < 0 || o.device >= ndev) return fail(nullptr, GSE_E_DEVICE, "device %d of %d", o.device, ndev);
+  hipDeviceProp_t prop;
+  if ((e = hipGetDeviceProperties(&prop, o.device)) != hipSuccess)
+    return fail(nullptr, GSE_E_DEVICE, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(nullptr, GSE_E_DEVICE, "device %d is %s; this library is built for gfx950", o.device, prop.gcnArchName);
+  gse_handle *h = new (std::nothrow) gse_handle();
+  if (!h) return fail(nullptr, GSE_E_DEVICE, "out of host memory");
+  DeviceGuard g(o.device);
+  h->device = o.device;
+  h->max_rows = o.max_rows;
+  h->max_vocab = o.max_vocab;
+  h->nchmax = (o.max_vocab + gse::CH - 1) / gse::CH;
+  const size_t nrc = (size_t)h->max_rows * h->nchmax;
+  if ((e = hipMalloc(&h->hdr, nrc * sizeof(gse::ChunkHdr))) != hipSuccess ||
+      (e = hipMalloc(&h->cand, nrc * gse::CAPC * sizeof(uint64_t))) != hipSuccess ||
+      (e = hipMalloc(&h->info, (size_t)h->max_rows * sizeof(gse::RowInfo))) != hipSuccess ||
+      (e = hipMalloc(&h->done, (size_t)h->max_rows * sizeof(uint32_t))) != hipSuccess ||
+      (e = hipMemset(h->done, 0, (size_t)h->max_rows * sizeof(uint32_t))) != hipSuccess ||
+      (e = hipMemset(h->info, 0, (size_t)h->max_rows * sizeof(gse::RowInfo))) != hipSuccess ||
+      (e = hipDeviceSynchronize()) != hipSuccess) {
+    fail(nullptr, GSE_E_DEVICE, "workspace allocation (%zu rows x chunks): %s", nrc, hipGetErrorString(e));
+    gse_close(h);
+    return GSE_E_DEVICE;
+  }
+  *out = h;
+  return GSE_OK;
+}
+
+GSE_API int gse_sample(gse_handle *h, const gse_batch *in, const gse_out *out) {
+  if (!h) return fail(nullptr, GSE_E_ARG, "null handle");
+  gse_batch b;
+  gse_out o;
+  if (!take(in, b) || !take(out, o)) return fail(h, GSE_E_ARG, "null or short gse_batch / gse_out");
+  int rc = check_batch(h, b);
+  if (rc) return rc;
+  if (!o.tokens) return fail(h, GSE_E_ARG, "tokens output is required");
+  if ((o.logprob_ids == nullptr) != (o.logprobs == nullptr))
+    return fail(h, GSE_E_ARG, "logprob_ids and logprobs go together");
+  if (o.logprob_ids && o.logprobs_ld < GSE_MAX_LOGPROBS && o.logprobs_ld <= 0)
+    return fail(h, GSE_E_ARG, "logprobs_ld must be > 0");
+  if (o.processed && o.processed_ld < (int64_t)b.vocab) return fail(h, GSE_E_ARG, "processed_ld < vocab");
+  if (b.rows == 0) return GSE_OK;
+  DeviceGuard g(h->device);
+  gse::ScanArgs a = make_args(h, b, gse::MODE_SAMPLE);
+  a.processed = o.processed;
+  a.processed_ld = o.processed_ld;
+  a.tokens = o.tokens;
+  a.lp_ids = o.logprob_ids;
+  a.lps = o.logprobs;
+  a.lp_ld = o.logprobs_ld;
+  hipStream_t s = (hipStream_t)b.stream;
+  hipEvent_t *ev = nullptr;
+  if ((b.flags & GSE_BATCH_PROFILE) && (rc = prof_slot(h, 2, &ev)) != GSE_OK) return rc;
+  hipError_t e;
+  if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(h, e, "event record");
+  if ((e = gse::launch_scan(a, s)) != hipSuccess) return hip_fail(h, e, "scan launch");
+  if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return hip_fail(h, e, "event record");
+  if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
+  if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return hip_fail(h, e, "event record");
+  return GSE_OK;
+}
+
+GSE_API int gse_dist(gse_handle *h, const gse_batch *in, double *probs, int64_t probs_ld) {
+  if (!h) return fail(nullptr, GSE_E_ARG, "null handle");
+  gse_batch b;
+  if (!take(in, b)) return fail(h, GSE_E_ARG, "null or short gse_batch");
+  int rc = check_batch(h, b);
+  if (rc) return rc;
+  if (!probs || probs_ld < (int64_t)b.vocab) return fail(h, GSE_E_ARG, "probs missing or probs_ld < vocab");
+  if (b.rows == 0) return GSE_OK;
+  DeviceGuard g(h->device);
+  gse::ScanArgs a = make_args(h, b, gse::MODE_DIST);
+  hipStream_t s = (hipStream_t)b.stream;
+  hipEvent_t *ev = nullptr;
+  if ((b.flags & GSE_BATCH_PROFILE) && (rc = prof_slot(h, 3, &ev)) != GSE_OK) return rc;
+  hipError_t e;
+  if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(h, e, "event record");
+  if ((e = gse::launch_scan(a, s)) != hipSuccess) return hip_fail(h, e, "scan launch");
+  if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return hip_fail(h, e, "event record");
+  if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
+  if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return hip_fail(h, e, "event record");
+  if ((e = gse::launch_dist_write(a, probs, probs_ld, s)) != hipSuccess) return hip_fail(h, e, "dist launch");
+  if (ev && (e = hipEventRecord(ev[3], s)) != hipSuccess) return hip_fail(h, e, "event record");
+  return GSE_OK;
+}
+
+GSE_API int gse_draw(gse_handle *h, const double *q, int64_t q_ld, uint32_t rows, uint32_t vocab, const double *u,
+                     int32_t *out, void *stream) {
+  if (!h) return fail(nullptr, GSE_E_ARG, "null handle");
+  if (!q || !u || !out) return fail(h, GSE_E_ARG, "q, u and out are required");
+  if (vocab == 0 || q_ld < (int64_t)vocab) return fail(h, GSE_E_ARG, "vocab 0 or q_ld < vocab");
+  if (rows == 0) return GSE_OK;
+  DeviceGuard g(h->device);
+  hipError_t e = gse::launch_draw(q, q_ld, (int)rows, (int)vocab, u, out, (hipStream_t)stream);
+  return e == hipSuccess ? GSE_OK : hip_fail(h, e, "draw launch");
+}
+
+GSE_API int gse_mss(gse_handle *h, const gse_mss_batch *in) {
+  if (!h) return fail(nullptr, GSE_E_ARG, "null handle");
+  gse_mss_batch b;
+  if (!take(in, b)) return fail(h, GSE_E_ARG, "null or short gse_mss_batch");
+  if (!b.p || !b.kid_tok || !b.kid_q || !b.seed || !b.idx || !b.out_token || !b.out_kid)
+    return fail(h, GSE_E_ARG, "p, kid_tok, kid_q, seed, idx, out_token, out_kid are required");
+  if (b.vocab == 0 || b.p_ld < (int64_t)b.vocab) return fail(h, GSE_E_ARG, "vocab 0 or p_ld < vocab");
+  if (b.q && b.q_ld < (int64_t)b.vocab) return fail(h, GSE_E_ARG, "q_ld < vocab");
+  if (b.nodes == 0) return GSE_OK;
+  DeviceGuard g(h->device);
+  hipError_t e = gse::launch_mss(b, (hipStream_t)b.stream);
+  return e == hipSuccess ? GSE_OK : hip_fail(h, e, "mss launch");
+}
+
+GSE_API int gse_pack_mask(gse_handle *h, const uint8_t *bools, int64_t bool_ld, uint32_t rows, uint32_t vocab,
+                          int32_t *words, int64_t words_ld, void *stream) {
+  if (!h) return fail(nullptr, GSE_E_ARG, "null handle");
+  if (!bools || !words) return fail(h, GSE_E_ARG, "bools and words are required");
+  if (bool_ld < (int64_t)vocab || words_ld < (int64_t)((vocab + 31) / 32))
+    return fail(h, GSE_E_ARG, "bool_ld < vocab or words_ld < ceil(vocab / 32)");
+  if (rows == 0 || vocab == 0) return GSE_OK;
+  DeviceGuard g(h->device);
+  hipError_t e = gse::launch_pack(bools, bool_ld, (int)rows, (int)vocab, words, words_ld, (hipStream_t)stream);
+  return e == hipSuccess ? GSE_OK : hip_fail(h, e, "pack launch");
+}
+
+GSE_API int gse_profile(gse_handle *h, float *ms, uint32_t n, uint32_t *calls) {
+  if (!h) return fail(nullptr, GSE_E_ARG, "null handle");
+  for (uint32_t i = 0; i < n && ms; ++i) ms[i] = 0.0f;
+  if (calls) *calls = (uint32_t)h->nring;
+  if (h->nring == 0) return 0;
+  DeviceGuard g(h->device);
+  hipError_t e = hipEventSynchronize(h->ring[h->nring - 1][h->nprof]);
+  if (e != hipSuccess) return hip_fail(h, e, "event synchronize");
+  for (int c = 0; c < h->nring; ++c) {
+    for (int i = 0; i < h->nprof && (uint32_t)i < n; ++i) {
+      float t = 0.0f;
+      if ((e = hipEventElapsedTime(&t, h->ring[c][i], h->ring[c][i + 1])) != hipSuccess)
+        return hip_fail(h, e, "event elapsed");
+      if (ms) ms[i] += t;
+    }
+  }
+  const int k = h->nprof;
+  h->nring = 0;
+  return k;
+}
+
+GSE_API const char *gse_last_error(gse_handle *h) { return h ? h->err.c_str() : g_open_err.c_str(); }
+
+GSE_API void gse_close(gse_handle *h) {
+  if (!h) return;
+  {
+    DeviceGuard g(h->device);
+    (void)hipDeviceSynchronize();
+    if (h->hdr) (void)hipFree(h->hdr);
+    if (h->cand) (void)hipFree(h->cand);
+    if (h->info) (void)hipFree(h->info);
+    if (h->done) (void)hipFree(h->done);
+    if (h->ring) {
+      for (int c = 0; c < GSE_PROFILE_CALLS; ++c)
+        for (int i = 0; i < 4; ++i)
+          if (h->ring[c][i]) (void)hipEventDestroy(h->ring[c][i]);
+      delete[] h->ring;
+    }
+  }
+  delete h;
+}
+
+}  // extern "C"

@@ -1,0 +1,193 @@
+// Device helpers shared by the selection kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/gse.h"
+
+namespace gse {
+
+constexpr int WAVE = 64;
+constexpr int CH = 8192;           // tokens per chunk (one scan workgroup)
+constexpr int SCAN_THREADS = 256;  // 4 waves
+constexpr int EPT = CH / SCAN_THREADS;  // 32 tokens per thread, kept in registers as keys
+
+// Order-preserving 32-bit keys of fp32 values: larger value -> larger key; -0 and +0 share a key (numpy's stable
+// argsort sees them as equal); NaN -> 0, below every other key (numpy sorts NaN of -z last).
+constexpr uint32_t KEY_NEGINF = 0x007FFFFFu;
+constexpr uint32_t KEY_POSINF = 0xFF800000u;
+constexpr uint32_t KEY_ZERO = 0x80000000u;
+
+__device__ __forceinline__ uint32_t fkey(float f) {
+  uint32_t b = __float_as_uint(f);
+  if ((b & 0x7FFFFFFFu) == 0u) return KEY_ZERO;
+  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float fkey_inv(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// Packed sort key: key desc, then token id asc, as one u64 compared descending.
+__device__ __forceinline__ uint64_t pack(uint32_t key, uint32_t id) {
+  return ((uint64_t)key << 32) | (uint64_t)(0xFFFFFFFFu - id);
+}
+__device__ __forceinline__ uint32_t pk_key(uint64_t p) { return (uint32_t)(p >> 32); }
+__device__ __forceinline__ uint32_t pk_id(uint64_t p) { return 0xFFFFFFFFu - (uint32_t)p; }
+
+// splitmix64 (goethe_engine/sampling.py:42-47) and uniform (sampling.py:50-51).
+__device__ __forceinline__ uint64_t mix64(uint64_t seed, uint64_t i) {
+  uint64_t z = seed + (i + 1ull) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__device__ __forceinline__ double uniform64(uint64_t seed, uint64_t i) {
+  return (double)(mix64(seed, i) >> 11) * (1.0 / 9007199254740992.0);
+}
+
+// Correctly rounded fp32 x / T. The fp64 quotient q1 (one Markstein correction step from R = RN(1/T)) is within
+// about one fp64 ulp of x / T; an fp32 x / T that is not an fp32 midpoint lies at least 2^-49 (relative) away from
+// every midpoint, so rounding q1 to fp32 gives RN(x / T) for every normal result. Zero, subnormal, infinite and NaN
+// cases take the IEEE fp32 division.
+__device__ __forceinline__ float div_rn(float x, float T, double Td, double Rd) {
+  double xd = (double)x;
+  double q0 = xd * Rd;
+  double r = fma(-q0, Td, xd);
+  double q1 = fma(r, Rd, q0);
+  float z = (float)q1;
+  if (!(fabs(q1) >= 0x1p-125) || !(fabs(q1) <= 0x1p+127)) z = x / T;
+  return z;
+}
+
+// Penalties on one fp32 logit with history count c > 0: repetition, then frequency, then presence, each a separately
+// rounded fp32 operation (the file is built with -ffp-contract=off).
+__device__ __forceinline__ float penalize(float x, uint32_t c, float rp, float fp, float pp) {
+  float y = (x < 0.0f) ? __fmul_rn(x, rp) : __fdiv_rn(x, rp);
+  y = __fsub_rn(y, __fmul_rn(fp, (float)c));
+  return __fsub_rn(y, pp);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// Reads that bypass the non-coherent per-CU caches: data another workgroup of the same launch wrote.
+template <typename T>
+__device__ __forceinline__ T ld_acq(const T *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ void st_rel(T *p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (WAVE - 1)); }
+
+__device__ __forceinline__ uint32_t shfl_xor_u32(uint32_t v, int m) { return (uint32_t)__shfl_xor((int)v, m, WAVE); }
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  uint32_t lo = shfl_xor_u32((uint32_t)v, m), hi = shfl_xor_u32((uint32_t)(v >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ double shfl_up_f64(double v, int d) {
+  int2 b = *reinterpret_cast<int2 *>(&v);
+  b.x = __shfl_up(b.x, d, WAVE);
+  b.y = __shfl_up(b.y, d, WAVE);
+  return *reinterpret_cast<double *>(&b);
+}
+__device__ __forceinline__ double shfl_f64(double v, int src) {
+  int2 b = *reinterpret_cast<int2 *>(&v);
+  b.x = __shfl(b.x, src, WAVE);
+  b.y = __shfl(b.y, src, WAVE);
+  return *reinterpret_cast<double *>(&b);
+}
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+  uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src, WAVE), hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src, WAVE);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  for (int m = 32; m; m >>= 1) {
+    uint64_t o = shfl_xor_u64(v, m);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  for (int m = 32; m; m >>= 1) v = max(v, shfl_xor_u32(v, m));
+  return v;
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  for (int m = 32; m; m >>= 1) {
+    int2 b = *reinterpret_cast<int2 *>(&v);
+    b.x = __shfl_xor(b.x, m, WAVE);
+    b.y = __shfl_xor(b.y, m, WAVE);
+    v += *reinterpret_cast<double *>(&b);
+  }
+  return v;
+}
+// Inclusive prefix sum over the 64 lanes (Hillis-Steele, fixed association).
+__device__ __forceinline__ double wave_incl_scan_f64(double v) {
+  int l = lane_id();
+  for (int d = 1; d < WAVE; d <<= 1) {
+    double o = shfl_up_f64(v, d);
+    if (l >= d) v += o;
+  }
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  int l = lane_id();
+  for (int d = 1; d < WAVE; d <<= 1) {
+    uint32_t o = (uint32_t)__shfl_up((int)v, d, WAVE);
+    if (l >= d) v += o;
+  }
+  return v;
+}
+
+// Bitonic sort of one u32 per lane across the wave, descending: lane i ends with the i-th largest value.
+__device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) {
+  int l = lane_id();
+#pragma unroll
+  for (int k = 2; k <= WAVE; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      uint32_t o = shfl_xor_u32(v, j);
+      bool take_max = ((l & k) == 0) == ((l & j) == 0);
+      uint32_t mx = max(v, o), mn = min(v, o);
+      v = take_max ? mx : mn;
+    }
+  }
+  return v;
+}
+
+__device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Bitonic sort (descending) of n_pow2 u64 values in LDS by the whole workgroup; n_pow2 a power of two.
+__device__ __forceinline__ void block_sort_desc_u64(uint64_t *a, int n_pow2) {
+  for (int k = 2; k <= n_pow2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < n_pow2; i += blockDim.x) {
+        int p = i ^ j;
+        if (p > i) {
+          uint64_t x = a[i], y = a[p];
+          bool desc = (i & k) == 0;
+          if (desc ? (x < y) : (x > y)) {
+            a[i] = y;
+            a[p] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__host__ __device__ constexpr int pow2_ceil(int n) {
+  int p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+}  // namespace gse

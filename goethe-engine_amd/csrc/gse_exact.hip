@@ -1,0 +1,601 @@
+// Exact radix-select path: one 1024-thread workgroup per row that the scan marked hard. It finds the keep prefix and
+// the draw of goethe_engine/sampling.py:77-83 without sorting the row:
+//
+//   m   = min(top_k, #{q_i >= min_p * q_0}, first rank with cumsum(q)_i - q_i >= top_p)    (sampling.py:80)
+//   j   = first rank with cumsum(q)_i >= u * c_last, c_last = cumsum(q)_{m-1}             (sampling.py:81-83)
+//
+// Every rank / mass query walks a 4096-bin histogram of the 32-bit key (count and mass per bin), then collects the one
+// bin that holds the answer into LDS and sorts it; a bin too large to collect is refined with a histogram of its own
+// key range (12 bits per level), and a single key with more elements than fit is ordered by token id (the stable order).
+// Masses are exact sums of per-element fixed-point values (2^-64 resolution), so every prefix is deterministic and
+// the same whichever order the atomics land in.
+#include "gse_rowctx.h"
+
+namespace gse {
+
+namespace {
+
+constexpr int XT = 1024;         // threads
+constexpr int XW = XT / WAVE;    // waves
+constexpr int NB = 4096;         // histogram bins
+constexpr int CAPS = 8192;       // collected elements
+constexpr int PER = CH / XT;     // tokens per thread per chunk (contiguous)
+
+struct Fx {  // value = hi * 2^-40 + lo * 2^-64
+  uint64_t hi, lo;
+};
+__device__ __forceinline__ Fx fx_of(double e) {
+  const double s = e * 1099511627776.0;  // 2^40
+  const double h = floor(s);
+  Fx f;
+  f.hi = (uint64_t)h;
+  f.lo = (uint64_t)floor((s - h) * 16777216.0);  // 2^24
+  return f;
+}
+__device__ __forceinline__ Fx fx_add(Fx a, Fx b) { return Fx{a.hi + b.hi, a.lo + b.lo}; }
+__device__ __forceinline__ double fx_val(Fx a) {
+  return (double)a.hi * 9.094947017729282e-13 + (double)a.lo * 5.421010862427522e-20;  // 2^-40, 2^-64
+}
+
+struct ExactShared {
+  uint32_t cnt[CH];
+  union {
+    struct {
+      uint32_t c[NB];
+      uint64_t hi[NB];
+      uint64_t lo[NB];
+    } h;
+    struct {
+      uint64_t k[CAPS];
+      uint64_t phi[XT];
+      uint64_t plo[XT];
+    } col;
+  } u;
+  uint64_t wred[XW];
+  uint64_t wred2[XW];
+  double dred[XW];
+  uint64_t xs[4];
+  uint32_t n, found;
+};
+
+// Context of the row being finished.
+struct XCtx {
+  const int32_t *hist;
+  RowCtx c;
+  int row, nch;
+  double M, S;
+};
+
+// Calls f(t, key) for every token of the row, thread-contiguous inside each chunk (ids increase with (tid, i)).
+template <typename F>
+__device__ __forceinline__ void for_each_key(const XCtx &x, ExactShared &sh, F f) {
+  const int tid = threadIdx.x;
+  for (int ch = 0; ch < x.nch; ++ch) {
+    const int c0 = ch * CH;
+    if (x.c.pen) build_counts(x.c, x.hist, c0, sh.cnt);
+    const int t0 = c0 + tid * PER;
+    const uint32_t mword = x.c.mw ? (t0 < x.c.V ? x.c.mw[t0 >> 5] : 0u) : 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int t = t0 + i;
+      if (t < x.c.V) {
+        const uint32_t ct = x.c.pen ? sh.cnt[t - c0] : 0u;
+        bool fn = false, ff = false;
+        float xm;
+        const uint32_t k = elem_key(x.c, load_one(x.c, t), ct, (mword >> (t & 31)) & 1u, fn, ff, xm);
+        f(t, k);
+      }
+    }
+    if (x.c.pen) __syncthreads();
+  }
+}
+
+// ---- block reductions / scans (1024 threads) ------------------------------------------------------------------------
+
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, ExactShared &sh) {
+  v = wave_max_u64(v);
+  __syncthreads();
+  if (lane_id() == 0) sh.wred[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint64_t r = 0;
+  for (int w = 0; w < XW; ++w) r = sh.wred[w] > r ? sh.wred[w] : r;
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+  for (int m = 32; m; m >>= 1) v += shfl_xor_u64(v, m);
+  return v;
+}
+
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, ExactShared &sh) {
+  v = wave_sum_u64(v);
+  __syncthreads();
+  if (lane_id() == 0) sh.wred[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint64_t r = 0;
+  for (int w = 0; w < XW; ++w) r += sh.wred[w];
+  __syncthreads();
+  return r;
+}
+
+// Deterministic block sum: wave tree, then waves in order.
+__device__ __forceinline__ double block_sum_f64(double v, ExactShared &sh) {
+  v = wave_sum_f64(v);
+  __syncthreads();
+  if (lane_id() == 0) sh.dred[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double r = 0.0;
+  for (int w = 0; w < XW; ++w) r += sh.dred[w];
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) {
+  const int l = lane_id();
+  for (int d = 1; d < WAVE; d <<= 1) {
+    const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)v, d, WAVE);
+    const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)(v >> 32), d, WAVE);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    if (l >= d) v += o;
+  }
+  return v;
+}
+
+// Exclusive block scan of two u64 values per thread (in thread order).
+__device__ __forceinline__ void block_excl_scan2(uint64_t &a, uint64_t &b, ExactShared &sh) {
+  const uint64_t ia = wave_incl_scan_u64(a), ib = wave_incl_scan_u64(b);
+  __syncthreads();
+  if (lane_id() == WAVE - 1) {
+    sh.wred[threadIdx.x >> 6] = ia;
+    sh.wred2[threadIdx.x >> 6] = ib;
+  }
+  __syncthreads();
+  uint64_t pa = 0, pb = 0;
+  const int w = threadIdx.x >> 6;
+  for (int k = 0; k < w; ++k) {
+    pa += sh.wred[k];
+    pb += sh.wred2[k];
+  }
+  a = pa + ia - a;
+  b = pb + ib - b;
+  __syncthreads();
+}
+
+// ---- histogram over a key window --------------------------------------------------------------------------------------
+
+struct Win {
+  uint32_t lo, hi;   // key range of the window (inclusive)
+  int shift;         // bin width 2^shift keys
+  uint64_t above_n;  // elements with key above the window
+  Fx above_m;        // their mass
+};
+
+// Builds counts and masses of the keys inside the window.
+__device__ void build_hist(const XCtx &x, ExactShared &sh, const Win &w) {
+  for (int b = threadIdx.x; b < NB; b += XT) {
+    sh.u.h.c[b] = 0;
+    sh.u.h.hi[b] = 0;
+    sh.u.h.lo[b] = 0;
+  }
+  __syncthreads();
+  const double M = x.M;
+  for_each_key(x, sh, [&](int, uint32_t k) {
+    if (k >= w.lo && k <= w.hi) {
+      const int b = (int)((k - w.lo) >> w.shift);
+      atomicAdd(&sh.u.h.c[b], 1u);
+      if (k > KEY_NEGINF) {
+        const Fx f = fx_of(exp((double)fkey_inv(k) - M));
+        if (f.hi) atomicAdd((unsigned long long *)&sh.u.h.hi[b], (unsigned long long)f.hi);
+        if (f.lo) atomicAdd((unsigned long long *)&sh.u.h.lo[b], (unsigned long long)f.lo);
+      }
+    }
+  });
+  __syncthreads();
+}
+
+// Query kinds: rank (0-based) / first rank whose exclusive mass >= target / first rank whose inclusive mass >= target.
+enum { Q_RANK = 0, Q_EXCL = 1, Q_INCL = 2 };
+
+struct Hit {
+  int64_t rank;    // rank of the answer element (V when no element qualifies)
+  uint64_t pk;     // its packed key (0 when none)
+  Fx above;        // mass of all elements ranked before it
+  Fx self;         // its own mass
+};
+
+__device__ __forceinline__ bool q_pred(int kind, uint64_t r, int64_t n_before, Fx m_before, Fx m_incl, double S,
+                                       double tgt) {
+  if (kind == Q_RANK) return (int64_t)r < n_before;
+  if (kind == Q_EXCL) return fx_val(m_before) / S >= tgt;
+  return fx_val(m_incl) / S >= tgt;
+}
+
+// Finds, in the current histogram (descending bins), the first bin whose inclusive prefix satisfies the query.
+// Returns -1 when none does; fills the window-relative prefix before that bin.
+__device__ int find_bin(ExactShared &sh, const Win &w, int kind, uint64_t r, double S, double tgt, uint64_t &nb_out,
+                        Fx &mb_out) {
+  // thread t owns 4 consecutive bins in descending order: NB-1-4t ... NB-4-4t
+  const int tid = threadIdx.x;
+  uint64_t n4 = 0, h4 = 0, l4 = 0;
+  for (int i = 0; i < 4; ++i) {
+    const int b = NB - 1 - (4 * tid + i);
+    n4 += sh.u.h.c[b];
+    h4 += sh.u.h.hi[b];
+    l4 += sh.u.h.lo[b];
+  }
+  uint64_t pn = n4, ph = h4;
+  block_excl_scan2(pn, ph, sh);
+  uint64_t pl = l4, dummy = 0;
+  block_excl_scan2(pl, dummy, sh);
+  if (tid == 0) sh.found = 0xFFFFFFFFu;
+  __syncthreads();
+  uint64_t n = w.above_n + pn;
+  Fx m = fx_add(w.above_m, Fx{ph, pl});
+  for (int i = 0; i < 4; ++i) {
+    const int b = NB - 1 - (4 * tid + i);
+    const uint64_t cb = sh.u.h.c[b];
+    const Fx mb{sh.u.h.hi[b], sh.u.h.lo[b]};
+    const Fx mi = fx_add(m, mb);
+    bool hit;
+    if (kind == Q_RANK) hit = r < n + cb;
+    else if (kind == Q_EXCL) hit = cb > 0 && fx_val(mi) / S >= tgt;
+    else hit = cb > 0 && fx_val(mi) / S >= tgt;
+    if (hit) {
+      atomicMin(&sh.found, (uint32_t)(4 * tid + i));
+      break;
+    }
+    n += cb;
+    m = mi;
+  }
+  __syncthreads();
+  const uint32_t f = sh.found;
+  __syncthreads();
+  if (f == 0xFFFFFFFFu) return -1;
+  // recompute the prefix before bin index f (descending index) on one thread and broadcast
+  if (tid == (int)(f >> 2)) {
+    uint64_t nn = w.above_n + pn;
+    Fx mm = fx_add(w.above_m, Fx{ph, pl});
+    for (uint32_t i = 0; i < (f & 3u); ++i) {
+      const int b = NB - 1 - (int)(4 * (f >> 2) + i);
+      nn += sh.u.h.c[b];
+      mm = fx_add(mm, Fx{sh.u.h.hi[b], sh.u.h.lo[b]});
+    }
+    sh.xs[0] = nn;
+    sh.xs[1] = mm.hi;
+    sh.xs[2] = mm.lo;
+  }
+  __syncthreads();
+  nb_out = sh.xs[0];
+  mb_out = Fx{sh.xs[1], sh.xs[2]};
+  __syncthreads();
+  return NB - 1 - (int)f;
+}
+
+// Collects the packed keys of every element with key in [klo, khi] into LDS (sorted descending). Returns the count
+// (possibly above CAPS: then the list is partial).
+__device__ uint32_t collect(const XCtx &x, ExactShared &sh, uint32_t klo, uint32_t khi) {
+  if (threadIdx.x == 0) sh.n = 0;
+  __syncthreads();
+  for_each_key(x, sh, [&](int t, uint32_t k) {
+    if (k >= klo && k <= khi) {
+      const uint32_t pos = atomicAdd(&sh.n, 1u);
+      if (pos < (uint32_t)CAPS) sh.u.col.k[pos] = pack(k, (uint32_t)t);
+    }
+  });
+  __syncthreads();
+  const uint32_t n = sh.n;
+  if (n <= (uint32_t)CAPS) {
+    const int np2 = pow2_ceil(max((int)n, 2));
+    for (int i = (int)n + threadIdx.x; i < np2; i += XT) sh.u.col.k[i] = 0;
+    __syncthreads();
+    block_sort_desc_u64(sh.u.col.k, np2);
+  }
+  return n;
+}
+
+// Walks a collected, sorted list (n <= CAPS) for the query, with n_before / m_before the prefix above the list.
+// Returns the index inside the list (or n when no element qualifies) and fills the element's prefix mass.
+__device__ int walk_list(const XCtx &x, ExactShared &sh, int n, int kind, uint64_t r, uint64_t n_before, Fx m_before,
+                         double tgt, Fx &above, Fx &self) {
+  const int tid = threadIdx.x;
+  constexpr int PT = CAPS / XT;  // 8 elements per thread, consecutive
+  Fx ef[PT];
+  uint64_t sh_hi = 0, sh_lo = 0;
+  for (int i = 0; i < PT; ++i) {
+    const int idx = tid * PT + i;
+    ef[i] = Fx{0, 0};
+    if (idx < n) {
+      const uint32_t k = pk_key(sh.u.col.k[idx]);
+      if (k > KEY_NEGINF) ef[i] = fx_of(exp((double)fkey_inv(k) - x.M));
+    }
+    sh_hi += ef[i].hi;
+    sh_lo += ef[i].lo;
+  }
+  block_excl_scan2(sh_hi, sh_lo, sh);
+  if (tid == 0) sh.found = 0xFFFFFFFFu;
+  __syncthreads();
+  Fx m = fx_add(m_before, Fx{sh_hi, sh_lo});
+  for (int i = 0; i < PT; ++i) {
+    const int idx = tid * PT + i;
+    if (idx >= n) break;
+    const Fx mi = fx_add(m, ef[i]);
+    if (q_pred(kind, r, (int64_t)n_before + idx + 1, m, mi, x.S, tgt)) {
+      atomicMin(&sh.found, (uint32_t)idx);
+      break;
+    }
+    m = mi;
+  }
+  __syncthreads();
+  const uint32_t f = sh.found;
+  __syncthreads();
+  if (f == 0xFFFFFFFFu) return n;
+  if (tid == (int)(f / PT)) {
+    Fx mm = fx_add(m_before, Fx{sh_hi, sh_lo});
+    for (uint32_t i = 0; i < f % PT; ++i) mm = fx_add(mm, ef[i]);
+    sh.xs[0] = mm.hi;
+    sh.xs[1] = mm.lo;
+    sh.xs[2] = ef[f % PT].hi;
+    sh.xs[3] = ef[f % PT].lo;
+  }
+  __syncthreads();
+  above = Fx{sh.xs[0], sh.xs[1]};
+  self = Fx{sh.xs[2], sh.xs[3]};
+  __syncthreads();
+  return (int)f;
+}
+
+// Elements sharing one key, taken in token-id order: the token at position p (0-based) among them.
+__device__ uint32_t nth_with_key(const XCtx &x, ExactShared &sh, uint32_t key, uint64_t p) {
+  const int tid = threadIdx.x;
+  uint64_t base = 0;
+  if (tid == 0) sh.found = 0xFFFFFFFFu;
+  __syncthreads();
+  for (int ch = 0; ch < x.nch; ++ch) {
+    const int c0 = ch * CH;
+    if (x.c.pen) build_counts(x.c, x.hist, c0, sh.cnt);
+    const int t0 = c0 + tid * PER;
+    const uint32_t mword = x.c.mw ? (t0 < x.c.V ? x.c.mw[t0 >> 5] : 0u) : 0xFFFFFFFFu;
+    uint32_t match = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int t = t0 + i;
+      if (t < x.c.V) {
+        const uint32_t ct = x.c.pen ? sh.cnt[t - c0] : 0u;
+        bool fn = false, ff = false;
+        float xm;
+        if (elem_key(x.c, load_one(x.c, t), ct, (mword >> (t & 31)) & 1u, fn, ff, xm) == key) match |= 1u << i;
+      }
+    }
+    uint64_t cntm = (uint64_t)__popc(match), d = 0;
+    block_excl_scan2(cntm, d, sh);
+    const uint64_t total = block_sum_u64((uint64_t)__popc(match), sh);
+    const uint64_t mine = base + cntm;
+    if (p >= mine && p < mine + (uint64_t)__popc(match)) {
+      uint32_t left = (uint32_t)(p - mine), mm = match;
+      for (int i = 0; i < PER; ++i) {
+        if (mm & (1u << i)) {
+          if (left == 0) {
+            sh.found = (uint32_t)(t0 + i);
+            break;
+          }
+          --left;
+        }
+      }
+    }
+    base += total;
+    if (x.c.pen) __syncthreads();
+    __syncthreads();
+    if (sh.found != 0xFFFFFFFFu) break;
+  }
+  __syncthreads();
+  return sh.found;
+}
+
+// Runs one query to its element: histogram levels, collection, walk.
+__device__ Hit query(const XCtx &x, ExactShared &sh, int kind, uint64_t r, double tgt) {
+  Hit out;
+  Win w{0u, 0xFFFFFFFFu, 20, 0, Fx{0, 0}};
+  for (int level = 0; level < 3; ++level) {
+    build_hist(x, sh, w);
+    uint64_t nb = 0;
+    Fx mb{0, 0};
+    const int b = find_bin(sh, w, kind, r, x.S, tgt, nb, mb);
+    if (b < 0) {
+      out.rank = -1;
+      out.pk = 0;
+      return out;
+    }
+    const uint64_t cb = sh.u.h.c[b];
+    const uint32_t klo = w.lo + ((uint32_t)b << w.shift);
+    const uint32_t khi = w.shift == 0 ? klo : klo + ((1u << w.shift) - 1u);
+    __syncthreads();
+    if (cb <= (uint64_t)CAPS) {
+      const uint32_t n = collect(x, sh, klo, khi);
+      Fx above, self;
+      const int i = walk_list(x, sh, (int)n, kind, r, nb, mb, tgt, above, self);
+      if (i >= (int)n) {  // no element of the bin qualifies (exclusive mass): the answer is the next bin's first
+        out.rank = (int64_t)(nb + n);
+        out.pk = 0;
+        return out;
+      }
+      out.rank = (int64_t)(nb + i);
+      out.pk = sh.u.col.k[i];
+      out.above = above;
+      out.self = self;
+      __syncthreads();
+      return out;
+    }
+    if (w.shift == 0) {
+      // one key with more elements than fit: equal z, equal mass; the answer is positional in token-id order
+      const uint32_t k = klo;
+      const Fx e = k > KEY_NEGINF ? fx_of(exp((double)fkey_inv(k) - x.M)) : Fx{0, 0};
+      uint64_t pos;
+      if (kind == Q_RANK) {
+        pos = r - nb;
+      } else {
+        // smallest p with (before + p * e (+ e)) / S >= tgt; the bin holds the answer so p < cb
+        uint64_t lo = 0, hi = cb - 1;
+        while (lo < hi) {
+          const uint64_t mid = (lo + hi) / 2;
+          const Fx mp = fx_add(mb, Fx{e.hi * (mid + (kind == Q_INCL)), e.lo * (mid + (kind == Q_INCL))});
+          if (fx_val(mp) / x.S >= tgt) hi = mid;
+          else lo = mid + 1;
+        }
+        pos = lo;
+      }
+      const uint32_t t = nth_with_key(x, sh, k, pos);
+      out.rank = (int64_t)(nb + pos);
+      out.pk = pack(k, t);
+      out.above = fx_add(mb, Fx{e.hi * pos, e.lo * pos});
+      out.self = e;
+      return out;
+    }
+    w = Win{klo, khi, w.shift > 12 ? w.shift - 12 : 0, nb, mb};
+  }
+  out.rank = -1;
+  out.pk = 0;
+  return out;
+}
+
+__device__ uint64_t count_ge(const XCtx &x, ExactShared &sh, uint32_t kmin) {
+  uint64_t n = 0;
+  for_each_key(x, sh, [&](int, uint32_t k) { n += (k >= kmin) ? 1u : 0u; });
+  return block_sum_u64(n, sh);
+}
+
+// Collects the elements with packed key >= pk (the top ranks) and sorts them.
+__device__ uint32_t collect_top(const XCtx &x, ExactShared &sh, uint64_t pk) {
+  if (threadIdx.x == 0) sh.n = 0;
+  __syncthreads();
+  for_each_key(x, sh, [&](int t, uint32_t k) {
+    const uint64_t p = pack(k, (uint32_t)t);
+    if (p >= pk) {
+      const uint32_t pos = atomicAdd(&sh.n, 1u);
+      if (pos < (uint32_t)CAPS) sh.u.col.k[pos] = p;
+    }
+  });
+  __syncthreads();
+  const uint32_t n = min(sh.n, (uint32_t)CAPS);
+  const int np2 = pow2_ceil(max((int)n, 2));
+  for (int i = (int)n + threadIdx.x; i < np2; i += XT) sh.u.col.k[i] = 0;
+  __syncthreads();
+  block_sort_desc_u64(sh.u.col.k, np2);
+  return n;
+}
+
+__global__ __launch_bounds__(XT) void exact_kernel(ScanArgs a) {
+  const int row = blockIdx.x;
+  RowInfo *ri = a.info + row;
+  if (!(ri->flags & R_HARD)) return;
+  __shared__ ExactShared sh;
+  const int tid = threadIdx.x;
+  const gse_row P = a.params[row];
+  const bool greedy = is_greedy(a.mode, P);
+  XCtx x;
+  x.hist = a.hist;
+  x.row = row;
+  x.nch = a.nch;
+  x.c = make_ctx(a, row, P);
+  if (greedy) {  // logprobs of a greedy row are taken over z = x
+    x.c.greedy = false;
+    x.c.divide = false;
+  }
+  const int nlp = a.lp_ids ? min(min(P.logprobs, GSE_MAX_LOGPROBS), (int)a.lp_ld) : 0;
+  // pass 0: the row maximum of z
+  uint64_t best = 0;
+  for_each_key(x, sh, [&](int t, uint32_t k) {
+    const uint64_t p = pack(k, (uint32_t)t);
+    best = p > best ? p : best;
+  });
+  best = block_max_u64(best, sh);
+  const uint32_t mk = pk_key(best);
+  if (mk >= KEY_POSINF || mk <= KEY_NEGINF) {
+    for (int i = tid; i < nlp; i += XT) {
+      a.lp_ids[(int64_t)row * a.lp_ld + i] = -1;
+      a.lps[(int64_t)row * a.lp_ld + i] = __builtin_nanf("");
+    }
+    if (tid == 0) ri->flags = R_DONE | R_SPECIAL | (greedy ? R_GREEDY : 0u);
+    return;
+  }
+  x.M = (double)fkey_inv(mk);
+  // pass A: S (fixed thread order, deterministic)
+  double s = 0.0;
+  for_each_key(x, sh, [&](int, uint32_t k) { s += k > KEY_NEGINF ? exp((double)fkey_inv(k) - x.M) : 0.0; });
+  x.S = block_sum_f64(s, sh);
+  const double S = x.S;
+  const int64_t V = a.V;
+
+  if (!greedy) {
+    const double q0 = 1.0 / S;
+    int64_t m = V;
+    if (P.top_k > 0 && P.top_k < m) m = P.top_k;
+    if (P.min_p > 0.0) {
+      // smallest key whose q passes q >= min_p * q_0 (monotone in the key), then count the keys above it
+      const double thr = P.min_p * q0;
+      uint32_t lo = KEY_NEGINF + 1u, hi = mk;
+      while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (exp((double)fkey_inv(mid) - x.M) / S >= thr) hi = mid;
+        else lo = mid + 1;
+      }
+      const int64_t mm = (int64_t)count_ge(x, sh, lo);
+      if (mm < m) m = mm;
+    }
+    {
+      const Hit hp = query(x, sh, Q_EXCL, 0, P.top_p);
+      if (hp.rank >= 0 && hp.rank < m) m = hp.rank;
+    }
+    if (m < 1) m = 1;
+    const Hit hl = query(x, sh, Q_RANK, (uint64_t)(m - 1), 0.0);
+    const double clast = fx_val(fx_add(hl.above, hl.self)) / S;
+    int32_t tok = -1;
+    if (a.mode == MODE_SAMPLE) {
+      const double u = a.uni ? a.uni[row] : uniform64(P.seed, P.idx);
+      const double thr = u * clast;
+      Hit hj = query(x, sh, Q_INCL, 0, thr);
+      if (hj.rank < 0 || hj.rank > m - 1) hj = hl;  // j = min(count, keep.sum() - 1)
+      tok = (int32_t)pk_id(hj.pk);
+    }
+    if (tid == 0) {
+      RowInfo r = {};
+      r.cmax = best;
+      r.kkeep = hl.pk;
+      r.S = S;
+      r.Z = clast;
+      r.flags = R_DONE;
+      r.token = tok;
+      if (a.mode == MODE_SAMPLE) a.tokens[row] = tok;
+      *ri = r;
+    }
+  } else if (tid == 0) {
+    ri->flags = R_DONE | R_GREEDY;
+  }
+  if (nlp > 0) {
+    const int n_top = (int)min((int64_t)nlp, V);
+    const Hit hn = query(x, sh, Q_RANK, (uint64_t)(n_top - 1), 0.0);
+    const uint32_t n = collect_top(x, sh, hn.pk);
+    const double lS = log(S);
+    for (int i = tid; i < nlp; i += XT) {
+      int32_t id = -1;
+      float lp = __builtin_nanf("");
+      if (i < (int)n) {
+        const uint64_t pk = sh.u.col.k[i];
+        id = (int32_t)pk_id(pk);
+        const uint32_t k = pk_key(pk);
+        lp = k > KEY_NEGINF ? (float)(((double)fkey_inv(k) - x.M) - lS) : -INFINITY;
+      }
+      a.lp_ids[(int64_t)row * a.lp_ld + i] = id;
+      a.lps[(int64_t)row * a.lp_ld + i] = lp;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_exact(const ScanArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL(exact_kernel, dim3(a.rows), dim3(XT), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace gse

@@ -1,0 +1,181 @@
+/* gse.h: C ABI of libgse.so, the MI355X (gfx950) token-selection library.
+ *
+ * It replaces the host arithmetic under goethe-engine's sampling.py / spec.py / grammar.py call surface with HIP
+ * kernels. Python binds it with ctypes (goethe-engine_amd/_lib.py), in the conventions of the reference's own C ABI
+ * (abi/gc.h:1-22, bound by goethe_engine/gc_c.py:58-77):
+ *
+ *   Versioning  gse_abi_version() = MAJOR << 16 | MINOR. A minor only appends fields, flags and functions.
+ *   Structs     every in/out struct starts with `size`, the caller's sizeof; the library reads only fields inside
+ *               min(size, its own size) and treats absent fields as zero.
+ *   Handles     gse_open returns an independent instance (own device workspace). One handle is not thread safe; each
+ *               call takes the caller's HIP stream and is asynchronous on it.
+ *   Errors      functions return GSE_OK (0) or a negative GSE_E_* code; gse_last_error(h) returns the text of the last
+ *               error on that handle (gse_last_error(NULL): the last gse_open failure on this thread).
+ *   Memory      every data pointer below is a device pointer unless marked host. Inputs are borrowed, never written;
+ *               outputs are caller-owned buffers.
+ */
+#ifndef GSE_H
+#define GSE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GSE_ABI_MAJOR 1
+#define GSE_ABI_MINOR 0
+#define GSE_ABI_VERSION ((GSE_ABI_MAJOR << 16) | GSE_ABI_MINOR)
+
+#if defined(__GNUC__)
+#define GSE_API __attribute__((visibility("default")))
+#else
+#define GSE_API
+#endif
+
+typedef struct gse_handle gse_handle;
+
+enum {
+  GSE_OK = 0,
+  GSE_E_ARG = -1,         /* bad argument or struct size */
+  GSE_E_DEVICE = -4,      /* no such device, wrong architecture, out of device memory, HIP failure */
+  GSE_E_UNSUPPORTED = -5, /* a request this library version cannot run */
+  GSE_E_CAPACITY = -7     /* more rows / a larger vocabulary than the handle was opened for */
+};
+
+enum { GSE_F32 = 0, GSE_BF16 = 1 }; /* logits dtype */
+
+typedef struct gse_open_params {
+  uint32_t size;
+  int32_t device;     /* HIP device ordinal */
+  uint32_t max_rows;  /* rows per call */
+  uint32_t max_vocab; /* vocabulary size per row, <= 2^21 */
+} gse_open_params;
+
+/* One row's selection parameters (device array of gse_row, 72 bytes each). The reference's SamplingParams
+ * (goethe_engine/sampling.py:8-21) carries temperature, top_p, top_k; the other fields extend it with neutral
+ * defaults (repetition 1, frequency 0, presence 0, min_p 0, logprobs 0). */
+typedef struct gse_row {
+  float temperature;        /* float32(t) as sampling.py:61 divides by; 0 = greedy (sampling.py:76-78) */
+  int32_t top_k;            /* 0 = off (sampling.py:80 `top_k or V`) */
+  double top_p;             /* (0, 1], compared in fp64 as sampling.py:80 does */
+  double min_p;             /* [0, 1]; keep q_i >= min_p * q_0 */
+  float repetition_penalty; /* > 0; 1 = off */
+  float frequency_penalty;  /* finite; 0 = off */
+  float presence_penalty;   /* finite; 0 = off */
+  int32_t mask_row;         /* row of gse_batch.mask holding this row's packed bitmask, -1 = no mask */
+  uint64_t seed;            /* uniform(seed, idx) (sampling.py:42-51) unless gse_batch.uniforms is given */
+  uint64_t idx;
+  int32_t hist_begin;       /* this row's token history: gse_batch.hist[hist_begin, hist_end) */
+  int32_t hist_end;
+  int32_t logprobs;         /* N of the top-N logprobs to return, 0..GSE_MAX_LOGPROBS */
+  uint32_t flags;           /* GSE_ROW_* */
+} gse_row;
+
+/* gse_row.flags */
+enum {
+  GSE_ROW_TEMP_UNDERFLOW = 1u /* temperature > 0 whose float32 is 0: sampled, dividing by 0 as sampling.py:61 does */
+};
+
+#define GSE_MAX_LOGPROBS 64
+
+typedef struct gse_batch {
+  uint32_t size;
+  uint32_t dtype;          /* GSE_F32 or GSE_BF16 */
+  uint32_t rows;
+  uint32_t vocab;
+  int64_t ld;              /* logits row stride in elements */
+  const void *logits;      /* [rows][ld] (backend.py:37-42: one row per wanted token) */
+  const gse_row *params;   /* [rows] */
+  const int32_t *mask;     /* packed bitmask rows, token t = bit t % 32 of word t / 32 (grammar.py:42-45), or NULL */
+  int64_t mask_ld;         /* words per mask row, >= ceil(vocab / 32) */
+  const int32_t *hist;     /* token history ids for the penalties (ids outside [0, vocab) are ignored), or NULL */
+  const double *uniforms;  /* [rows] shared per-row draws in [0, 1), or NULL: splitmix64(seed, idx) */
+  void *stream;            /* hipStream_t; NULL = the null stream */
+  uint32_t flags;          /* GSE_BATCH_* */
+  uint32_t reserved;
+} gse_batch;
+
+/* gse_batch.flags */
+enum {
+  GSE_BATCH_EXACT = 1u,  /* finish every sampled row on the exact radix-select path (same results, slower) */
+  GSE_BATCH_PROFILE = 2u /* record HIP events around each kernel of this call on its stream (read with gse_profile) */
+};
+
+typedef struct gse_out {
+  uint32_t size;
+  uint32_t reserved;
+  int32_t *tokens;         /* [rows]: the sampled token, -1 for a row without a finite choice (sampling.py:84) */
+  float *processed;        /* optional [rows][processed_ld]: logits after penalties and mask, before temperature */
+  int64_t processed_ld;
+  int32_t *logprob_ids;    /* optional [rows][logprobs_ld]: top-N token ids, descending, ties to the lowest id */
+  float *logprobs;         /* optional [rows][logprobs_ld]: fp32 of fp64 log_softmax(z) at those ids */
+  int64_t logprobs_ld;
+} gse_out;
+
+/* Node batch for multi-step speculative sampling (SpecInfer VerifyStochastic, goethe_engine/spec.py:88-103). */
+typedef struct gse_mss_batch {
+  uint32_t size;
+  uint32_t nodes;          /* independent nodes */
+  uint32_t vocab;
+  uint32_t max_kids;
+  double *p;               /* [nodes][p_ld] target distributions (vocabulary order); used as scratch, overwritten */
+  int64_t p_ld;
+  const double *q;         /* draft distribution rows [*][q_ld], or NULL when every kid is one-hot */
+  int64_t q_ld;
+  const int32_t *kid_tok;  /* [nodes][max_kids] kid tokens in draft order, -1 pads */
+  const int32_t *kid_q;    /* [nodes][max_kids] row of q for the kid, -1 = one-hot (q None in spec.py:93) */
+  const uint64_t *seed;    /* [nodes] request seed */
+  const uint64_t *idx;     /* [nodes] uniform index (the engine's nout, engine.py:282) */
+  int32_t *out_token;      /* [nodes] */
+  int32_t *out_kid;        /* [nodes] index of the accepted kid, -1 when every kid was rejected */
+  void *stream;
+} gse_mss_batch;
+
+/* Replaces: nothing (version handshake, as gc_abi_version, abi/gc.h:82). */
+GSE_API uint32_t gse_abi_version(void);
+
+/* Replaces: the host-side state of sampling.py (none); allocates the device workspace for max_rows x max_vocab. */
+GSE_API int gse_open(const gse_open_params *p, gse_handle **out);
+
+/* Replaces: goethe_engine/sampling.py:68-85 sample() with the mask application of grammar.py:42-45 / engine.py:272-273
+ * fused in, plus penalties, min-p and top-N logprobs. One token per row; -1 for a NaN row or a row without a finite
+ * choice. Greedy rows (temperature 0) take the first argmax of nan_to_num; the others the inverse CDF of
+ * sampling.py:80-83 over the stable descending order. */
+GSE_API int gse_sample(gse_handle *h, const gse_batch *in, const gse_out *out);
+
+/* Replaces: goethe_engine/sampling.py:88-97 dist(): fp64 probabilities over the vocabulary (vocabulary order) that
+ * sample() draws a temperature > 0 row from, with top-k, top-p, min-p, penalties and mask; probs is [rows][probs_ld]. */
+GSE_API int gse_dist(gse_handle *h, const gse_batch *in, double *probs, int64_t probs_ld);
+
+/* Replaces: goethe_engine/sampling.py:100-104 draw(): inverse CDF in vocabulary order of each fp64 row q at u[r]:
+ * min(count(cumsum(q) < u * sum(q)), last index with q > 0). */
+GSE_API int gse_draw(gse_handle *h, const double *q, int64_t q_ld, uint32_t rows, uint32_t vocab, const double *u,
+                     int32_t *out, void *stream);
+
+/* Replaces: goethe_engine/spec.py:88-103 mss(), batched over independent nodes. */
+GSE_API int gse_mss(gse_handle *h, const gse_mss_batch *in);
+
+/* Replaces: the bool unpack of grammar.py:44-45 in reverse: bool rows [rows][bool_ld] (1 byte per token) -> packed
+ * int32 words [rows][words_ld], so Matcher.mask() tensors can feed gse_batch.mask. */
+GSE_API int gse_pack_mask(gse_handle *h, const uint8_t *bools, int64_t bool_ld, uint32_t rows, uint32_t vocab,
+                          int32_t *words, int64_t words_ld, void *stream);
+
+/* Replaces: nothing (measurement; the reference has no profiler). Calls made with GSE_BATCH_PROFILE record HIP events
+ * around each of their kernels on their stream (no synchronisation), for up to GSE_PROFILE_CALLS calls. gse_profile
+ * waits for the last recorded event, writes into ms[i] the total milliseconds of kernel i (launch order: scan, exact[,
+ * dist]) over the recorded calls and into *calls their number, then clears the record. Returns the number of kernels
+ * per call (<= n are written) or a negative GSE_E_* code. */
+#define GSE_PROFILE_CALLS 512
+GSE_API int gse_profile(gse_handle *h, float *ms, uint32_t n, uint32_t *calls);
+
+/* Replaces: gc_last_error (abi/gc.h, goethe_engine/gc_c.py:222-227 turns it into RuntimeError). */
+GSE_API const char *gse_last_error(gse_handle *h);
+
+GSE_API void gse_close(gse_handle *h);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GSE_H */

@@ -1,0 +1,171 @@
+"""GPU parity: the HIP path (through the C ABI) against the reference's golden vectors and the oracle, on seeded inputs
+of every workload at sizes the oracle finishes in seconds. Token ids are compared bit-exact, probabilities and logprobs
+within the stated tolerances, processed logits bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampling_ref as ora
+from oracle import spec_ref as spo
+
+pytestmark = pytest.mark.gpu
+
+DIST_RTOL = 1e-12      # fp64 probabilities: GPU exp vs numpy exp, tree vs pairwise sums
+LOGPROB_RTOL = 1e-5    # fp32 logprobs (the stated 1e-5 relative bar)
+
+
+def _P(ge, **kw):
+    return ge.sampling.SamplingParams(**kw)
+
+
+def both_paths(ge, x, params, seeds, idxs, masks, history=None, uniforms=None):
+    fast = ge.sampling.sample(x, params, seeds, idxs, masks, history=history, uniforms=uniforms)
+    exact = ge.sampling.sample(x, params, seeds, idxs, masks, history=history, uniforms=uniforms, exact=True)
+    return fast, exact
+
+
+def test_golden_tiny(ge, gpu, golden):
+    x = torch.from_numpy(golden["tiny_x"]).to(gpu)
+    for (t, k, p), want in zip(golden["tiny_params"], golden["tiny_tok"]):
+        params = [_P(ge, temperature=float(t), top_k=int(k), top_p=float(p))] * 64
+        xs = x.expand(64, -1).contiguous()
+        f, e = both_paths(ge, xs, params, list(range(64)), [0] * 64, None)
+        assert f == list(want) and e == list(want), (t, k, p)
+
+
+@pytest.mark.parametrize("prefix", ["rows", "edge"])
+def test_golden_rows(ge, gpu, golden, prefix):
+    g = golden
+    n = len(g[prefix + "_T"])
+    params = [_P(ge, temperature=float(t), top_k=int(k), top_p=float(p))
+              for t, k, p in zip(g[prefix + "_T"], g[prefix + "_K"], g[prefix + "_TP"])]
+    masks = [torch.from_numpy(g[prefix + "_mask"][r]) if g[prefix + "_has_mask"][r] else None for r in range(n)]
+    x = torch.from_numpy(g[prefix + "_x"]).to(gpu)
+    toks = g[prefix + "_tok"]
+    for j in range(toks.shape[1]):
+        if prefix == "rows":
+            seeds, idxs = [int(s) for s in g["rows_seed"][:, j]], [int(i) for i in g["rows_idx"][:, j]]
+        else:
+            seeds, idxs = [int(g["edge_seed"][j])] * n, [j] * n
+        f, e = both_paths(ge, x, params, seeds, idxs, masks)
+        assert f == list(toks[:, j]), (prefix, j)
+        assert e == list(toks[:, j]), (prefix, j, "exact")
+
+
+def test_golden_dist_draw_mss(ge, gpu, golden):
+    g = golden
+    for r, (t, k, p) in enumerate(g["dist_params"]):
+        m = torch.from_numpy(g["dist_mask"][r]) if g["dist_has_mask"][r] else None
+        d = ge.sampling.dist(torch.from_numpy(g["dist_x"][r]).to(gpu), _P(ge, temperature=float(t), top_k=int(k),
+                                                                           top_p=float(p)), m)
+        np.testing.assert_allclose(d.cpu().numpy(), g["dist_out"][r], rtol=DIST_RTOL, atol=1e-300)
+    for r in range(g["draw_q"].shape[0]):
+        q = torch.from_numpy(g["draw_q"][r]).to(gpu)
+        assert [ge.sampling.draw(q, float(u)) for u in g["draw_u"][r]] == list(g["draw_out"][r])
+    kids = [[(int(t), g["mss_q"][n, k] if g["mss_has_q"][n, k] else None) for k, t in enumerate(g["mss_tok"][n])
+             if t >= 0] for n in range(g["mss_p"].shape[0])]
+    toks, ks = ge.spec.mss_batch(g["mss_p"], kids, [int(s) for s in g["mss_seed"]], [int(i) for i in g["mss_i"]])
+    assert toks == list(g["mss_out_tok"])
+    assert [-1 if k is None else k for k in ks] == list(g["mss_out_kid"])
+
+
+def _run(ge, batch, gpu, exact=False, processed=False):
+    x = torch.from_numpy(batch.logits).to(gpu)
+    if batch.bf16:
+        x = x.view(torch.bfloat16)
+    masks = None if batch.masks is None else [torch.from_numpy(m) for m in batch.masks]
+    return ge.sampling.sample_ex(x, batch.params, None, None, masks, history=batch.history, uniforms=batch.uniforms,
+                                 exact=exact, processed=processed)
+
+
+def _oracle(batch):
+    masks = None if batch.masks is None else [ora.unpack_mask(m, batch.vocab) for m in batch.masks]
+    return ora.sample_full(batch.logits_f32(), batch.params, None, None, masks, batch.history, batch.uniforms)
+
+
+def _check(ge, batch, gpu, check_processed=True):
+    want = _oracle(batch)
+    for exact in (False, True):
+        sel = _run(ge, batch, gpu, exact=exact, processed=check_processed)
+        toks = sel.tolist()
+        assert toks == [w["token"] for w in want], (batch.name, exact)
+        if check_processed and not exact:
+            proc = sel.processed.cpu().numpy()
+            for r, w in enumerate(want):
+                assert np.array_equal(proc[r].view(np.uint32), w["processed"].view(np.uint32)), (batch.name, r)
+        if sel.logprobs is not None:
+            ids, lps = sel.logprob_ids.cpu().numpy(), sel.logprobs.cpu().numpy()
+            for r, w in enumerate(want):
+                n = len(w["logprob_ids"])
+                assert list(ids[r, :n]) == list(w["logprob_ids"]), (batch.name, r)
+                np.testing.assert_allclose(lps[r, :n], w["logprobs"], rtol=LOGPROB_RTOL)
+    return want
+
+
+def test_c1_cpu_sampler_workload(ge, gpu):
+    _check(ge, ge.workloads.c1(), gpu)
+
+
+def test_c2_masked_greedy(ge, gpu):
+    b = ge.workloads.c2()
+    want = _check(ge, b, gpu, check_processed=False)
+    assert all(t >= 0 for t in (w["token"] for w in want))
+
+
+@pytest.mark.parametrize("rows", [list(range(0, 16)), list(range(100, 116)), list(range(240, 256))])
+def test_c3_full_stack_rows(ge, gpu, rows):
+    _check(ge, ge.workloads.c3(rows=rows), gpu)
+
+
+def test_c5_bf16_nucleus_logprobs(ge, gpu):
+    _check(ge, ge.workloads.c5(rows=list(range(8))), gpu, check_processed=False)
+
+
+def test_c4_tree_verify(ge, gpu):
+    reqs = ge.workloads.c4(requests=range(4), v=128256)
+    qrows = []
+    for r in reqs:
+        q = {}
+        for u in range(9):
+            if r["draft"][u].any():
+                z = r["draft"][u].astype(np.float64)
+                e = np.exp(z - z.max())
+                q[u] = e / e.sum()
+        qrows.append(q)
+    got = ge.spec.verify_tree([dict(target=r["target"], q=q, tokens=r["tokens"], parents=r["parents"],
+                                    params=r["params"], seed=r["seed"]) for r, q in zip(reqs, qrows)])
+    for (out, path), r, q in zip(got, reqs, qrows):
+        want = spo.verify_tree(r["target"], q, r["tokens"], r["parents"], r["params"], r["seed"])
+        assert (out, path) == want
+
+
+@pytest.mark.parametrize("v", [1, 7, 33, 8191, 8193, 20000])
+def test_odd_vocab_sizes_and_strides(ge, gpu, v):
+    rng = np.random.default_rng(v)
+    n = 12
+    x = (rng.normal(0, 2, size=(n, v + 5)) ).astype(np.float32)
+    x[3, : min(v, 4)] = 1.0   # ties
+    P = ge.sampling.SamplingParams
+    params = [P(), P(temperature=0.9), P(temperature=1.0, top_k=3), P(temperature=1.4, top_p=0.7),
+              P(temperature=0.6, min_p=0.1), P(temperature=1.0, repetition_penalty=1.3, frequency_penalty=0.4)] * 2
+    hist = [rng.integers(0, v, size=9) for _ in range(n)]
+    m = rng.random(v) < 0.5
+    m[0] = True
+    masks = [m if r % 4 == 1 else None for r in range(n)]
+    seeds, idxs = list(range(n)), [5] * n
+    xt = torch.from_numpy(x).to(gpu)[:, 2:2 + v]          # row stride v + 5, misaligned start
+    want = ora.sample(x[:, 2:2 + v], params, seeds, idxs, masks, history=hist)
+    f, e = both_paths(ge, xt, params, seeds, idxs, masks, history=hist)
+    assert f == want and e == want
+
+
+def test_determinism_and_batch_invariance_full_c3(ge, gpu):
+    b = ge.workloads.c3()
+    a1 = _run(ge, b, gpu).tolist()
+    a2 = _run(ge, b, gpu).tolist()
+    ax = _run(ge, b, gpu, exact=True).tolist()
+    assert a1 == a2 == ax
+    perm = np.random.default_rng(0).permutation(b.rows)
+    pb = ge.workloads.Batch(b.name, b.logits[perm], [b.params[i] for i in perm], b.uniforms[perm], b.masks[perm],
+                            [b.history[i] for i in perm])
+    assert _run(ge, pb, gpu).tolist() == [a1[i] for i in perm]

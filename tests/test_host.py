@@ -1,0 +1,84 @@
+"""Host logic of the drop-in modules, without a GPU: parameter validation (sampling.py:23-39 plus the extensions),
+the host integer helpers, the per-row record packing, mask packing, the synthetic workloads, and that the product path
+refuses to run (no CPU fallback) when there is no HIP device."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampling_ref as ora
+
+
+def test_validate(ge):
+    P = ge.sampling.SamplingParams
+    for bad in (P(temperature=-1), P(top_p=0), P(top_k=-1), P(max_tokens=0), P(n=2), P(stop_sequences=((),)),
+                P(accept="x"), P(repetition_penalty=0.0), P(frequency_penalty=float("inf")), P(min_p=1.5),
+                P(min_p=-0.1), P(logprobs=65)):
+        with pytest.raises(ValueError):
+            bad.validate()
+    P(temperature=0.7, top_k=5, top_p=0.9, min_p=0.05, repetition_penalty=1.2, frequency_penalty=-0.5,
+      presence_penalty=0.3, logprobs=20).validate()
+
+
+def test_mix_uniform_equal_the_oracle(ge):
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        s, i = int(rng.integers(0, 2 ** 63)), int(rng.integers(0, 2 ** 40))
+        assert ge.sampling.mix(s, i) == ora.mix(s, i)
+        assert ge.sampling.uniform(s, i) == ora.uniform(s, i)
+    idx = np.arange(100, dtype=np.uint64)
+    assert (ge.workloads.mix_array(12345, idx) == ora.mix_np(12345, idx)).all()
+    assert np.array_equal(ge.workloads.uniforms(3, idx), ora.uniform_np(3, idx))
+
+
+def test_row_records(ge):
+    P = ge.sampling.SamplingParams
+    ps = [P(), P(temperature=1e-50, top_k=7, top_p=0.9, min_p=0.05, repetition_penalty=1.1, logprobs=3),
+          P(temperature=0.8, top_k=10 ** 12)]
+    r = ge.sampling._rows(ps, [1, 2 ** 64 + 5, None], [0, 9, 3], np.array([0, 2, 2, 5]))
+    assert r["temperature"].tolist() == [0.0, 0.0, np.float32(0.8)]
+    assert r["flags"].tolist() == [0, ge._lib.ROW_TEMP_UNDERFLOW, 0]   # positive t whose float32 is 0 is sampled
+    assert r["top_k"].tolist() == [0, 7, 0x7FFFFFFF]
+    assert r["seed"].tolist() == [1, 5, 0] and r["idx"].tolist() == [0, 9, 3]
+    assert r["hist_begin"].tolist() == [0, 2, 2] and r["hist_end"].tolist() == [2, 2, 5]
+    assert r["repetition_penalty"][1] == np.float32(1.1) and r["logprobs"].tolist() == [0, 3, 0]
+
+
+def test_grammar_pack_unpack(ge):
+    rng = np.random.default_rng(1)
+    for v in (1, 31, 32, 33, 1000, 4097):
+        m = rng.random(v) < 0.3
+        w = ge.grammar.pack(m)
+        assert w.shape == ((v + 31) // 32,)
+        assert (ge.grammar.unpack(w, v).numpy() == m).all()
+        assert (ora.unpack_mask(w.numpy(), v) == m).all()
+        assert (w.numpy() == ora.pack_mask(m)).all()
+        assert (ge.workloads.pack_bits(m[None])[0] == ora.pack_mask(m)).all()
+
+
+def test_workloads_are_seeded_and_row_independent(ge):
+    a = ge.workloads.c1()
+    b = ge.workloads.c1(rows=[3, 5])
+    assert a.logits.shape == (8, 32000) and a.logits.dtype == np.float32
+    assert np.array_equal(a.logits[[3, 5]], b.logits) and np.array_equal(a.uniforms[[3, 5]], b.uniforms)
+    assert abs(float(a.logits.std()) - 2.0) < 0.02
+    c = ge.workloads.c3(rows=[0, 1])
+    assert c.masks.shape == (2, 4748) and c.logits.shape == (2, 151936) and len(c.history[0]) == 2048
+    allowed = ora.unpack_mask(c.masks[0], 151936)
+    assert 0.02 < allowed.mean() < 0.08 and ora.unpack_mask(c.masks[1], 151936).all()
+    assert abs(float(c.logits[0].mean())) < 1e-3
+    p = c.params[0]
+    assert 0.5 <= p.temperature <= 1.5 and p.top_k in (0, 20, 50, 200) and 0.8 <= p.top_p <= 1.0
+    e = ge.workloads.c5(rows=[0])
+    assert e.logits.dtype == np.uint16 and e.bf16
+    f = ge.workloads.bf16_bits_to_f32(e.logits)
+    assert np.isfinite(f).all() and abs(float(np.median(f)) - 1.5 * -np.log(np.log(2.0))) < 0.02   # Gumbel median
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the behaviour without a HIP device")
+def test_product_path_refuses_without_a_gpu(ge):
+    P = ge.sampling.SamplingParams
+    x = np.zeros((1, 10), np.float32)
+    with pytest.raises(RuntimeError):
+        ge.sampling.sample(x, [P()], [0], [0], [None])
+    with pytest.raises(RuntimeError):
+        ge.sampling.draw(np.ones(4) / 4, 0.5)
