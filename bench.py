@@ -58,6 +58,9 @@ def main():
     ap.add_argument("--copies", type=int, default=0, help="input copies to rotate over (0: enough to exceed the MALL)")
     ap.add_argument("--cpu-passes", type=int, default=2, help="passes of the CPU oracle over the sample rows")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="before the steps, copy a MIB-MiB device buffer 5 times (a plain copy kernel of known size, "
+                         "the reference point for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -74,6 +77,16 @@ def main():
         raise RuntimeError("bench.py needs a HIP device")
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration: 5 device copies of {n} bytes ({args.calibrate_copy} MiB)")
+        del src, dst
 
     t0 = time.perf_counter()
     batch = getattr(ge.workloads, args.config)()
