@@ -12,7 +12,7 @@
 struct gse_handle {
   int device = 0;
   uint32_t max_rows = 0, max_vocab = 0, nchmax = 0;
-  gse::ChunkHdr *hdr = nullptr;
+  gse::SliceRec *rec = nullptr;
   uint64_t *cand = nullptr;
   gse::RowInfo *info = nullptr;
   uint32_t *done = nullptr;
@@ -106,15 +106,15 @@ gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   a.V = (int)b.vocab;
   a.rows = (int)b.rows;
   a.nch = (int)((b.vocab + gse::CH - 1) / gse::CH);
-  a.nchmax = (int)h->nchmax;
   a.mode = mode;
+  a.xcd_map = 1;
   a.force_exact = (b.flags & GSE_BATCH_EXACT) ? 1 : 0;
   a.params = b.params;
   a.mask = b.mask;
   a.mask_ld = b.mask_ld;
   a.hist = b.hist;
   a.uni = b.uniforms;
-  a.hdr = h->hdr;
+  a.rec = h->rec;
   a.cand = h->cand;
   a.info = h->info;
   a.done = h->done;
@@ -150,7 +150,7 @@ GSE_API int gse_open(const gse_open_params *p, gse_handle **out) {
   h->max_vocab = o.max_vocab;
   h->nchmax = (o.max_vocab + gse::CH - 1) / gse::CH;
   const size_t nrc = (size_t)h->max_rows * h->nchmax;
-  if ((e = hipMalloc(&h->hdr, nrc * sizeof(gse::ChunkHdr))) != hipSuccess ||
+  if ((e = hipMalloc(&h->rec, nrc * sizeof(gse::SliceRec))) != hipSuccess ||
       (e = hipMalloc(&h->cand, nrc * gse::CAPC * sizeof(uint64_t))) != hipSuccess ||
       (e = hipMalloc(&h->info, (size_t)h->max_rows * sizeof(gse::RowInfo))) != hipSuccess ||
       (e = hipMalloc(&h->done, (size_t)h->max_rows * sizeof(uint32_t))) != hipSuccess ||
@@ -192,7 +192,7 @@ GSE_API int gse_sample(gse_handle *h, const gse_batch *in, const gse_out *out) {
   if ((b.flags & GSE_BATCH_PROFILE) && (rc = prof_slot(h, 2, &ev)) != GSE_OK) return rc;
   hipError_t e;
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(h, e, "event record");
-  if ((e = gse::launch_scan(a, s)) != hipSuccess) return hip_fail(h, e, "scan launch");
+  if ((e = gse::launch_main(a, s)) != hipSuccess) return hip_fail(h, e, "main launch");
   if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return hip_fail(h, e, "event record");
   if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
   if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return hip_fail(h, e, "event record");
@@ -214,7 +214,7 @@ GSE_API int gse_dist(gse_handle *h, const gse_batch *in, double *probs, int64_t 
   if ((b.flags & GSE_BATCH_PROFILE) && (rc = prof_slot(h, 3, &ev)) != GSE_OK) return rc;
   hipError_t e;
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(h, e, "event record");
-  if ((e = gse::launch_scan(a, s)) != hipSuccess) return hip_fail(h, e, "scan launch");
+  if ((e = gse::launch_main(a, s)) != hipSuccess) return hip_fail(h, e, "main launch");
   if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return hip_fail(h, e, "event record");
   if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
   if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return hip_fail(h, e, "event record");
@@ -288,7 +288,7 @@ GSE_API void gse_close(gse_handle *h) {
   {
     DeviceGuard g(h->device);
     (void)hipDeviceSynchronize();
-    if (h->hdr) (void)hipFree(h->hdr);
+    if (h->rec) (void)hipFree(h->rec);
     if (h->cand) (void)hipFree(h->cand);
     if (h->info) (void)hipFree(h->info);
     if (h->done) (void)hipFree(h->done);

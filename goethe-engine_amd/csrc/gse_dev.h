@@ -8,9 +8,7 @@
 namespace gse {
 
 constexpr int WAVE = 64;
-constexpr int CH = 8192;           // tokens per chunk (one scan workgroup)
-constexpr int SCAN_THREADS = 256;  // 4 waves
-constexpr int EPT = CH / SCAN_THREADS;  // 32 tokens per thread, kept in registers as keys
+constexpr int CH = 8192;  // tokens per slice (one main-pass workgroup; the exact path walks rows in the same chunks)
 
 // Order-preserving 32-bit keys of fp32 values: larger value -> larger key; -0 and +0 share a key (numpy's stable
 // argsort sees them as equal); NaN -> 0, below every other key (numpy sorts NaN of -z last).
@@ -71,14 +69,21 @@ __device__ __forceinline__ float penalize(float x, uint32_t c, float rp, float f
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 
-// Reads that bypass the non-coherent per-CU caches: data another workgroup of the same launch wrote.
+// Data one workgroup hands to another workgroup of the same launch goes through agent-scope relaxed atomic stores and
+// loads (global_store / global_load with sc1 on gfx950: coherent across the XCDs' L2s), so no L2 writeback or
+// invalidate (what __threadfence() emits) is needed. The writer waits for its stores to complete (store_wait) before
+// the atomic ticket that publishes them; the reader issues its loads after it has seen the ticket.
 template <typename T>
-__device__ __forceinline__ T ld_acq(const T *p) {
+__device__ __forceinline__ T ld_ag(const T *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 template <typename T>
-__device__ __forceinline__ void st_rel(T *p, T v) {
+__device__ __forceinline__ void st_ag(T *p, T v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_wait() { __builtin_amdgcn_s_waitcnt(0); }
+__device__ __forceinline__ uint32_t ticket_add(uint32_t *p) {
+  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (WAVE - 1)); }
@@ -160,6 +165,37 @@ __device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) {
 }
 
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
+
+// The k-th largest (1-based) of the wave's 64 values: the largest r with at least k values >= r, bit by bit.
+__device__ __forceinline__ uint32_t wave_kth_largest_u32(uint32_t v, int k) {
+  uint32_t r = 0;
+#pragma unroll
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t c = r | (1u << b);
+    if (__popcll(ballot64(v >= c)) >= (uint64_t)k) r = c;
+  }
+  return r;
+}
+
+// The same over 16-bit values (v < 2^16).
+__device__ __forceinline__ uint32_t wave_kth_largest_u16(uint32_t v, int k) {
+  uint32_t r = 0;
+#pragma unroll
+  for (int b = 15; b >= 0; --b) {
+    const uint32_t c = r | (1u << b);
+    if (__popcll(ballot64(v >= c)) >= (uint64_t)k) r = c;
+  }
+  return r;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+  for (int m = 32; m; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, WAVE));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  for (int m = 32; m; m >>= 1) v = min(v, shfl_xor_u32(v, m));
+  return v;
+}
 __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }

@@ -502,6 +502,50 @@ __global__ __launch_bounds__(XT) void exact_kernel(ScanArgs a) {
     x.c.divide = false;
   }
   const int nlp = a.lp_ids ? min(min(P.logprobs, GSE_MAX_LOGPROBS), (int)a.lp_ld) : 0;
+  if (ri->flags & R_FULL) {
+    // the main pass could not count the history: recompute the row flags and, for a greedy row, the argmax
+    // (first maximum of nan_to_num of the masked logits, sampling.py:70-76)
+    RowCtx gc = make_ctx(a, row, P);
+    bool fnan = false, ffin = false;
+    uint64_t gb = 0;
+    for (int ch = 0; ch < x.nch; ++ch) {
+      const int c0 = ch * CH;
+      if (gc.pen) build_counts(gc, x.hist, c0, sh.cnt);
+      const int t0 = c0 + tid * PER;
+      const uint32_t mword = gc.mw ? (t0 < gc.V ? gc.mw[t0 >> 5] : 0u) : 0xFFFFFFFFu;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int t = t0 + i;
+        if (t < gc.V) {
+          float xm;
+          const uint32_t k = elem_key(gc, load_one(gc, t), gc.pen ? sh.cnt[t - c0] : 0u, (mword >> (t & 31)) & 1u, fnan,
+                                      ffin, xm);
+          const uint64_t p = pack(k, (uint32_t)t);
+          gb = p > gb ? p : gb;
+        }
+      }
+      if (gc.pen) __syncthreads();
+    }
+    gb = block_max_u64(gb, sh);
+    const bool anynan = block_sum_u64(fnan ? 1u : 0u, sh) != 0;
+    const bool anyfin = block_sum_u64(ffin ? 1u : 0u, sh) != 0;
+    const bool bad = anynan || !anyfin;
+    if (a.mode == MODE_SAMPLE && (bad || greedy)) {
+      const int32_t tok = bad ? -1 : (int32_t)pk_id(gb);
+      if (tid == 0) a.tokens[row] = tok;
+      if (bad || !nlp) {
+        for (int i = tid; i < nlp; i += XT) {
+          a.lp_ids[(int64_t)row * a.lp_ld + i] = -1;
+          a.lps[(int64_t)row * a.lp_ld + i] = __builtin_nanf("");
+        }
+        if (tid == 0) ri->flags = R_DONE | (bad ? R_BAD : 0u) | (greedy ? R_GREEDY : 0u);
+        return;
+      }
+    } else if (anynan) {  // dist of a NaN row is NaN everywhere
+      if (tid == 0) ri->flags = R_DONE | R_SPECIAL;
+      return;
+    }
+  }
   // pass 0: the row maximum of z
   uint64_t best = 0;
   for_each_key(x, sh, [&](int t, uint32_t k) {

@@ -12,35 +12,34 @@ static_assert(sizeof(gse_row) == 72, "gse_row layout is part of the ABI");
 enum : uint32_t {
   F_NAN = 1u,       // a NaN in the row after penalties (before the mask): the row is bad (sampling.py:71)
   F_FINITE = 2u,    // a finite value after the mask (sampling.py:75)
-  F_OVERFLOW = 4u,  // a chunk's candidate list did not fit
+  F_OVERFLOW = 4u,  // a slice's candidate list did not fit, or a history longer than the u16 counts allow
 };
 
 enum : uint32_t {
   R_GREEDY = 1u,   // temperature 0 in sample mode
   R_BAD = 2u,      // token -1
   R_SPECIAL = 4u,  // processed z holds +inf, or its maximum is -inf / NaN: token = order[0], dist = NaN
-  R_HARD = 8u,     // the exact radix-select path must finish the row
+  R_HARD = 8u,     // the exact path must finish the row
   R_DONE = 16u,
+  R_FULL = 32u,    // with R_HARD: the exact path also recomputes the flags and the greedy argmax
 };
 
 enum { MODE_SAMPLE = 0, MODE_DIST = 1 };
 
-constexpr int CAPC = 256;  // candidates per chunk record
-constexpr int CAPW = 128;  // candidates per wave during the scan
-constexpr int KW = 16;     // lane maxima per wave that bound the certified threshold
-constexpr int CERT_CAP = 4096;
+constexpr int CAPC = 512;  // candidates per slice record
 
-struct ChunkHdr {   // 64 bytes, one per (row, chunk)
-  uint64_t cmax;    // packed (key, id) maximum: greedy key in greedy rows, z key otherwise
-  uint32_t tau;     // every element of the chunk with key >= tau is in its candidate list
-  uint32_t ncand;
-  uint32_t flags;
-  uint32_t mkey;    // chunk maximum z key
-  double sc;        // sum over the chunk of exp(z - z_max_chunk), v_exp_f32 based
-  double mom;       // sum of exp(z - z_max_chunk) * |z - z_max_chunk| (error bound of sc)
+// One per (row, slice), written by the slice's workgroup with agent-scope stores, read by the row's resolve.
+struct SliceRec {   // 64 bytes
+  uint64_t top;     // packed (key, lowest id) of the slice maximum: z for sampled rows, nan_to_num(x) for greedy rows
+  uint32_t kappa;   // certified key: every element of the slice with key >= kappa is in the candidate list
+  uint32_t ncand;   // candidates listed (<= CAPC)
+  uint32_t flags;   // F_*
+  uint32_t mkey;    // key of the slice maximum of z (z = x for greedy rows)
+  double s;         // sum over the slice's unlisted elements of exp(z - z_slice_max), fp32 exp2 terms
+  double bnd;       // absolute error bound of s
   uint32_t pad[6];
 };
-static_assert(sizeof(ChunkHdr) == 64, "");
+static_assert(sizeof(SliceRec) == 64, "");
 
 struct RowInfo {    // 64 bytes, one per row, written by the row resolve, read by the exact path and dist
   uint64_t cmax;    // packed maximum z (key, id)
@@ -57,7 +56,7 @@ static_assert(sizeof(RowInfo) == 64, "");
 struct ScanArgs {
   const void *logits;
   int64_t ld;
-  int dtype, V, rows, nch, nchmax, mode, force_exact, pad;
+  int dtype, V, rows, nch, mode, force_exact, xcd_map, pad;
   const gse_row *params;
   const int32_t *mask;
   int64_t mask_ld;
@@ -69,13 +68,13 @@ struct ScanArgs {
   int32_t *lp_ids;
   float *lps;
   int64_t lp_ld;
-  ChunkHdr *hdr;
-  uint64_t *cand;
+  SliceRec *rec;    // [rows][nch]
+  uint64_t *cand;   // [rows][nch][CAPC]
   RowInfo *info;
-  uint32_t *done;
+  uint32_t *done;   // [rows] slice tickets, zero between calls
 };
 
-hipError_t launch_scan(const ScanArgs &a, hipStream_t s);
+hipError_t launch_main(const ScanArgs &a, hipStream_t s);
 hipError_t launch_exact(const ScanArgs &a, hipStream_t s);
 hipError_t launch_dist_write(const ScanArgs &a, double *probs, int64_t probs_ld, hipStream_t s);
 hipError_t launch_draw(const double *q, int64_t ld, int rows, int V, const double *u, int32_t *out, hipStream_t s);
