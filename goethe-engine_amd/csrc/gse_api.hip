@@ -12,6 +12,8 @@
 struct gse_handle {
   int device = 0;
   uint32_t max_rows = 0, max_vocab = 0, nchmax = 0;
+  uint32_t nrec = 0;     // part records (and wave lists) in the workspace
+  uint32_t target = 0;   // main-pass workgroups to aim for (4 per CU: all resident at once)
   gse::SliceRec *rec = nullptr;
   uint64_t *cand = nullptr;
   gse::RowInfo *info = nullptr;
@@ -98,6 +100,20 @@ int check_batch(gse_handle *h, const gse_batch &b) {
   return GSE_OK;
 }
 
+// Parts per row for the main pass: each at most PTOK tokens, a multiple of PCHUNK long, and enough of them over the
+// batch to give every CU about four workgroups. rows * parts <= rows * (ceil(vocab / PTOK) + 1) + target.
+void parts(const gse_handle *h, uint32_t rows, uint32_t vocab, int *nparts, int *plen) {
+  const uint32_t nck = (vocab + gse::PCHUNK - 1) / gse::PCHUNK;
+  uint32_t np = (vocab + gse::PTOK - 1) / gse::PTOK;
+  const uint32_t want = (h->target + rows - 1) / rows;
+  if (want > np) np = want;
+  if (np > (uint32_t)gse::MAXP) np = gse::MAXP;
+  if (np > nck) np = nck;
+  const uint32_t len = ((vocab + np - 1) / np + gse::PCHUNK - 1) / gse::PCHUNK * gse::PCHUNK;
+  *plen = (int)len;
+  *nparts = (int)((vocab + len - 1) / len);
+}
+
 gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   gse::ScanArgs a = {};
   a.logits = b.logits;
@@ -106,6 +122,7 @@ gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   a.V = (int)b.vocab;
   a.rows = (int)b.rows;
   a.nch = (int)((b.vocab + gse::CH - 1) / gse::CH);
+  parts(h, b.rows, b.vocab, &a.nparts, &a.plen);
   a.mode = mode;
   a.xcd_map = 1;
   a.force_exact = (b.flags & GSE_BATCH_EXACT) ? 1 : 0;
@@ -149,15 +166,16 @@ GSE_API int gse_open(const gse_open_params *p, gse_handle **out) {
   h->max_rows = o.max_rows;
   h->max_vocab = o.max_vocab;
   h->nchmax = (o.max_vocab + gse::CH - 1) / gse::CH;
-  const size_t nrc = (size_t)h->max_rows * h->nchmax;
-  if ((e = hipMalloc(&h->rec, nrc * sizeof(gse::SliceRec))) != hipSuccess ||
-      (e = hipMalloc(&h->cand, nrc * gse::CAPC * sizeof(uint64_t))) != hipSuccess ||
+  h->target = 4u * (uint32_t)(prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256);
+  h->nrec = h->max_rows * ((o.max_vocab + gse::PTOK - 1) / gse::PTOK + 1) + h->target;
+  if ((e = hipMalloc(&h->rec, (size_t)h->nrec * sizeof(gse::SliceRec))) != hipSuccess ||
+      (e = hipMalloc(&h->cand, (size_t)h->nrec * gse::PWAVES * gse::CAPW * sizeof(uint64_t))) != hipSuccess ||
       (e = hipMalloc(&h->info, (size_t)h->max_rows * sizeof(gse::RowInfo))) != hipSuccess ||
       (e = hipMalloc(&h->done, (size_t)h->max_rows * sizeof(uint32_t))) != hipSuccess ||
       (e = hipMemset(h->done, 0, (size_t)h->max_rows * sizeof(uint32_t))) != hipSuccess ||
       (e = hipMemset(h->info, 0, (size_t)h->max_rows * sizeof(gse::RowInfo))) != hipSuccess ||
       (e = hipDeviceSynchronize()) != hipSuccess) {
-    fail(nullptr, GSE_E_DEVICE, "workspace allocation (%zu rows x chunks): %s", nrc, hipGetErrorString(e));
+    fail(nullptr, GSE_E_DEVICE, "workspace allocation (%u part records): %s", h->nrec, hipGetErrorString(e));
     gse_close(h);
     return GSE_E_DEVICE;
   }

@@ -559,7 +559,12 @@ __global__ __launch_bounds__(XT) void exact_kernel(ScanArgs a) {
       a.lp_ids[(int64_t)row * a.lp_ld + i] = -1;
       a.lps[(int64_t)row * a.lp_ld + i] = __builtin_nanf("");
     }
-    if (tid == 0) ri->flags = R_DONE | R_SPECIAL | (greedy ? R_GREEDY : 0u);
+    if (tid == 0) {
+      // z holds +inf or its maximum is -inf: token = order[0], the lowest id at the maximum key (sampling.py:82)
+      ri->cmax = best;
+      ri->flags = R_DONE | R_SPECIAL | (greedy ? R_GREEDY : 0u);
+      if (a.mode == MODE_SAMPLE && !greedy) a.tokens[row] = (int32_t)pk_id(best);
+    }
     return;
   }
   x.M = (double)fkey_inv(mk);

@@ -26,18 +26,24 @@ enum : uint32_t {
 
 enum { MODE_SAMPLE = 0, MODE_DIST = 1 };
 
-constexpr int CAPC = 512;  // candidates per slice record
+constexpr int CAPW = 512;   // candidates listed per wave per part
+constexpr int PWAVES = 4;   // waves per part workgroup
+constexpr int MAXP = 64;    // parts per row
+constexpr int PTOK = 40960; // tokens per part, at most
+constexpr int PCHUNK = 1024;  // part lengths are multiples of this (one wave chunk)
 
-// One per (row, slice), written by the slice's workgroup with agent-scope stores, read by the row's resolve.
-struct SliceRec {   // 64 bytes
-  uint64_t top;     // packed (key, lowest id) of the slice maximum: z for sampled rows, nan_to_num(x) for greedy rows
-  uint32_t kappa;   // certified key: every element of the slice with key >= kappa is in the candidate list
-  uint32_t ncand;   // candidates listed (<= CAPC)
-  uint32_t flags;   // F_*
-  uint32_t mkey;    // key of the slice maximum of z (z = x for greedy rows)
-  double s;         // sum over the slice's unlisted elements of exp(z - z_slice_max), fp32 exp2 terms
-  double bnd;       // absolute error bound of s
-  uint32_t pad[6];
+// One per (row, part), written by the part's workgroup with agent-scope stores, read by the row's resolve.
+struct SliceRec {    // 64 bytes
+  uint64_t top;      // packed (key, lowest id): of nan_to_num(x)'s maximum for greedy rows; of -inf for sampled rows
+                     // (used when the row has no z > -inf)
+  uint32_t kappa;    // certified key: every element of the part with key >= kappa is in its waves' lists
+  uint32_t flags;    // F_*
+  uint32_t mkey;     // key of the part maximum of z (z = x for greedy rows)
+  uint32_t wcnt[PWAVES];  // elements listed by each wave (<= CAPW)
+  uint32_t pad0;
+  double s;          // sum over the part's unlisted elements of exp(z - z_part_max), fp32 exp2 terms
+  double bnd;        // absolute error bound of s
+  uint32_t pad[2];
 };
 static_assert(sizeof(SliceRec) == 64, "");
 
@@ -56,7 +62,8 @@ static_assert(sizeof(RowInfo) == 64, "");
 struct ScanArgs {
   const void *logits;
   int64_t ld;
-  int dtype, V, rows, nch, mode, force_exact, xcd_map, pad;
+  int dtype, V, rows, nch, mode, force_exact, xcd_map;
+  int nparts, plen;  // the main pass: parts per row, tokens per part (a multiple of 1024; the last part may be shorter)
   const gse_row *params;
   const int32_t *mask;
   int64_t mask_ld;
@@ -68,8 +75,8 @@ struct ScanArgs {
   int32_t *lp_ids;
   float *lps;
   int64_t lp_ld;
-  SliceRec *rec;    // [rows][nch]
-  uint64_t *cand;   // [rows][nch][CAPC]
+  SliceRec *rec;    // [rows][nparts]: one record per part
+  uint64_t *cand;   // [rows][nparts][PWAVES][CAPW]
   RowInfo *info;
   uint32_t *done;   // [rows] slice tickets, zero between calls
 };

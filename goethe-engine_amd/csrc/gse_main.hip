@@ -1,6 +1,8 @@
-// The fused selection pass: one 256-thread workgroup per (row, 8192-token slice) holds its slice in registers after a
-// single HBM read of the logits, the packed mask words and the row's history ids; the last workgroup of each row to
-// finish (atomic ticket, nothing waits) resolves the row.
+// The fused selection pass. One 256-thread workgroup per (row, part), a part being a contiguous run of at most 40960
+// tokens of the row. Its four waves stream the part in 1024-token chunks (64 lanes x 16 tokens), each wave on its own:
+// chunks are taken from an LDS counter, the next chunk's loads are in flight while the current one is processed, and
+// no barrier separates two chunks. One HBM read of the logits, the packed mask words and the row's history ids; the
+// last workgroup of each row to finish (atomic ticket, nothing waits) resolves the row.
 //
 // Reference semantics (goethe_engine/sampling.py:59-85):
 //   bad   = NaN anywhere before the mask, or no finite value after it        -> token -1            (sampling.py:71-75,84)
@@ -8,14 +10,16 @@
 //   T > 0 -> z = x / float32(T); stable descending order; fp64 softmax q; keep = rank < top_k AND cumsum(q) - q < top_p
 //            (AND q >= min_p * q_0); c = cumsum(q * keep); token = order[count(c < u * c[-1])]   (sampling.py:59-83)
 //
-// Per slice, in registers: penalties (u16 history counts in LDS), the NaN test, the mask, z = RN(x / T) computed as
-// RN32(x * RN64(1 / T)) (exact, see div_exact), the slice maximum, and the softmax sum of the elements the slice does
-// not list, from v_exp_f32 with a rigorous error bound. Each wave takes the 16th largest of its 64 lane maxima (to 16
-// key bits) as a threshold; the slice lists (exact key, id) of every element at or above the largest of its waves'
-// thresholds, so the listed set certifies the slice's top elements down to that key.
+// Per chunk, in registers: penalties (history counts from an LDS bitset of the part's tokens, indexed by rank), the NaN
+// test, the mask, z = RN(x / T) computed as RN32(x * RN64(1 / T)) (exact, see div_exact), each lane's running maximum,
+// and the softmax sum of the elements the wave does not list, from v_exp_f32 with a rigorous error bound (rescaled in
+// fp64 when a lane's maximum rises). The part's listing threshold is the 24th largest of the 256 lane maxima of its
+// waves' first chunks (to 16 key bits; the rank scaled down by the share of lanes that saw a z > -inf); a wave whose list passes half its capacity raises its own to the 8th largest of
+// its running lane maxima. Every element at or above the threshold in force for its chunk is listed (exact key, id);
+// thresholds only rise, so a wave's list certifies its top elements down to its final threshold.
 //
-// Row resolve: the union of the slices' lists cut at the largest certified key is the row's certified head: exactly its
-// top elements, stable order included. The resolve sorts the top ~512 of the head (the whole head when the keep prefix
+// Row resolve: the union of the waves' lists cut at the largest certified key is the row's certified head: exactly its
+// top elements, stable order included. The resolve sorts the top ~256 of the head (the whole head when the keep prefix
 // runs past them), takes exact fp64 masses of it (and of every listed element for S), and decides the keep prefix and
 // the draw. Top-k, min-p and the draw do not depend on S (they compare masses with masses); top-p uses the S bounds.
 // A decision inside the bound, a keep prefix that runs past the head, or an overflow marks the row hard: the exact
@@ -26,46 +30,61 @@ namespace gse {
 
 namespace {
 
-constexpr int MT = 256;                // threads per slice workgroup
+constexpr int MT = 256;                // threads per part workgroup
 constexpr int NWV = MT / WAVE;         // waves
-constexpr int EPT = CH / MT;           // 32 elements per thread
-constexpr int KW = 16;                 // lane rank of a wave's candidate threshold
+constexpr int EPL = 16;                // tokens per lane per chunk
+constexpr int CHK = WAVE * EPL;        // tokens per chunk
+constexpr int PMAX = PTOK;             // tokens per part, at most
+constexpr int PWORDS = PMAX / 32;      // history bitset words of a part
+constexpr int HMAX = 2048;             // distinct history ids of a part (more: the row takes the exact path)
+constexpr int KP = 24;                 // rank, among the part's 256 first-chunk lane maxima, of its listing threshold
+constexpr int KV = 8;                  // rank, among a wave's running lane maxima, of its raised threshold (when its
+                                       // list passes half its capacity)
 constexpr int NH = 2048;               // certified head capacity of the row resolve
-constexpr int NSUB = 1024;             // sorted sub-head capacity
-constexpr int SUBT = 512;              // sub-head target size
+constexpr int NSUB = 512;              // sorted sub-head capacity
+constexpr int SUBT = 256;              // sub-head target size
+constexpr int NSUB2 = 1024;            // the larger sorted top
 constexpr int HPT = 8;                 // history ids per thread per round
 constexpr int GPT = 8;                 // listed entries per thread per gather round
-constexpr int MAXSL = (1 << 21) / CH;  // slices of the largest vocabulary (= MT: one record per thread)
+constexpr int NSL = MAXP * PWAVES;     // wave lists of a row, at most (one per resolve thread)
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float FLTMAX = 3.402823466e+38f;
-static_assert(MAXSL <= MT, "one slice record per resolve thread");
+static_assert(NWV == PWAVES, "");
+static_assert(NSL <= MT, "one wave list per resolve thread");
 
 template <int DT>
 struct Lay;
 template <>
-struct Lay<GSE_F32> {  // thread tid, vector v, lane element k: token c0 + v * 1024 + tid * 4 + k
-  static constexpr int VEC = 4, NV = EPT / 4, STRIDE = MT * 4;
+struct Lay<GSE_F32> {  // chunk base cb, lane l, vector v, element k: token cb + v * 256 + l * 4 + k
+  static constexpr int VEC = 4, NV = EPL / 4, STRIDE = WAVE * 4;
 };
 template <>
-struct Lay<GSE_BF16> {  // token c0 + v * 2048 + tid * 8 + k
-  static constexpr int VEC = 8, NV = EPT / 8, STRIDE = MT * 8;
+struct Lay<GSE_BF16> {  // token cb + v * 512 + l * 8 + k
+  static constexpr int VEC = 8, NV = EPL / 8, STRIDE = WAVE * 8;
 };
 
 struct Shared {
   union {
-    uint32_t cnt[CH / 2];  // history counts of the slice's tokens, two u16 per word
+    struct {                   // history of the part's tokens: bitset, prefix popcounts, counts by rank
+      uint32_t bits[PWORDS];
+      uint32_t pre[PWORDS];
+      uint32_t cnt[HMAX];
+    } h;
     struct {
-      uint64_t head[NH];   // listed elements at or above the certified key
-      uint64_t sub[NSUB];  // the top of the head
+      uint64_t head[NH];       // listed elements at or above the certified key
+      uint64_t sub[NSUB2];     // the top of the head
     } r;
   };
+  uint32_t next;               // next chunk of the part
+  uint32_t hover;              // more distinct history ids than HMAX
+  uint32_t ticket;
   float wmax[NWV];
-  uint32_t wtau[NWV];
-  uint32_t wflags[NWV];
+  uint32_t wflags[NWV], wkap[NWV], wcnt[NWV];
+  uint32_t lmax[MT];           // first-chunk lane maxima (16 key bits)
+  uint64_t wtop[NWV];
   double wred[NWV], wred2[NWV];
-  uint32_t minid, ncand, ticket, hover;
   // resolve
-  uint32_t loff[MAXSL];
+  uint32_t loff[NSL];
   uint32_t bins[256];
   uint64_t rtop, rtopL;
   uint32_t rflags, rkappa, rmkey, ltot, nh, ns, mfail_sure, mfail_maybe, jcount, bsel;
@@ -82,71 +101,97 @@ __device__ __forceinline__ int nlp_of(const ScanArgs &a, const gse_row &P) {
   return a.lp_ids ? min(min(P.logprobs, GSE_MAX_LOGPROBS), (int)a.lp_ld) : 0;
 }
 
-// u16 history counts of tokens [c0, c0 + CH) into sh.cnt; hid holds this thread's ids of the first round (loaded
-// before the logits). Returns true (in every thread) when a token occurs more than 65535 times (its counter would
-// carry): the row then takes the exact path. Ends with a barrier.
-__device__ __forceinline__ bool build_counts16(const RowCtx &c, const int32_t *hist, const int (&hid)[HPT], int c0,
-                                               Shared &sh) {
-  for (int i = threadIdx.x; i < CH / 8; i += MT) reinterpret_cast<uint4 *>(sh.cnt)[i] = make_uint4(0, 0, 0, 0);
-  if (threadIdx.x == 0) sh.hover = 0;
+// The part's history [p0, p1): bitset of the tokens present, their prefix popcounts, and the count of each present
+// token indexed by its rank among them. hid holds this thread's first ids (loaded before the logits). Ends with a
+// barrier.
+__device__ __forceinline__ void build_history(const RowCtx &c, const int32_t *hist, const int (&hid)[HPT], int p0,
+                                              int p1, Shared &sh) {
+  const int tid = threadIdx.x;
+  const int nw = (p1 - p0 + 31) >> 5;
+  for (int i = tid; i < nw; i += MT) sh.h.bits[i] = 0;
   __syncthreads();
-  bool ov = false;
-  auto add = [&](int t) {
-    if (t >= c0 && t < c0 + CH && t < c.V) {
-      const int o = t - c0, s = (o & 1) * 16;
-      const uint32_t old = atomicAdd(&sh.cnt[o >> 1], 1u << s);
-      ov |= ((old >> s) & 0xFFFFu) == 0xFFFFu;
+  auto each = [&](auto f) {
+#pragma unroll
+    for (int k = 0; k < HPT; ++k)
+      if (hid[k] >= p0 && hid[k] < p1) f(hid[k] - p0);
+    for (int j0 = c.hb + MT * HPT; j0 < c.he; j0 += MT * HPT) {
+      int more[HPT];
+#pragma unroll
+      for (int k = 0; k < HPT; ++k) {
+        const int j = j0 + k * MT + tid;
+        more[k] = j < c.he ? hist[j] : -1;
+      }
+#pragma unroll
+      for (int k = 0; k < HPT; ++k)
+        if (more[k] >= p0 && more[k] < p1) f(more[k] - p0);
     }
   };
-#pragma unroll
-  for (int k = 0; k < HPT; ++k) add(hid[k]);
-  for (int j0 = c.hb + MT * HPT; j0 < c.he; j0 += MT * HPT) {
-    int more[HPT];
-#pragma unroll
-    for (int k = 0; k < HPT; ++k) {
-      const int j = j0 + k * MT + (int)threadIdx.x;
-      more[k] = j < c.he ? hist[j] : -1;
-    }
-#pragma unroll
-    for (int k = 0; k < HPT; ++k) add(more[k]);
-  }
-  if (ov) sh.hover = 1u;
+  each([&](int o) { atomicOr(&sh.h.bits[o >> 5], 1u << (o & 31)); });
   __syncthreads();
-  return sh.hover != 0;
+  // exclusive prefix of the word popcounts (words per thread contiguous)
+  const int per = (nw + MT - 1) / MT, w0 = tid * per;
+  uint32_t loc = 0;
+  for (int i = 0; i < per; ++i)
+    if (w0 + i < nw) loc += __popc(sh.h.bits[w0 + i]);
+  const uint32_t inc = wave_incl_scan_u32(loc);
+  if (lane_id() == WAVE - 1) sh.wcnt[tid >> 6] = inc;
+  __syncthreads();
+  uint32_t run = inc - loc, tot = 0;
+#pragma unroll
+  for (int w = 0; w < NWV; ++w) {
+    run += w < (tid >> 6) ? sh.wcnt[w] : 0u;
+    tot += sh.wcnt[w];
+  }
+  for (int i = 0; i < per; ++i)
+    if (w0 + i < nw) {
+      sh.h.pre[w0 + i] = run;
+      run += __popc(sh.h.bits[w0 + i]);
+    }
+  const uint32_t nd = min(tot, (uint32_t)HMAX);
+  for (uint32_t i = tid; i < nd; i += MT) sh.h.cnt[i] = 0;
+  if (tid == 0 && tot > (uint32_t)HMAX) sh.hover = 1;
+  __syncthreads();
+  each([&](int o) {
+    const uint32_t r = sh.h.pre[o >> 5] + __popc(sh.h.bits[o >> 5] & ((1u << (o & 31)) - 1u));
+    if (r < (uint32_t)HMAX) atomicAdd(&sh.h.cnt[r], 1u);
+  });
+  __syncthreads();
 }
 
-template <int DT, bool FULL>
-__device__ __forceinline__ void load_slice(const RowCtx &c, int c0, float (&x)[EPT]) {
+// One chunk's logits into registers (fp32, or bf16 widened exactly) and its packed mask words; AL: the row start is
+// 16-byte aligned, so a whole vector is one 16-byte load. A token past the part end loads 0.
+template <int DT, bool AL>
+__device__ __forceinline__ void load_chunk(const RowCtx &c, int cb, int p1, float (&x)[EPL],
+                                           uint32_t (&mw)[Lay<DT>::NV]) {
   using L = Lay<DT>;
-  const int tid = threadIdx.x;
+  const int l = lane_id();
+#pragma unroll
+  for (int v = 0; v < L::NV; ++v) {
+    const int t0 = cb + v * L::STRIDE + l * L::VEC;
+    mw[v] = c.mw ? (t0 < p1 ? c.mw[t0 >> 5] : 0u) : 0xFFFFFFFFu;
+  }
   if constexpr (DT == GSE_F32) {
-    const float *p = (const float *)c.base + c0 + tid * 4;
+    const float *p = (const float *)c.base + cb + l * 4;
 #pragma unroll
     for (int v = 0; v < L::NV; ++v) {
-      if (FULL) {
+      const int t0 = cb + v * L::STRIDE + l * 4;
+      if (AL && t0 + 4 <= p1) {
         const float4 f = *reinterpret_cast<const float4 *>(p + v * L::STRIDE);
         x[4 * v] = f.x;
         x[4 * v + 1] = f.y;
         x[4 * v + 2] = f.z;
         x[4 * v + 3] = f.w;
       } else {
-        const int t0 = c0 + v * L::STRIDE + tid * 4;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) x[4 * v + k] = 0.0f;
-        if (t0 < c.V) {
-          const float *q = p + v * L::STRIDE;
-          x[4 * v] = q[0];
-#pragma unroll
-          for (int k = 1; k < 4; ++k)
-            if (t0 + k < c.V) x[4 * v + k] = q[k];
-        }
+        for (int k = 0; k < 4; ++k) x[4 * v + k] = t0 + k < p1 ? p[v * L::STRIDE + k] : 0.0f;
       }
     }
   } else {
-    const uint16_t *p = (const uint16_t *)c.base + c0 + tid * 8;
+    const uint16_t *p = (const uint16_t *)c.base + cb + l * 8;
 #pragma unroll
     for (int v = 0; v < L::NV; ++v) {
-      if (FULL) {
+      const int t0 = cb + v * L::STRIDE + l * 8;
+      if (AL && t0 + 8 <= p1) {
         const uint4 u = *reinterpret_cast<const uint4 *>(p + v * L::STRIDE);
         const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
@@ -155,15 +200,8 @@ __device__ __forceinline__ void load_slice(const RowCtx &c, int c0, float (&x)[E
           x[8 * v + 2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
         }
       } else {
-        const int t0 = c0 + v * L::STRIDE + tid * 8;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) x[8 * v + k] = 0.0f;
-        if (t0 < c.V) {
-          const uint16_t *q = p + v * L::STRIDE;
-#pragma unroll
-          for (int k = 0; k < 8; ++k)
-            if (t0 + k < c.V) x[8 * v + k] = bf16_to_f32(q[k]);
-        }
+        for (int k = 0; k < 8; ++k) x[8 * v + k] = t0 + k < p1 ? bf16_to_f32(p[v * L::STRIDE + k]) : 0.0f;
       }
     }
   }
@@ -195,22 +233,49 @@ __device__ __forceinline__ double block_excl_scan_f64(double v, double *red) {
   return pre + inc - v;
 }
 
-// Descending bitonic sort of n (a power of two) packed keys in LDS, one compare-exchange pair per thread per step.
-__device__ __forceinline__ void bitonic_desc(uint64_t *a, int n) {
-  const int half = n >> 1;
-  for (int k = 2; k <= n; k <<= 1) {
+// Descending bitonic sort of MT * S packed keys held S per thread (element i = tid * S + s). Pairs closer than S are
+// in one thread, closer than WAVE * S in one wave (lane shuffles); only the three widest steps go through LDS (buf,
+// MT * S entries), each between two barriers.
+template <int S>
+__device__ __forceinline__ void sort_regs(uint64_t (&v)[S], uint64_t *buf) {
+  constexpr int N = MT * S;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int p = threadIdx.x; p < half; p += MT) {
-        const int lo = ((p & ~(j - 1)) << 1) | (p & (j - 1));
-        const int hi = lo | j;
-        const uint64_t x = a[lo], y = a[hi];
-        const bool desc = (lo & k) == 0;
-        if (desc ? (x < y) : (x > y)) {
-          a[lo] = y;
-          a[hi] = x;
+      if (j < S) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          if ((s ^ j) > s) {
+            const bool desc = ((tid * S + s) & k) == 0;
+            const uint64_t x = v[s], y = v[s ^ j];
+            if (desc ? (x < y) : (x > y)) {
+              v[s] = y;
+              v[s ^ j] = x;
+            }
+          }
+        }
+      } else {
+        uint64_t o[S];
+        if (j < WAVE * S) {
+#pragma unroll
+          for (int s = 0; s < S; ++s) o[s] = shfl_xor_u64(v[s], j / S);
+        } else {
+#pragma unroll
+          for (int s = 0; s < S; ++s) buf[tid * S + s] = v[s];
+          __syncthreads();
+#pragma unroll
+          for (int s = 0; s < S; ++s) o[s] = buf[(tid * S + s) ^ j];
+          __syncthreads();
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const int i = tid * S + s;
+          const bool keep_max = (((i & k) == 0) == ((i & j) == 0));  // lower of a descending pair, upper of an ascending
+          v[s] = keep_max ? (o[s] > v[s] ? o[s] : v[s]) : (o[s] < v[s] ? o[s] : v[s]);
         }
       }
-      __syncthreads();
     }
   }
 }
@@ -248,40 +313,42 @@ struct RowEval {
   const gse_row *P;
 };
 
-// Keep prefix, draw and logprobs over the sorted top arr[0, ns) of the head (ns == n: the whole head).
-template <int RPT>
-__device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, int ns, Shared &sh) {
+// Sorts the top arr[0, ns) of the head (ns <= MT * S; ns == n: the whole head) and decides the keep prefix, the draw
+// and the logprobs over it. arr is overwritten with the sorted ranks.
+template <int S>
+__device__ __forceinline__ int evaluate(const RowEval &ev, uint64_t *arr, int ns, Shared &sh) {
   const ScanArgs &a = *ev.a;
   const gse_row &P = *ev.P;
   const int tid = threadIdx.x;
   const bool all = ns == ev.n;
   if (ev.nlp > ns && !all) return EV_MORE;
   if (ev.nlp > ns) return EV_HARD;  // logprobs past the finite elements: -inf ranks in id order
+  uint64_t v[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) v[s] = tid * S + s < ns ? arr[tid * S + s] : 0ull;
+  __syncthreads();
+  sort_regs<S>(v, arr);
+#pragma unroll
+  for (int s = 0; s < S; ++s) arr[tid * S + s] = v[s];
   if (tid == 0) {
     sh.mfail_sure = 0xFFFFFFFFu;
     sh.mfail_maybe = 0xFFFFFFFFu;
     sh.jcount = 0;
   }
-  // ranks [r0, r0 + RPT) per thread: exact masses e, exclusive prefixes A, inclusive prefixes I
-  const int r0 = tid * RPT;
-  const double M = ev.M, S = ev.S;
-  double e[RPT], A[RPT], I[RPT];
+  // ranks tid * S + s: exact masses e; prefixes recomputed from the thread's exclusive base (A_s = base + e_0 + ...
+  // + e_{s-1}, I_s = A_s + e_s, the same additions in the same order every time)
+  const int r0 = tid * S;
+  const double M = ev.M, Sm = ev.S;
+  double e[S];
   double loc = 0.0;
 #pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    const int r = r0 + i;
-    e[i] = r < ns ? exp((double)fkey_inv(pk_key(arr[r])) - M) : 0.0;
-    loc += e[i];
+  for (int s = 0; s < S; ++s) {
+    e[s] = r0 + s < ns ? exp((double)fkey_inv(pk_key(v[s])) - M) : 0.0;
+    loc += e[s];
   }
-  double run = block_excl_scan_f64(loc, sh.wred);
-#pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    A[i] = run;
-    run += e[i];
-    I[i] = run;
-  }
+  const double base = block_excl_scan_f64(loc, sh.wred);  // (its barriers publish arr and the resets above)
   if (ev.nlp > 0) {
-    const double lS = log(S);
+    const double lS = log(Sm);
     for (int i = tid; i < ev.nlp; i += MT) {
       const uint64_t pk = arr[i];
       a.lp_ids[(int64_t)ev.row * a.lp_ld + i] = (int32_t)pk_id(pk);
@@ -290,25 +357,34 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
   }
   RowInfo *ri = a.info + ev.row;
   if (ev.greedy) {
-    if (tid == 0) set_info(ri, ev.gtop, 0, S, 0.0, R_DONE | R_GREEDY, (int32_t)pk_id(ev.gtop));
+    if (tid == 0) set_info(ri, ev.gtop, 0, Sm, 0.0, R_DONE | R_GREEDY, (int32_t)pk_id(ev.gtop));
     return EV_DONE;
   }
   // keep_r = r < K AND A_r / S < top_p AND q_r >= min_p q_0 (sampling.py:80 plus min-p). A top-p decision is sure when
   // it holds for every S in [S - B, S + B]; the first rank that surely fails and the first that may fail must agree.
   const int64_t K = P.top_k > 0 ? (int64_t)P.top_k : (int64_t)0x7FFFFFFFFFFFll;
   const double topp = P.top_p, minp = P.min_p;
-  const double q0 = 1.0 / S, Slo = S - ev.B, Shi = S + ev.B;
+  const double q0 = 1.0 / Sm, Slo = Sm - ev.B, Shi = Sm + ev.B;
+  uint32_t fsure = 0xFFFFFFFFu, fmaybe = 0xFFFFFFFFu;
+  {
+    double A = base;
 #pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    const int r = r0 + i;
-    if (r < ns) {
-      const bool kk = (int64_t)r < K;
-      const bool km = !(minp > 0.0) || (e[i] / S >= minp * q0);
-      const bool fs = !kk || !km || (A[i] / Shi >= topp);
-      const bool fm = !kk || !km || !(A[i] / Slo < topp);
-      if (fs) atomicMin(&sh.mfail_sure, (uint32_t)r);
-      if (fm) atomicMin(&sh.mfail_maybe, (uint32_t)r);
+    for (int s = 0; s < S; ++s) {
+      const int r = r0 + s;
+      if (r < ns) {
+        const bool kk = (int64_t)r < K;
+        const bool km = !(minp > 0.0) || (e[s] / Sm >= minp * q0);
+        if ((!kk || !km || (A / Shi >= topp)) && fsure == 0xFFFFFFFFu) fsure = (uint32_t)r;
+        if ((!kk || !km || !(A / Slo < topp)) && fmaybe == 0xFFFFFFFFu) fmaybe = (uint32_t)r;
+      }
+      A += e[s];
     }
+  }
+  fsure = wave_min_u32(fsure);
+  fmaybe = wave_min_u32(fmaybe);
+  if (lane_id() == 0) {
+    atomicMin(&sh.mfail_sure, fsure);
+    atomicMin(&sh.mfail_maybe, fmaybe);
   }
   __syncthreads();
   uint32_t m = sh.mfail_sure;
@@ -319,9 +395,14 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
     m = (uint32_t)ns;
   }
   // c_last = I_{m-1}; j = #{r < m : I_r < u c_last}, clamped to [0, m - 1] (sampling.py:81-83)
+  {
+    double I = base;
 #pragma unroll
-  for (int i = 0; i < RPT; ++i)
-    if ((uint32_t)(r0 + i) == m - 1) sh.rsc = I[i];
+    for (int s = 0; s < S; ++s) {
+      I += e[s];
+      if ((uint32_t)(r0 + s) == m - 1) sh.rsc = I;
+    }
+  }
   __syncthreads();
   const double clast = sh.rsc;
   int32_t tok = -1;
@@ -329,26 +410,70 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
     const double u = a.uni ? a.uni[ev.row] : uniform64(P.seed, P.idx);
     const double thr = u * clast;
     uint32_t cnt = 0;
+    double I = base;
 #pragma unroll
-    for (int i = 0; i < RPT; ++i)
-      if ((uint32_t)(r0 + i) < m && I[i] < thr) ++cnt;
-    if (cnt) atomicAdd(&sh.jcount, cnt);
+    for (int s = 0; s < S; ++s) {
+      I += e[s];
+      if ((uint32_t)(r0 + s) < m && I < thr) ++cnt;
+    }
+    cnt = wave_incl_scan_u32(cnt);
+    if (lane_id() == WAVE - 1 && cnt) atomicAdd(&sh.jcount, cnt);
     __syncthreads();
     tok = (int32_t)pk_id(arr[min(sh.jcount, m - 1u)]);
   }
   if (tid == 0) {
-    set_info(ri, arr[0], arr[m - 1], S, clast / S, R_DONE, tok);
+    set_info(ri, arr[0], arr[m - 1], Sm, clast / Sm, R_DONE, tok);
     if (a.mode == MODE_SAMPLE) a.tokens[ev.row] = tok;
   }
   return EV_DONE;
 }
 
+// Copies into sh.r.sub the elements of the head sh.r.head[0, n) in the bins of a 256-bin count histogram of
+// (mk - key) up to the bin where the count crosses target (or the bin before it when that one would exceed cap).
+// Returns the number copied (more than cap when even that does not fit; then nothing past cap is copied).
+__device__ __forceinline__ int select_top(Shared &sh, int n, uint32_t mk, uint32_t kappa, int target, int cap) {
+  const int tid = threadIdx.x;
+  const uint32_t span = mk - kappa;
+  const int shift = span >> 8 ? 32 - __clz(span) - 8 : 0;
+  __syncthreads();
+  sh.bins[tid] = 0;
+  if (tid == 0) {
+    sh.bsel = 255;
+    sh.ns = 0;
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += MT) atomicAdd(&sh.bins[(mk - pk_key(sh.r.head[i])) >> shift], 1u);
+  __syncthreads();
+  const uint32_t cb = sh.bins[tid];
+  const uint32_t inc = wave_incl_scan_u32(cb);
+  if (lane_id() == WAVE - 1) sh.wcnt[tid >> 6] = inc;
+  __syncthreads();
+  uint32_t pre = 0;
+#pragma unroll
+  for (int w = 0; w < NWV; ++w) pre += w < (tid >> 6) ? sh.wcnt[w] : 0u;
+  const uint32_t incl = pre + inc;
+  if (incl >= (uint32_t)target && incl - cb < (uint32_t)target)  // the bin that crosses the target
+    atomicMin(&sh.bsel, incl <= (uint32_t)cap || tid == 0 ? (uint32_t)tid : (uint32_t)tid - 1u);
+  __syncthreads();
+  const uint32_t bsel = sh.bsel;
+  for (int i = tid; i < n; i += MT) {
+    const uint64_t pk = sh.r.head[i];
+    if (((mk - pk_key(pk)) >> shift) <= bsel) {
+      const uint32_t pos = atomicAdd(&sh.ns, 1u);
+      if (pos < (uint32_t)cap) sh.r.sub[pos] = pk;
+    }
+  }
+  __syncthreads();
+  return (int)sh.ns;
+}
+
 __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gse_row &P, Shared &sh) {
   const int tid = threadIdx.x;
-  const SliceRec *rb = a.rec + (size_t)row * a.nch;
+  const SliceRec *rb = a.rec + (size_t)row * a.nparts;
   const bool greedy = is_greedy(a.mode, P);
   RowInfo *ri = a.info + row;
   const int nlp = nlp_of(a, P);
+  const int nsl = a.nparts * PWAVES;
   if (tid == 0) {
     sh.rtop = 0;
     sh.rtopL = 0;
@@ -358,39 +483,42 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
     sh.nh = 0;
     sh.ns = 0;
   }
-  // One round of record loads: thread s holds slice s's record.
+  // One round of record loads: thread j holds wave list j (part j / 4), threads j % 4 == 0 the part's record.
+  const int prt = tid / PWAVES;
   uint32_t r_nc = 0, r_mkey = 0, r_kap = 0, r_fl = 0;
   uint64_t r_top = 0;
   double r_s = 0.0, r_b = 0.0;
-  if (tid < a.nch) {
-    const SliceRec *r = rb + tid;
-    r_top = ld_ag(&r->top);
-    r_kap = ld_ag(&r->kappa);
-    r_fl = ld_ag(&r->flags);
-    r_nc = ld_ag(&r->ncand);
-    r_mkey = ld_ag(&r->mkey);
-    r_s = ld_ag(&r->s);
-    r_b = ld_ag(&r->bnd);
+  if (tid < nsl) {
+    const SliceRec *r = rb + prt;
+    r_nc = min(ld_ag(&r->wcnt[tid % PWAVES]), (uint32_t)CAPW);
+    if (tid % PWAVES == 0) {
+      r_top = ld_ag(&r->top);
+      r_kap = ld_ag(&r->kappa);
+      r_fl = ld_ag(&r->flags);
+      r_mkey = ld_ag(&r->mkey);
+      r_s = ld_ag(&r->s);
+      r_b = ld_ag(&r->bnd);
+    }
   }
   __syncthreads();
-  if (tid < a.nch) {
+  if (tid < nsl && tid % PWAVES == 0) {
     atomicOr(&sh.rflags, r_fl);
     atomicMax((unsigned long long *)&sh.rtop, (unsigned long long)r_top);
     atomicMax(&sh.rkappa, r_kap);
     atomicMax(&sh.rmkey, r_mkey);
   }
-  // exclusive prefix of the list lengths (one record per thread)
+  // exclusive prefix of the list lengths (one list per thread)
   {
     const uint32_t inc = wave_incl_scan_u32(r_nc);
-    if (lane_id() == WAVE - 1) sh.wtau[tid >> 6] = inc;
+    if (lane_id() == WAVE - 1) sh.wcnt[tid >> 6] = inc;
     __syncthreads();
     uint32_t pre = 0, tot = 0;
 #pragma unroll
     for (int w = 0; w < NWV; ++w) {
-      pre += w < (tid >> 6) ? sh.wtau[w] : 0u;
-      tot += sh.wtau[w];
+      pre += w < (tid >> 6) ? sh.wcnt[w] : 0u;
+      tot += sh.wcnt[w];
     }
-    if (tid < a.nch) sh.loff[tid] = pre + inc - r_nc;
+    if (tid < nsl) sh.loff[tid] = pre + inc - r_nc;
     if (tid == 0) sh.ltot = tot;
   }
   __syncthreads();
@@ -400,7 +528,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   const bool bad = (flags & F_NAN) || !(flags & F_FINITE);
 
   if ((flags & F_OVERFLOW) && (greedy || bad)) {
-    // a history counter carried: the exact path redoes the whole row (flags, argmax, logprobs)
+    // more distinct history ids than a part can count: the exact path redoes the whole row (flags, argmax, logprobs)
     if (tid == 0) set_info(ri, gtop, 0, 0.0, 0.0, R_HARD | R_FULL | (greedy ? R_GREEDY : 0u), -1);
     return;
   }
@@ -431,13 +559,13 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   const uint32_t kappa = max(sh.rkappa, KEY_NEGINF + 1u);
   const bool complete = kappa <= KEY_NEGINF + 1u;
   double srest = 0.0, brest = 0.0;
-  if (tid < a.nch && finite_max && r_mkey > KEY_NEGINF) {
+  if (tid < nsl && tid % PWAVES == 0 && finite_max && r_mkey > KEY_NEGINF) {
     const double f = exp((double)fkey_inv(r_mkey) - M);
     srest = f * r_s;
     brest = f * r_b;
   }
   double scand = 0.0;
-  const uint64_t *cl0 = a.cand + (size_t)row * a.nch * CAPC;
+  const uint64_t *cl0 = a.cand + (size_t)row * nsl * CAPW;
   const uint32_t ltot = sh.ltot;
   uint64_t bestL = 0;
   for (uint32_t f0 = 0; f0 < ltot; f0 += MT * GPT) {
@@ -447,13 +575,13 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
       const uint32_t f = f0 + g * MT + tid;
       pk[g] = 0;
       if (f < ltot) {
-        int lo = 0, hi = a.nch - 1;  // the slice whose range [loff, loff + ncand) holds f
+        int lo = 0, hi = nsl - 1;  // the wave list whose range [loff, loff + count) holds f
         while (lo < hi) {
           const int mid = (lo + hi + 1) >> 1;
           if (sh.loff[mid] <= f) lo = mid;
           else hi = mid - 1;
         }
-        pk[g] = ld_ag(&cl0[(size_t)lo * CAPC + (f - sh.loff[lo])]);
+        pk[g] = ld_ag(&cl0[(size_t)lo * CAPW + (f - sh.loff[lo])]);
       }
     }
 #pragma unroll
@@ -506,58 +634,16 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   int st = EV_HARD;
   if (!((flags & F_OVERFLOW) || nh_all > (uint32_t)NH || a.force_exact)) {
     if (n <= NSUB) {
-      const int np2 = pow2_ceil(max(n, 2));
-      for (int i = n + tid; i < np2; i += MT) sh.r.head[i] = 0;
-      __syncthreads();
-      bitonic_desc(sh.r.head, np2);
       st = evaluate<NSUB / MT>(ev, sh.r.head, n, sh);
     } else {
-      // The top of the head: a 256-bin count histogram of (max key - key) picks a key bound with >= SUBT elements
-      // above it (<= NSUB when the bins allow); those are sorted first.
-      const uint32_t span = mk - kappa;
-      const int shift = span >> 8 ? 32 - __clz(span) - 8 : 0;
-      sh.bins[tid] = 0;
-      if (tid == 0) sh.bsel = 255;
-      __syncthreads();
-      for (int i = tid; i < n; i += MT) atomicAdd(&sh.bins[(mk - pk_key(sh.r.head[i])) >> shift], 1u);
-      __syncthreads();
-      const uint32_t cb = sh.bins[tid];
-      const uint32_t inc = wave_incl_scan_u32(cb);
-      if (lane_id() == WAVE - 1) sh.wtau[tid >> 6] = inc;
-      __syncthreads();
-      uint32_t pre = 0;
-#pragma unroll
-      for (int w = 0; w < NWV; ++w) pre += w < (tid >> 6) ? sh.wtau[w] : 0u;
-      const uint32_t incl = pre + inc;
-      if (incl >= (uint32_t)SUBT && incl - cb < (uint32_t)SUBT) {  // the bin that crosses the target
-        atomicMin(&sh.bsel, incl <= (uint32_t)NSUB || tid == 0 ? (uint32_t)tid : (uint32_t)tid - 1u);
-      }
-      __syncthreads();
-      const uint32_t bsel = sh.bsel;
-      for (int i = tid; i < n; i += MT) {
-        const uint64_t pk = sh.r.head[i];
-        if (((mk - pk_key(pk)) >> shift) <= bsel) {
-          const uint32_t pos = atomicAdd(&sh.ns, 1u);
-          if (pos < (uint32_t)NSUB) sh.r.sub[pos] = pk;
-        }
-      }
-      __syncthreads();
-      const int ns = (int)min(sh.ns, (uint32_t)NSUB);
-      if (sh.ns <= (uint32_t)NSUB) {
-        const int np2 = pow2_ceil(max(ns, 2));
-        for (int i = ns + tid; i < np2; i += MT) sh.r.sub[i] = 0;
-        __syncthreads();
-        bitonic_desc(sh.r.sub, np2);
-        st = evaluate<NSUB / MT>(ev, sh.r.sub, ns, sh);
-      } else {
-        st = EV_MORE;
-      }
-      if (st == EV_MORE) {  // the keep prefix (or the logprobs) run past the sorted top: sort the whole head
-        const int np2 = pow2_ceil(n);
-        for (int i = n + tid; i < np2; i += MT) sh.r.head[i] = 0;
-        __syncthreads();
-        bitonic_desc(sh.r.head, np2);
-        st = evaluate<NH / MT>(ev, sh.r.head, n, sh);
+      // The top of the head first (>= 256 elements, <= 512 when the bins allow), then a larger top (<= 1024) when the
+      // keep prefix runs past it; a keep prefix past that takes the exact path.
+      const int ns = select_top(sh, n, mk, kappa, SUBT, NSUB);
+      st = ns <= NSUB ? evaluate<NSUB / MT>(ev, sh.r.sub, ns, sh) : EV_MORE;
+      if (st == EV_MORE) {
+        const int ns2 = select_top(sh, n, mk, kappa, NSUB2 - NSUB2 / 4, NSUB2);
+        st = ns2 <= NSUB2 ? evaluate<NSUB2 / MT>(ev, sh.r.sub, ns2, sh) : EV_HARD;
+        if (st == EV_MORE) st = EV_HARD;
       }
     }
   }
@@ -568,21 +654,177 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
+// Part streaming.
 
-// One slice. Returns true in the workgroup that finished the row last (it then resolves the row).
-template <int DT, bool FULL>
-__device__ __forceinline__ bool slice_body(const ScanArgs &a, const gse_row &P, const RowCtx &c, int row, int sl,
-                                           Shared &sh) {
+// Per-lane running state of a wave.
+struct Lane {
+  float m;         // running maximum of this lane's z
+  double s;        // sum of this lane's unlisted exp(z - m) (fp32 terms)
+  double b;        // its error bound
+  uint32_t kap;    // the wave's listing threshold key in force (uniform in the wave; only rises)
+  uint32_t woff;   // elements the wave has listed (uniform)
+  float g;         // greedy rows: largest nan_to_num(x) so far, at token gid (the first one)
+  uint32_t gid;
+  uint32_t fid;    // first token of this lane with z not NaN (the lowest -inf when the row has no z > -inf)
+  bool fnan, ffin;
+};
+
+// Phase 1 of a chunk: penalties, NaN test (before the mask), mask, z in place. Returns the lane's chunk maximum of z.
+template <int DT>
+__device__ __forceinline__ float chunk_phase1(const ScanArgs &a, const RowCtx &c, int row, int cb, int p0, int p1,
+                                              float (&xr)[EPL], const uint32_t (&mw)[Lay<DT>::NV], Lane &ln,
+                                              const Shared &sh) {
   using L = Lay<DT>;
   constexpr uint32_t VMASK = (1u << L::VEC) - 1u;
-  const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
-  const int c0 = sl * CH;
-  const int nlp = nlp_of(a, P);
-  const bool listing = !c.greedy || nlp > 0;  // candidates and the softmax sum are needed
+  const int l = lane_id();
   const bool divide = c.divide;
   const double Rd = c.Rd;
+  float *proc = a.processed ? a.processed + (int64_t)row * a.processed_ld : nullptr;
+  float cmax = -INFINITY;
+#pragma unroll
+  for (int v = 0; v < L::NV; ++v) {
+    const int t0 = cb + v * L::STRIDE + l * L::VEC;
+    uint32_t bits = (mw[v] >> ((l * L::VEC) & 31)) & VMASK;
+    if (t0 + L::VEC > p1) bits &= t0 >= p1 ? 0u : (1u << (p1 - t0)) - 1u;  // past the part end
+    if (c.pen && t0 < p1) {
+      const int o = t0 - p0;
+      const uint32_t hw = sh.h.bits[o >> 5];
+      const uint32_t hb = (hw >> (o & 31)) & VMASK;
+      if (hb) {
+#pragma unroll
+        for (int k = 0; k < L::VEC; ++k) {
+          if ((hb >> k) & 1u) {
+            const int ok = o + k;
+            const uint32_t r = sh.h.pre[ok >> 5] + __popc(sh.h.bits[ok >> 5] & ((1u << (ok & 31)) - 1u));
+            xr[v * L::VEC + k] = penalize(xr[v * L::VEC + k], sh.h.cnt[min(r, (uint32_t)HMAX - 1u)], c.rp, c.fp,
+                                          c.pp);
+          }
+        }
+      }
+    }
+    if (bits == VMASK) {  // every token of the vector allowed
+#pragma unroll
+      for (int k = 0; k < L::VEC; ++k) {
+        const int i = v * L::VEC + k;
+        const float x = xr[i];
+        ln.fnan |= (x != x);
+        ln.ffin |= fabsf(x) < INFINITY;
+        if (proc) proc[t0 + k] = x;
+        const float z = divide ? div_exact(x, Rd) : x;
+        xr[i] = z;
+        cmax = fmaxf(cmax, z);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < L::VEC; ++k) {
+        const int i = v * L::VEC + k;
+        const float x = xr[i];
+        ln.fnan |= (x != x);  // (a token past the part end loads 0)
+        const bool al = (bits >> k) & 1u;
+        const float xm = al ? x : -INFINITY;
+        ln.ffin |= fabsf(xm) < INFINITY;
+        if (proc && t0 + k < p1) proc[t0 + k] = xm;
+        const float z = (divide && al) ? div_exact(x, Rd) : xm;
+        xr[i] = z;
+        cmax = fmaxf(cmax, z);
+      }
+    }
+  }
+  // the first token with z not NaN (only until this lane has one)
+  if (ln.fid == 0xFFFFFFFFu) {
+#pragma unroll
+    for (int i = EPL - 1; i >= 0; --i) {
+      const int t = cb + (i / L::VEC) * L::STRIDE + l * L::VEC + (i % L::VEC);
+      if (t < p1 && xr[i] == xr[i]) ln.fid = (uint32_t)t;
+    }
+  }
+  if (c.greedy) {  // first maximum of nan_to_num(x) (sampling.py:76), in token order
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const float g = fminf(fmaxf(xr[i], -FLTMAX), FLTMAX);
+      const int t = cb + (i / L::VEC) * L::STRIDE + l * L::VEC + (i % L::VEC);
+      if (t < p1 && xr[i] == xr[i] && (g > ln.g || ln.gid == 0xFFFFFFFFu)) {
+        ln.g = g;
+        ln.gid = (uint32_t)t;
+      }
+    }
+  }
+  return cmax;
+}
 
-  // History ids first, then the logits and mask words: the counts build while the logits stream in.
+// Phase 2 of a chunk (rows that list): the lane maximum, the threshold valve, the sum of the unlisted elements relative
+// to the lane maximum, the listing.
+template <int DT>
+__device__ __forceinline__ void chunk_phase2(const ScanArgs &a, int row, int wl, int cb, float cmax, float (&xr)[EPL],
+                                              Lane &ln) {
+  using L = Lay<DT>;
+  const int l = lane_id();
+  const float mnew = fmaxf(ln.m, cmax);
+  if (ln.woff > (uint32_t)(CAPW / 2)) ln.kap = max(ln.kap, wave_kth_largest_u16(fkey(mnew) >> 16, KV) << 16);
+  const float tauf = fkey_inv(ln.kap);
+  if (mnew > ln.m && ln.m > -INFINITY) {  // rescale the lane's sum to its new maximum (fp64)
+    const double f = exp((double)ln.m - (double)mnew);
+    ln.s *= f;
+    ln.b *= f;
+  }
+  ln.m = mnew;
+  const bool dosum = fabsf(mnew) < INFINITY;
+  double s64 = 0.0;
+  float mom = 0.0f;
+  uint32_t woff = ln.woff;
+  uint64_t *cl = a.cand + ((size_t)row * a.nparts * PWAVES + wl) * CAPW;
+#pragma unroll
+  for (int v = 0; v < L::NV; ++v) {
+    float ev[L::VEC];
+#pragma unroll
+    for (int k = 0; k < L::VEC; ++k) {
+      const int i = v * L::VEC + k;
+      const float z = xr[i];
+      const bool p = z >= tauf;
+      float e = 0.0f;
+      if (dosum) {  // -inf (masked) gives t = -inf, e = 0, and 0 * 1e4 in the moment; NaN rows are bad anyway
+        const float t = (z - mnew) * LOG2E;
+        const float ex = __builtin_amdgcn_exp2f(t);
+        e = p ? 0.0f : ex;
+        mom = fmaf(e, fminf(-t, 1.0e4f), mom);
+      }
+      ev[k] = e;
+      const uint64_t bl = ballot64(p);
+      if (bl) {
+        if (p) {
+          const uint32_t pos = woff + lanes_below(bl);
+          const int t = cb + v * L::STRIDE + l * L::VEC + k;
+          if (pos < (uint32_t)CAPW) st_ag(&cl[pos], pack(fkey(z), (uint32_t)t));
+        }
+        woff += (uint32_t)__popcll(bl);
+      }
+    }
+    // fixed pairwise order inside the vector, fp64 across vectors
+    if constexpr (L::VEC == 4) {
+      s64 += (double)((ev[0] + ev[1]) + (ev[2] + ev[3]));
+    } else {
+      s64 += (double)(((ev[0] + ev[1]) + (ev[2] + ev[3])) + ((ev[4] + ev[5]) + (ev[6] + ev[7])));
+    }
+  }
+  ln.woff = woff;
+  // error bound: v_exp_f32 (2 ulp), the argument's three roundings (2.6 ulp of |t|, times ln 2), two fp32 pairwise
+  // additions; flushed subnormal results
+  ln.s += s64;
+  ln.b += s64 * 4.2e-7 + (double)mom * 1.12e-7 + 1e-36;
+}
+
+// One part [p0, p1) of the row. Returns true in the workgroup that finished the row last (it then resolves the row).
+template <int DT, bool AL>
+__device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, const RowCtx &c, int row, int part,
+                                          Shared &sh) {
+  using L = Lay<DT>;
+  const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
+  const int p0 = part * a.plen, p1 = min(a.V, p0 + a.plen);
+  const int nck = (p1 - p0 + CHK - 1) / CHK;
+  const bool listing = !c.greedy || nlp_of(a, P) > 0;  // candidates and the softmax sum are needed
+  const int wl = part * PWAVES + w;                     // this wave's list
+
+  // History ids first, then the wave's first chunk: the history tables build while the logits stream in.
   int hid[HPT];
   if (c.pen) {
 #pragma unroll
@@ -591,199 +833,116 @@ __device__ __forceinline__ bool slice_body(const ScanArgs &a, const gse_row &P, 
       hid[k] = j < c.he ? a.hist[j] : -1;
     }
   }
-  float xr[EPT];
-  load_slice<DT, FULL>(c, c0, xr);
-  uint32_t mw[L::NV];
-#pragma unroll
-  for (int v = 0; v < L::NV; ++v) {
-    const int t0 = c0 + v * L::STRIDE + tid * L::VEC;
-    mw[v] = c.mw ? ((FULL || t0 < c.V) ? c.mw[t0 >> 5] : 0u) : 0xFFFFFFFFu;
-  }
+  float xa[EPL], xb[EPL];
+  uint32_t ma[L::NV], mb[L::NV];
+  int ck = w;  // chunks 0..3 go to waves 0..3; later ones from the LDS counter
+  if (ck < nck) load_chunk<DT, AL>(c, p0 + ck * CHK, p1, xa, ma);
   if (tid == 0) {
-    sh.minid = 0xFFFFFFFFu;
-    sh.ncand = 0;
+    sh.next = NWV;
+    sh.hover = 0;
   }
-  const bool hover = c.pen ? build_counts16(c, a.hist, hid, c0, sh) : false;
-  float *proc = a.processed ? a.processed + (int64_t)row * a.processed_ld : nullptr;
+  if (c.pen) build_history(c, a.hist, hid, p0, p1, sh);
+  else __syncthreads();
 
-  // Phase 1: penalties, NaN test (before the mask), mask, z; lane maximum and flags.
-  bool fnan = false, ffin = false;
-  float zmax = -INFINITY;
+  Lane ln;
+  ln.m = -INFINITY;
+  ln.s = 0.0;
+  ln.b = 0.0;
+  ln.kap = 0;
+  ln.woff = 0;
+  ln.g = -INFINITY;
+  ln.gid = 0xFFFFFFFFu;
+  ln.fid = 0xFFFFFFFFu;
+  ln.fnan = false;
+  ln.ffin = false;
+  auto grab = [&]() -> int {
+    uint32_t n = 0;
+    if (lane == 0) n = atomicAdd(&sh.next, 1u);
+    return __shfl((int)n, 0, WAVE);
+  };
+  // First chunk of each wave, phase 1; the part's listing threshold from the 256 lane maxima.
+  float cmax = -INFINITY;
+  if (ck < nck) cmax = chunk_phase1<DT>(a, c, row, p0 + ck * CHK, p0, p1, xa, ma, ln, sh);
+  if (listing) {
+    sh.lmax[tid] = fkey(cmax) >> 16;
+    __syncthreads();
+    // the rank scales with the lanes that saw a z > -inf (a sparse mask leaves most lanes without one)
+    uint32_t act = 0;
 #pragma unroll
-  for (int v = 0; v < L::NV; ++v) {
-    const int t0 = c0 + v * L::STRIDE + tid * L::VEC;
-    uint32_t bits = (mw[v] >> ((tid * L::VEC) & 31)) & VMASK;
-    if (!FULL) bits &= t0 >= c.V ? 0u : (c.V - t0 >= L::VEC ? VMASK : (1u << (c.V - t0)) - 1u);  // past the row end
-    uint32_t cw[L::VEC / 2];
-    bool anycnt = false;
-    if (c.pen) {
-      const int o = (v * L::STRIDE + tid * L::VEC) >> 1;
-      if constexpr (L::VEC == 4) {
-        const uint2 q = *reinterpret_cast<const uint2 *>(&sh.cnt[o]);
-        cw[0] = q.x;
-        cw[1] = q.y;
-      } else {
-        const uint4 q = *reinterpret_cast<const uint4 *>(&sh.cnt[o]);
-        cw[0] = q.x;
-        cw[1] = q.y;
-        cw[2] = q.z;
-        cw[3] = q.w;
-      }
+    for (int q = 0; q < NWV; ++q) act += (uint32_t)__popcll(ballot64(sh.lmax[q * WAVE + lane] > (KEY_NEGINF >> 16)));
+    const uint32_t kp = max(1u, (KP * act + MT - 1) / MT);
+    uint32_t r = 0;
 #pragma unroll
-      for (int k = 0; k < L::VEC / 2; ++k) anycnt |= cw[k] != 0u;
+    for (int b = 15; b >= 0; --b) {
+      const uint32_t cand = r | (1u << b);
+      uint32_t cnt = 0;
+#pragma unroll
+      for (int q = 0; q < NWV; ++q) cnt += (uint32_t)__popcll(ballot64(sh.lmax[q * WAVE + lane] >= cand));
+      if (cnt >= kp) r = cand;
     }
-    if (anycnt) {
-#pragma unroll
-      for (int k = 0; k < L::VEC; ++k) {
-        const uint32_t ct = (cw[k >> 1] >> ((k & 1) * 16)) & 0xFFFFu;
-        if (ct) xr[v * L::VEC + k] = penalize(xr[v * L::VEC + k], ct, c.rp, c.fp, c.pp);
-      }
-    }
-    if (bits == VMASK) {  // every token of the vector allowed
-#pragma unroll
-      for (int k = 0; k < L::VEC; ++k) {
-        const int i = v * L::VEC + k;
-        const float x = xr[i];
-        fnan |= (x != x);
-        ffin |= fabsf(x) < INFINITY;
-        if (proc) proc[t0 + k] = x;
-        const float z = divide ? div_exact(x, Rd) : x;
-        xr[i] = z;
-        zmax = fmaxf(zmax, z);
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < L::VEC; ++k) {
-        const int i = v * L::VEC + k;
-        const float x = xr[i];
-        fnan |= (x != x);  // (a token past the row end loads 0)
-        const bool al = (bits >> k) & 1u;
-        const float xm = al ? x : -INFINITY;
-        ffin |= fabsf(xm) < INFINITY;
-        if (proc && (FULL || t0 + k < c.V)) proc[t0 + k] = xm;
-        const float z = (divide && al) ? div_exact(x, Rd) : xm;
-        xr[i] = z;
-        zmax = fmaxf(zmax, z);
-      }
-    }
+    ln.kap = max(r << 16, KEY_NEGINF + 1u);
+  }
+  bool first = true;
+  while (ck < nck) {
+    const int cn = grab();
+    if (cn < nck) load_chunk<DT, AL>(c, p0 + cn * CHK, p1, xb, mb);
+    if (!first) cmax = chunk_phase1<DT>(a, c, row, p0 + ck * CHK, p0, p1, xa, ma, ln, sh);
+    first = false;
+    if (listing) chunk_phase2<DT>(a, row, wl, p0 + ck * CHK, cmax, xa, ln);
+    if (cn >= nck) break;
+    const int cn2 = grab();
+    if (cn2 < nck) load_chunk<DT, AL>(c, p0 + cn2 * CHK, p1, xa, ma);
+    cmax = chunk_phase1<DT>(a, c, row, p0 + cn * CHK, p0, p1, xb, mb, ln, sh);
+    if (listing) chunk_phase2<DT>(a, row, wl, p0 + cn * CHK, cmax, xb, ln);
+    ck = cn2;
   }
 
-  // Wave reductions: maximum, flags, the wave's candidate threshold (16th largest lane maximum, to 16 key bits).
-  const float wmx = wave_max_f32(zmax);
-  const uint64_t bn = ballot64(fnan), bf = ballot64(ffin);
-  uint32_t tau = 0;
-  if (listing) tau = wave_kth_largest_u16(fkey(zmax) >> 16, KW) << 16;
+  // Part record: the part maximum, then every lane's sum rescaled to it (fp64, fixed order).
+  const float wm = wave_max_f32(ln.m);
+  const uint64_t bn = ballot64(ln.fnan), bf = ballot64(ln.ffin);
+  uint64_t top;
+  if (c.greedy) {
+    top = ln.gid != 0xFFFFFFFFu ? pack(fkey(ln.g), ln.gid) : 0ull;
+  } else {
+    top = ln.fid != 0xFFFFFFFFu ? pack(KEY_NEGINF, ln.fid) : 0ull;
+  }
+  top = wave_max_u64(top);
   if (lane == 0) {
-    sh.wmax[w] = wmx;
+    sh.wmax[w] = wm;
     sh.wflags[w] = (bn ? F_NAN : 0u) | (bf ? F_FINITE : 0u);
-    sh.wtau[w] = tau;
+    sh.wtop[w] = top;
+    sh.wkap[w] = ln.kap;
+    sh.wcnt[w] = ln.woff;
   }
   __syncthreads();
-  float zw = sh.wmax[0];
-  uint32_t flags = sh.wflags[0];
-  tau = sh.wtau[0];
+  float M = sh.wmax[0];
 #pragma unroll
-  for (int k = 1; k < NWV; ++k) {
-    zw = fmaxf(zw, sh.wmax[k]);
-    flags |= sh.wflags[k];
-    tau = max(tau, sh.wtau[k]);
+  for (int k = 1; k < NWV; ++k) M = fmaxf(M, sh.wmax[k]);
+  double s = 0.0, b = 0.0;
+  if (ln.m > -INFINITY && fabsf(M) < INFINITY) {
+    const double f = exp((double)ln.m - (double)M);
+    s = ln.s * f;
+    b = ln.b * f;
   }
-  const bool badrow = (flags & F_NAN) != 0;
-
-  // Lowest id holding the slice maximum: greedy rows (of nan_to_num(x), sampling.py:76), and slices without z > -inf
-  // (of -inf: the row may have nothing else). Sampled rows otherwise take it from their listed elements.
-  const bool want_id = c.greedy || !(zw > -INFINITY);
-  if (want_id) {
-    const float target = c.greedy ? fminf(fmaxf(zw, -FLTMAX), FLTMAX) : zw;
-    uint32_t best = 0xFFFFFFFFu;
-#pragma unroll
-    for (int i = EPT - 1; i >= 0; --i) {
-      const float g = c.greedy ? fminf(fmaxf(xr[i], -FLTMAX), FLTMAX) : xr[i];
-      const int t = c0 + (i / L::VEC) * L::STRIDE + tid * L::VEC + (i % L::VEC);
-      if (g == target && (FULL || t < c.V) && xr[i] == xr[i]) best = (uint32_t)t;  // NaN: bad row anyway
-    }
-    best = wave_min_u32(best);
-    if (lane == 0 && best != 0xFFFFFFFFu) atomicMin(&sh.minid, best);
-  }
-
-  // Phase 2: listing and the softmax sum of the unlisted elements.
-  const uint32_t kap = max(tau, KEY_NEGINF + 1u);
-  const float tauf = fkey_inv(kap);
-  double s64 = 0.0;
-  float mom = 0.0f;
-  uint32_t ncl = 0;
-  if (listing && !badrow) {
-    const bool dosum = fabsf(zw) < INFINITY;
-#pragma unroll
-    for (int v = 0; v < L::NV; ++v) {
-      float ev[L::VEC];
-#pragma unroll
-      for (int k = 0; k < L::VEC; ++k) {
-        const float z = xr[v * L::VEC + k];
-        const bool p = z >= tauf;
-        ncl += p ? 1u : 0u;
-        float e = 0.0f;
-        if (dosum) {  // -inf (masked) gives t = -inf, e = 0, and 0 * 1e4 in the moment
-          const float t = (z - zw) * LOG2E;
-          const float ex = __builtin_amdgcn_exp2f(t);
-          e = p ? 0.0f : ex;
-          mom = fmaf(e, fminf(-t, 1.0e4f), mom);
-        }
-        ev[k] = e;
-      }
-      // fixed pairwise order inside the vector, fp64 across vectors
-      if constexpr (L::VEC == 4) {
-        s64 += (double)((ev[0] + ev[1]) + (ev[2] + ev[3]));
-      } else {
-        s64 += (double)(((ev[0] + ev[1]) + (ev[2] + ev[3])) + ((ev[4] + ev[5]) + (ev[6] + ev[7])));
-      }
-    }
-  }
-  // Candidate positions: wave prefix of the lane counts, one LDS atomic per wave.
-  const uint32_t off = wave_incl_scan_u32(ncl) - ncl;
-  const uint32_t wtot = (uint32_t)__shfl((int)(off + ncl), WAVE - 1, WAVE);
-  uint32_t base = 0;
-  if (lane == 0 && wtot) base = atomicAdd(&sh.ncand, wtot);
-  base = (uint32_t)__shfl((int)base, 0, WAVE);
-  uint64_t *cl = a.cand + ((size_t)row * a.nch + sl) * CAPC;
-  if (ncl) {
-    uint32_t pos = base + off;
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-      const float z = xr[i];
-      if (z >= tauf) {
-        const int t = c0 + (i / L::VEC) * L::STRIDE + tid * L::VEC + (i % L::VEC);
-        if (pos < (uint32_t)CAPC) st_ag(&cl[pos], pack(fkey(z), (uint32_t)t));
-        ++pos;
-      }
-    }
-  }
-  // error bound of the unlisted sum: v_exp_f32 (2 ulp), the argument's three roundings (2.6 ulp of |t|, times ln 2),
-  // two fp32 pairwise additions; flushed subnormal results
-  const double bnd = s64 * 4.2e-7 + (double)mom * 1.12e-7 + 1e-36;
-  const double sw = wave_sum_f64(s64), bw = wave_sum_f64(bnd);
-  if (lane == 0) {
-    sh.wred[w] = sw;
-    sh.wred2[w] = bw;
-  }
-  __syncthreads();
+  s = block_sum_f64(s, sh.wred);
+  b = block_sum_f64(b, sh.wred);
   if (tid == 0) {
-    double s = 0.0, b = 0.0;
+    uint32_t flags = sh.hover ? F_OVERFLOW : 0u, kap = 0;
+    uint64_t t = 0;
 #pragma unroll
     for (int k = 0; k < NWV; ++k) {
-      s += sh.wred[k];
-      b += sh.wred2[k];
+      flags |= sh.wflags[k];
+      t = sh.wtop[k] > t ? sh.wtop[k] : t;
+      kap = max(kap, sh.wkap[k]);
+      if (sh.wcnt[k] > (uint32_t)CAPW) flags |= F_OVERFLOW;
     }
-    const uint32_t nc = sh.ncand;
-    const bool over = nc > (uint32_t)CAPC || hover;
-    const uint32_t mkey = fkey(zw);
-    const uint32_t topkey = c.greedy ? fkey(fminf(fmaxf(zw, -FLTMAX), FLTMAX)) : mkey;
-    SliceRec *r = a.rec + (size_t)row * a.nch + sl;
-    st_ag(&r->top, (want_id && sh.minid != 0xFFFFFFFFu) ? pack(topkey, sh.minid) : (uint64_t)0);
+    SliceRec *r = a.rec + (size_t)row * a.nparts + part;
+    st_ag(&r->top, t);
     st_ag(&r->kappa, listing ? kap : 0u);
-    st_ag(&r->ncand, min(nc, (uint32_t)CAPC));
-    st_ag(&r->flags, flags | (over ? F_OVERFLOW : 0u));
-    st_ag(&r->mkey, mkey);
+    st_ag(&r->flags, flags);
+    st_ag(&r->mkey, fkey(M));
+#pragma unroll
+    for (int k = 0; k < NWV; ++k) st_ag(&r->wcnt[k], min(sh.wcnt[k], (uint32_t)CAPW));
     st_ag(&r->s, s);
     st_ag(&r->bnd, b);
   }
@@ -792,28 +951,28 @@ __device__ __forceinline__ bool slice_body(const ScanArgs &a, const gse_row &P, 
   __syncthreads();
   if (tid == 0) sh.ticket = ticket_add(&a.done[row]);
   __syncthreads();
-  return sh.ticket == (uint32_t)(a.nch - 1);
+  return sh.ticket == (uint32_t)(a.nparts - 1);
 }
 
+// Four waves per SIMD: every workgroup of a 256-row batch is resident at once (4 per CU).
 template <int DT>
-__global__ __launch_bounds__(MT) void main_kernel(ScanArgs a) {
+__global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void main_kernel(ScanArgs a) {
   __shared__ Shared sh;
   const int L = blockIdx.x;
-  int row, sl;
-  if (a.xcd_map) {  // the slices of a row on one XCD (workgroups go round-robin over the 8 XCDs): shared L2
+  int row, part;
+  if (a.xcd_map) {  // the parts of a row on one XCD (workgroups go round-robin over the 8 XCDs): shared L2
     const int x = L & 7, i = L >> 3;
-    row = x + 8 * (i / a.nch);
-    sl = i % a.nch;
+    row = x + 8 * (i / a.nparts);
+    part = i % a.nparts;
   } else {
-    row = L / a.nch;
-    sl = L % a.nch;
+    row = L / a.nparts;
+    part = L % a.nparts;
   }
   if (row >= a.rows) return;
   const gse_row P = a.params[row];
   const RowCtx c = make_ctx(a, row, P);
   const bool aligned = (((uintptr_t)c.base) & 15u) == 0;
-  const bool last = (aligned && (sl + 1) * CH <= a.V) ? slice_body<DT, true>(a, P, c, row, sl, sh)
-                                                        : slice_body<DT, false>(a, P, c, row, sl, sh);
+  const bool last = aligned ? part_body<DT, true>(a, P, c, row, part, sh) : part_body<DT, false>(a, P, c, row, part, sh);
   if (!last) return;
   resolve_row(a, row, P, sh);
   if (threadIdx.x == 0) a.done[row] = 0u;
@@ -823,7 +982,7 @@ __global__ __launch_bounds__(MT) void main_kernel(ScanArgs a) {
 
 hipError_t launch_main(const ScanArgs &a, hipStream_t s) {
   const int rows = a.xcd_map ? (a.rows + 7) / 8 * 8 : a.rows;
-  dim3 grid((unsigned)(rows * a.nch)), block(MT);
+  dim3 grid((unsigned)(rows * a.nparts)), block(MT);
   if (a.dtype == GSE_BF16) {
     hipLaunchKernelGGL(main_kernel<GSE_BF16>, grid, block, 0, s, a);
   } else {
