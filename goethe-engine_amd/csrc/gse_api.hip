@@ -18,7 +18,11 @@ struct gse_handle {
   uint64_t *cand = nullptr;
   gse::RowInfo *info = nullptr;
   uint32_t *done = nullptr;
-  hipEvent_t (*ring)[4] = nullptr;  // kernel boundaries of up to GSE_PROFILE_CALLS profiled calls
+  uint32_t *dctl = nullptr;           // split-row finish: control word, slots, histograms, parts, window lists
+  gse::DeepSlot *dslot = nullptr;
+  uint64_t *dhist = nullptr;
+  uint64_t *dlist = nullptr;
+  hipEvent_t (*ring)[5] = nullptr;  // kernel boundaries of up to GSE_PROFILE_CALLS profiled calls
   int nring = 0;                    // calls recorded
   int nprof = 0;                    // kernels per recorded call
   std::string err;
@@ -71,10 +75,10 @@ struct DeviceGuard {
 int prof_slot(gse_handle *h, int kernels, hipEvent_t **ev) {
   *ev = nullptr;
   if (!h->ring) {
-    h->ring = new (std::nothrow) hipEvent_t[GSE_PROFILE_CALLS][4];
+    h->ring = new (std::nothrow) hipEvent_t[GSE_PROFILE_CALLS][5];
     if (!h->ring) return fail(h, GSE_E_DEVICE, "out of host memory");
     for (int c = 0; c < GSE_PROFILE_CALLS; ++c)
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 5; ++i) {
         hipError_t e = hipEventCreate(&h->ring[c][i]);
         if (e != hipSuccess) return hip_fail(h, e, "event create");
       }
@@ -114,6 +118,21 @@ void parts(const gse_handle *h, uint32_t rows, uint32_t vocab, int *nparts, int 
   *nparts = (int)((vocab + len - 1) / len);
 }
 
+// Slices of a deep row for the split-row finish: at most DSMAX of them, each a multiple of PCHUNK long and at most PTOK
+// (a vocabulary too long for that leaves deep rows to the exact path).
+void deep_slices(const gse_handle *h, uint32_t rows, uint32_t vocab, int *nsl, int *len, int *grid) {
+  uint32_t l = ((vocab + gse::DSMAX - 1) / gse::DSMAX + gse::PCHUNK - 1) / gse::PCHUNK * gse::PCHUNK;
+  if (l > (uint32_t)gse::PTOK) {
+    *nsl = *len = *grid = 0;
+    return;
+  }
+  *len = (int)l;
+  *nsl = (int)((vocab + l - 1) / l);
+  const uint32_t slots = rows < (uint32_t)gse::DEEP_MAX ? rows : (uint32_t)gse::DEEP_MAX;
+  const uint32_t items = (slots + 7) / 8 * 8 * (uint32_t)*nsl;
+  *grid = (int)(items < h->target ? items : h->target);
+}
+
 gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   gse::ScanArgs a = {};
   a.logits = b.logits;
@@ -135,6 +154,11 @@ gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   a.cand = h->cand;
   a.info = h->info;
   a.done = h->done;
+  a.dctl = h->dctl;
+  a.dslot = h->dslot;
+  a.dhist = h->dhist;
+  a.dlist = h->dlist;
+  deep_slices(h, b.rows, b.vocab, &a.dslices, &a.dlen, &a.dgrid);
   return a;
 }
 
@@ -174,6 +198,12 @@ GSE_API int gse_open(const gse_open_params *p, gse_handle **out) {
       (e = hipMalloc(&h->done, (size_t)h->max_rows * sizeof(uint32_t))) != hipSuccess ||
       (e = hipMemset(h->done, 0, (size_t)h->max_rows * sizeof(uint32_t))) != hipSuccess ||
       (e = hipMemset(h->info, 0, (size_t)h->max_rows * sizeof(gse::RowInfo))) != hipSuccess ||
+      (e = hipMalloc(&h->dctl, 64)) != hipSuccess || (e = hipMemset(h->dctl, 0, 64)) != hipSuccess ||
+      (e = hipMalloc(&h->dslot, gse::DEEP_MAX * sizeof(gse::DeepSlot))) != hipSuccess ||
+      (e = hipMemset(h->dslot, 0, gse::DEEP_MAX * sizeof(gse::DeepSlot))) != hipSuccess ||
+      (e = hipMalloc(&h->dhist, (size_t)gse::DEEP_MAX * 2 * gse::DNB * sizeof(uint64_t))) != hipSuccess ||
+      (e = hipMemset(h->dhist, 0, (size_t)gse::DEEP_MAX * 2 * gse::DNB * sizeof(uint64_t))) != hipSuccess ||
+      (e = hipMalloc(&h->dlist, (size_t)gse::DEEP_MAX * gse::DCAP * sizeof(uint64_t))) != hipSuccess ||
       (e = hipDeviceSynchronize()) != hipSuccess) {
     fail(nullptr, GSE_E_DEVICE, "workspace allocation (%u part records): %s", h->nrec, hipGetErrorString(e));
     gse_close(h);
@@ -207,13 +237,15 @@ GSE_API int gse_sample(gse_handle *h, const gse_batch *in, const gse_out *out) {
   a.lp_ld = o.logprobs_ld;
   hipStream_t s = (hipStream_t)b.stream;
   hipEvent_t *ev = nullptr;
-  if ((b.flags & GSE_BATCH_PROFILE) && (rc = prof_slot(h, 2, &ev)) != GSE_OK) return rc;
+  if ((b.flags & GSE_BATCH_PROFILE) && (rc = prof_slot(h, 3, &ev)) != GSE_OK) return rc;
   hipError_t e;
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(h, e, "event record");
   if ((e = gse::launch_main(a, s)) != hipSuccess) return hip_fail(h, e, "main launch");
   if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return hip_fail(h, e, "event record");
-  if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
+  if (a.dgrid > 0 && (e = gse::launch_deep(a, s)) != hipSuccess) return hip_fail(h, e, "deep launch");
   if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return hip_fail(h, e, "event record");
+  if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
+  if (ev && (e = hipEventRecord(ev[3], s)) != hipSuccess) return hip_fail(h, e, "event record");
   return GSE_OK;
 }
 
@@ -229,15 +261,17 @@ GSE_API int gse_dist(gse_handle *h, const gse_batch *in, double *probs, int64_t 
   gse::ScanArgs a = make_args(h, b, gse::MODE_DIST);
   hipStream_t s = (hipStream_t)b.stream;
   hipEvent_t *ev = nullptr;
-  if ((b.flags & GSE_BATCH_PROFILE) && (rc = prof_slot(h, 3, &ev)) != GSE_OK) return rc;
+  if ((b.flags & GSE_BATCH_PROFILE) && (rc = prof_slot(h, 4, &ev)) != GSE_OK) return rc;
   hipError_t e;
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(h, e, "event record");
   if ((e = gse::launch_main(a, s)) != hipSuccess) return hip_fail(h, e, "main launch");
   if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return hip_fail(h, e, "event record");
-  if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
+  if (a.dgrid > 0 && (e = gse::launch_deep(a, s)) != hipSuccess) return hip_fail(h, e, "deep launch");
   if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return hip_fail(h, e, "event record");
-  if ((e = gse::launch_dist_write(a, probs, probs_ld, s)) != hipSuccess) return hip_fail(h, e, "dist launch");
+  if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
   if (ev && (e = hipEventRecord(ev[3], s)) != hipSuccess) return hip_fail(h, e, "event record");
+  if ((e = gse::launch_dist_write(a, probs, probs_ld, s)) != hipSuccess) return hip_fail(h, e, "dist launch");
+  if (ev && (e = hipEventRecord(ev[4], s)) != hipSuccess) return hip_fail(h, e, "event record");
   return GSE_OK;
 }
 
@@ -310,6 +344,10 @@ GSE_API void gse_close(gse_handle *h) {
     if (h->cand) (void)hipFree(h->cand);
     if (h->info) (void)hipFree(h->info);
     if (h->done) (void)hipFree(h->done);
+    if (h->dctl) (void)hipFree(h->dctl);
+    if (h->dslot) (void)hipFree(h->dslot);
+    if (h->dhist) (void)hipFree(h->dhist);
+    if (h->dlist) (void)hipFree(h->dlist);
     if (h->ring) {
       for (int c = 0; c < GSE_PROFILE_CALLS; ++c)
         for (int i = 0; i < 4; ++i)

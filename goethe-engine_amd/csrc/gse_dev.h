@@ -220,6 +220,25 @@ __device__ __forceinline__ void block_sort_desc_u64(uint64_t *a, int n_pow2) {
   }
 }
 
+// Fixed-point masses: an fp64 exp(z - M) in [0, 1] as hi * 2^-40 + lo * 2^-64 (both floors, so the value is within
+// 2^-64 below the fp64 one). Sums of up to 2^24 of them add hi and lo separately with no carry, so a sum is the same
+// whatever order its terms are added in.
+struct Fx {  // value = hi * 2^-40 + lo * 2^-64
+  uint64_t hi, lo;
+};
+__device__ __forceinline__ Fx fx_of(double e) {
+  const double s = e * 1099511627776.0;  // 2^40
+  const double h = floor(s);
+  Fx f;
+  f.hi = (uint64_t)h;
+  f.lo = (uint64_t)floor((s - h) * 16777216.0);  // 2^24
+  return f;
+}
+__device__ __forceinline__ Fx fx_add(Fx a, Fx b) { return Fx{a.hi + b.hi, a.lo + b.lo}; }
+__device__ __forceinline__ double fx_val(Fx a) {
+  return (double)a.hi * 9.094947017729282e-13 + (double)a.lo * 5.421010862427522e-20;  // 2^-40, 2^-64
+}
+
 __host__ __device__ constexpr int pow2_ceil(int n) {
   int p = 1;
   while (p < n) p <<= 1;

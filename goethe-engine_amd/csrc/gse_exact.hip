@@ -21,22 +21,6 @@ constexpr int NB = 4096;         // histogram bins
 constexpr int CAPS = 8192;       // collected elements
 constexpr int PER = CH / XT;     // tokens per thread per chunk (contiguous)
 
-struct Fx {  // value = hi * 2^-40 + lo * 2^-64
-  uint64_t hi, lo;
-};
-__device__ __forceinline__ Fx fx_of(double e) {
-  const double s = e * 1099511627776.0;  // 2^40
-  const double h = floor(s);
-  Fx f;
-  f.hi = (uint64_t)h;
-  f.lo = (uint64_t)floor((s - h) * 16777216.0);  // 2^24
-  return f;
-}
-__device__ __forceinline__ Fx fx_add(Fx a, Fx b) { return Fx{a.hi + b.hi, a.lo + b.lo}; }
-__device__ __forceinline__ double fx_val(Fx a) {
-  return (double)a.hi * 9.094947017729282e-13 + (double)a.lo * 5.421010862427522e-20;  // 2^-40, 2^-64
-}
-
 struct ExactShared {
   uint32_t cnt[CH];
   union {
@@ -487,6 +471,7 @@ __device__ uint32_t collect_top(const XCtx &x, ExactShared &sh, uint64_t pk) {
 __global__ __launch_bounds__(XT) void exact_kernel(ScanArgs a) {
   const int row = blockIdx.x;
   RowInfo *ri = a.info + row;
+  if (row == 0 && threadIdx.x == 0) a.dctl[0] = 0u;  // the deep rows of this call are finished
   if (!(ri->flags & R_HARD)) return;
   __shared__ ExactShared sh;
   const int tid = threadIdx.x;

@@ -12,7 +12,8 @@ static_assert(sizeof(gse_row) == 72, "gse_row layout is part of the ABI");
 enum : uint32_t {
   F_NAN = 1u,       // a NaN in the row after penalties (before the mask): the row is bad (sampling.py:71)
   F_FINITE = 2u,    // a finite value after the mask (sampling.py:75)
-  F_OVERFLOW = 4u,  // a slice's candidate list did not fit, or a history longer than the u16 counts allow
+  F_OVERFLOW = 4u,  // a wave's candidate list did not fit
+  F_HOVER = 8u,     // a part with more distinct history ids than its count table holds
 };
 
 enum : uint32_t {
@@ -22,6 +23,7 @@ enum : uint32_t {
   R_HARD = 8u,     // the exact path must finish the row
   R_DONE = 16u,
   R_FULL = 32u,    // with R_HARD: the exact path also recomputes the flags and the greedy argmax
+  R_DEEP = 64u,    // with R_HARD: the split-row finish (gse_deep.hip) takes the row first
 };
 
 enum { MODE_SAMPLE = 0, MODE_DIST = 1 };
@@ -46,6 +48,36 @@ struct SliceRec {    // 64 bytes
   uint32_t pad[2];
 };
 static_assert(sizeof(SliceRec) == 64, "");
+
+// Split-row finish of deep rows (gse_deep.hip).
+constexpr int DEEP_MAX = 128;  // deep rows per call (more: the exact path takes them)
+constexpr int DSMAX = 32;      // slices per deep row
+constexpr int DNB = 512;       // histogram bins of d = z_max - z, 1/32 wide (the last one open-ended)
+constexpr int DCAP = 2048;     // window elements listed per deep row
+
+enum : uint32_t { DS_PENDING = 0u, DS_PLANNED = 1u, DS_FAIL = 2u };
+
+enum {  // DeepSlot.acc: exact fixed-point sums of the pick pass (hi: 2^-40 units, lo: 2^-64 units) and counts
+  DA_X0HI, DA_X0LO,  // bins before the draw window
+  DA_X1HI, DA_X1LO,  // bins strictly between the two windows
+  DA_SHI, DA_SLO,    // every element (S)
+  DA_C0, DA_C1,      // element counts of those two regions
+  DA_C2,             // elements after the cut window
+  DA_N
+};
+
+struct DeepSlot {    // 256 bytes, one per deep row of a call
+  gse_row P;         // the row's parameters, copied by the row resolve of the main pass
+  int32_t row;
+  float M;           // maximum of z
+  double u;          // the draw's uniform
+  uint32_t status;   // DS_*, written by the planner
+  uint32_t w2lo, w2hi, w1lo, w1hi;  // bin windows holding the draw and the last kept element (inclusive)
+  uint32_t lcnt, pad0[2];           // listed window elements
+  uint64_t acc[DA_N];               // pick-pass sums (atomic adds; zero between calls)
+  uint64_t pad[8];
+};
+static_assert(sizeof(DeepSlot) == 256, "");
 
 struct RowInfo {    // 64 bytes, one per row, written by the row resolve, read by the exact path and dist
   uint64_t cmax;    // packed maximum z (key, id)
@@ -79,9 +111,16 @@ struct ScanArgs {
   uint64_t *cand;   // [rows][nparts][PWAVES][CAPW]
   RowInfo *info;
   uint32_t *done;   // [rows] slice tickets, zero between calls
+  // split-row finish
+  uint32_t *dctl;    // [0]: deep rows taken by this call (reset by the exact pass)
+  DeepSlot *dslot;   // [DEEP_MAX]
+  uint64_t *dhist;   // [DEEP_MAX][2][DNB]: per bin, element count and fixed-point mass (2^-40 units), atomic adds
+  uint64_t *dlist;   // [DEEP_MAX][DCAP]: packed keys of the window elements
+  int dslices, dlen, dgrid;  // slices per deep row, tokens per slice (a multiple of 1024), workgroups per pass
 };
 
 hipError_t launch_main(const ScanArgs &a, hipStream_t s);
+hipError_t launch_deep(const ScanArgs &a, hipStream_t s);
 hipError_t launch_exact(const ScanArgs &a, hipStream_t s);
 hipError_t launch_dist_write(const ScanArgs &a, double *probs, int64_t probs_ld, hipStream_t s);
 hipError_t launch_draw(const double *q, int64_t ld, int rows, int V, const double *u, int32_t *out, hipStream_t s);

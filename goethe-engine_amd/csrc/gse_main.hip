@@ -24,19 +24,14 @@
 // the draw. Top-k, min-p and the draw do not depend on S (they compare masses with masses); top-p uses the S bounds.
 // A decision inside the bound, a keep prefix that runs past the head, or an overflow marks the row hard: the exact
 // path (gse_exact.hip) finishes it.
-#include "gse_rowctx.h"
+#include "gse_stream.h"
 
 namespace gse {
 
 namespace {
 
-constexpr int MT = 256;                // threads per part workgroup
-constexpr int NWV = MT / WAVE;         // waves
-constexpr int EPL = 16;                // tokens per lane per chunk
-constexpr int CHK = WAVE * EPL;        // tokens per chunk
-constexpr int PMAX = PTOK;             // tokens per part, at most
-constexpr int PWORDS = PMAX / 32;      // history bitset words of a part
-constexpr int HMAX = 2048;             // distinct history ids of a part (more: the row takes the exact path)
+using namespace strm;
+
 constexpr int KP = 24;                 // rank, among the part's 256 first-chunk lane maxima, of its listing threshold
 constexpr int KV = 8;                  // rank, among a wave's running lane maxima, of its raised threshold (when its
                                        // list passes half its capacity)
@@ -44,32 +39,14 @@ constexpr int NH = 2048;               // certified head capacity of the row res
 constexpr int NSUB = 512;              // sorted sub-head capacity
 constexpr int SUBT = 256;              // sub-head target size
 constexpr int NSUB2 = 1024;            // the larger sorted top
-constexpr int HPT = 8;                 // history ids per thread per round
 constexpr int GPT = 8;                 // listed entries per thread per gather round
 constexpr int NSL = MAXP * PWAVES;     // wave lists of a row, at most (one per resolve thread)
-constexpr float LOG2E = 1.4426950408889634f;
-constexpr float FLTMAX = 3.402823466e+38f;
 static_assert(NWV == PWAVES, "");
 static_assert(NSL <= MT, "one wave list per resolve thread");
 
-template <int DT>
-struct Lay;
-template <>
-struct Lay<GSE_F32> {  // chunk base cb, lane l, vector v, element k: token cb + v * 256 + l * 4 + k
-  static constexpr int VEC = 4, NV = EPL / 4, STRIDE = WAVE * 4;
-};
-template <>
-struct Lay<GSE_BF16> {  // token cb + v * 512 + l * 8 + k
-  static constexpr int VEC = 8, NV = EPL / 8, STRIDE = WAVE * 8;
-};
-
 struct Shared {
   union {
-    struct {                   // history of the part's tokens: bitset, prefix popcounts, counts by rank
-      uint32_t bits[PWORDS];
-      uint32_t pre[PWORDS];
-      uint32_t cnt[HMAX];
-    } h;
+    HistTab h;                 // history of the part's tokens
     struct {
       uint64_t head[NH];       // listed elements at or above the certified key
       uint64_t sub[NSUB2];     // the top of the head
@@ -87,198 +64,9 @@ struct Shared {
   uint32_t loff[NSL];
   uint32_t bins[256];
   uint64_t rtop, rtopL;
-  uint32_t rflags, rkappa, rmkey, ltot, nh, ns, mfail_sure, mfail_maybe, jcount, bsel;
+  uint32_t rflags, rkappa, rmkey, ltot, nh, ns, mfail_sure, mfail_maybe, jcount, bsel, lpw;
   double rsc;
 };
-
-// z = RN32(x / T) as RN32(x * Rd), Rd = RN64(1 / T). |x * Rd - x / T| <= 2^-51 |x / T| (two fp64 roundings), while
-// x / T lies at least 2^-49 |x / T| from every fp32 rounding midpoint (x and T have 24-bit significands, so x - m T
-// for a midpoint m is a nonzero multiple of 2^-47 of the binade); the fp32 rounding of the fp64 product therefore
-// equals the correctly rounded quotient, subnormal and overflowing results included.
-__device__ __forceinline__ float div_exact(float x, double Rd) { return (float)((double)x * Rd); }
-
-__device__ __forceinline__ int nlp_of(const ScanArgs &a, const gse_row &P) {
-  return a.lp_ids ? min(min(P.logprobs, GSE_MAX_LOGPROBS), (int)a.lp_ld) : 0;
-}
-
-// The part's history [p0, p1): bitset of the tokens present, their prefix popcounts, and the count of each present
-// token indexed by its rank among them. hid holds this thread's first ids (loaded before the logits). Ends with a
-// barrier.
-__device__ __forceinline__ void build_history(const RowCtx &c, const int32_t *hist, const int (&hid)[HPT], int p0,
-                                              int p1, Shared &sh) {
-  const int tid = threadIdx.x;
-  const int nw = (p1 - p0 + 31) >> 5;
-  for (int i = tid; i < nw; i += MT) sh.h.bits[i] = 0;
-  __syncthreads();
-  auto each = [&](auto f) {
-#pragma unroll
-    for (int k = 0; k < HPT; ++k)
-      if (hid[k] >= p0 && hid[k] < p1) f(hid[k] - p0);
-    for (int j0 = c.hb + MT * HPT; j0 < c.he; j0 += MT * HPT) {
-      int more[HPT];
-#pragma unroll
-      for (int k = 0; k < HPT; ++k) {
-        const int j = j0 + k * MT + tid;
-        more[k] = j < c.he ? hist[j] : -1;
-      }
-#pragma unroll
-      for (int k = 0; k < HPT; ++k)
-        if (more[k] >= p0 && more[k] < p1) f(more[k] - p0);
-    }
-  };
-  each([&](int o) { atomicOr(&sh.h.bits[o >> 5], 1u << (o & 31)); });
-  __syncthreads();
-  // exclusive prefix of the word popcounts (words per thread contiguous)
-  const int per = (nw + MT - 1) / MT, w0 = tid * per;
-  uint32_t loc = 0;
-  for (int i = 0; i < per; ++i)
-    if (w0 + i < nw) loc += __popc(sh.h.bits[w0 + i]);
-  const uint32_t inc = wave_incl_scan_u32(loc);
-  if (lane_id() == WAVE - 1) sh.wcnt[tid >> 6] = inc;
-  __syncthreads();
-  uint32_t run = inc - loc, tot = 0;
-#pragma unroll
-  for (int w = 0; w < NWV; ++w) {
-    run += w < (tid >> 6) ? sh.wcnt[w] : 0u;
-    tot += sh.wcnt[w];
-  }
-  for (int i = 0; i < per; ++i)
-    if (w0 + i < nw) {
-      sh.h.pre[w0 + i] = run;
-      run += __popc(sh.h.bits[w0 + i]);
-    }
-  const uint32_t nd = min(tot, (uint32_t)HMAX);
-  for (uint32_t i = tid; i < nd; i += MT) sh.h.cnt[i] = 0;
-  if (tid == 0 && tot > (uint32_t)HMAX) sh.hover = 1;
-  __syncthreads();
-  each([&](int o) {
-    const uint32_t r = sh.h.pre[o >> 5] + __popc(sh.h.bits[o >> 5] & ((1u << (o & 31)) - 1u));
-    if (r < (uint32_t)HMAX) atomicAdd(&sh.h.cnt[r], 1u);
-  });
-  __syncthreads();
-}
-
-// One chunk's logits into registers (fp32, or bf16 widened exactly) and its packed mask words; AL: the row start is
-// 16-byte aligned, so a whole vector is one 16-byte load. A token past the part end loads 0.
-template <int DT, bool AL>
-__device__ __forceinline__ void load_chunk(const RowCtx &c, int cb, int p1, float (&x)[EPL],
-                                           uint32_t (&mw)[Lay<DT>::NV]) {
-  using L = Lay<DT>;
-  const int l = lane_id();
-#pragma unroll
-  for (int v = 0; v < L::NV; ++v) {
-    const int t0 = cb + v * L::STRIDE + l * L::VEC;
-    mw[v] = c.mw ? (t0 < p1 ? c.mw[t0 >> 5] : 0u) : 0xFFFFFFFFu;
-  }
-  if constexpr (DT == GSE_F32) {
-    const float *p = (const float *)c.base + cb + l * 4;
-#pragma unroll
-    for (int v = 0; v < L::NV; ++v) {
-      const int t0 = cb + v * L::STRIDE + l * 4;
-      if (AL && t0 + 4 <= p1) {
-        const float4 f = *reinterpret_cast<const float4 *>(p + v * L::STRIDE);
-        x[4 * v] = f.x;
-        x[4 * v + 1] = f.y;
-        x[4 * v + 2] = f.z;
-        x[4 * v + 3] = f.w;
-      } else {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) x[4 * v + k] = t0 + k < p1 ? p[v * L::STRIDE + k] : 0.0f;
-      }
-    }
-  } else {
-    const uint16_t *p = (const uint16_t *)c.base + cb + l * 8;
-#pragma unroll
-    for (int v = 0; v < L::NV; ++v) {
-      const int t0 = cb + v * L::STRIDE + l * 8;
-      if (AL && t0 + 8 <= p1) {
-        const uint4 u = *reinterpret_cast<const uint4 *>(p + v * L::STRIDE);
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          x[8 * v + 2 * i] = __uint_as_float(w[i] << 16);
-          x[8 * v + 2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
-        }
-      } else {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) x[8 * v + k] = t0 + k < p1 ? bf16_to_f32(p[v * L::STRIDE + k]) : 0.0f;
-      }
-    }
-  }
-}
-
-// Block-wide sums over MT threads in a fixed order (wave trees, then waves in order): deterministic.
-__device__ __forceinline__ double block_sum_f64(double v, double *red) {
-  v = wave_sum_f64(v);
-  __syncthreads();
-  if (lane_id() == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  double r = 0.0;
-#pragma unroll
-  for (int w = 0; w < NWV; ++w) r += red[w];
-  __syncthreads();
-  return r;
-}
-
-// Exclusive prefix over MT threads in thread order.
-__device__ __forceinline__ double block_excl_scan_f64(double v, double *red) {
-  const double inc = wave_incl_scan_f64(v);
-  __syncthreads();
-  if (lane_id() == WAVE - 1) red[threadIdx.x >> 6] = inc;
-  __syncthreads();
-  double pre = 0.0;
-  const int w = threadIdx.x >> 6;
-  for (int k = 0; k < w; ++k) pre += red[k];
-  __syncthreads();
-  return pre + inc - v;
-}
-
-// Descending bitonic sort of MT * S packed keys held S per thread (element i = tid * S + s). Pairs closer than S are
-// in one thread, closer than WAVE * S in one wave (lane shuffles); only the three widest steps go through LDS (buf,
-// MT * S entries), each between two barriers.
-template <int S>
-__device__ __forceinline__ void sort_regs(uint64_t (&v)[S], uint64_t *buf) {
-  constexpr int N = MT * S;
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int k = 2; k <= N; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      if (j < S) {
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          if ((s ^ j) > s) {
-            const bool desc = ((tid * S + s) & k) == 0;
-            const uint64_t x = v[s], y = v[s ^ j];
-            if (desc ? (x < y) : (x > y)) {
-              v[s] = y;
-              v[s ^ j] = x;
-            }
-          }
-        }
-      } else {
-        uint64_t o[S];
-        if (j < WAVE * S) {
-#pragma unroll
-          for (int s = 0; s < S; ++s) o[s] = shfl_xor_u64(v[s], j / S);
-        } else {
-#pragma unroll
-          for (int s = 0; s < S; ++s) buf[tid * S + s] = v[s];
-          __syncthreads();
-#pragma unroll
-          for (int s = 0; s < S; ++s) o[s] = buf[(tid * S + s) ^ j];
-          __syncthreads();
-        }
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          const int i = tid * S + s;
-          const bool keep_max = (((i & k) == 0) == ((i & j) == 0));  // lower of a descending pair, upper of an ascending
-          v[s] = keep_max ? (o[s] > v[s] ? o[s] : v[s]) : (o[s] < v[s] ? o[s] : v[s]);
-        }
-      }
-    }
-  }
-}
 
 __device__ __forceinline__ void lp_invalid(const ScanArgs &a, int row, int nlp) {
   for (int i = threadIdx.x; i < nlp; i += MT) {
@@ -348,6 +136,7 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, uint64_t *arr, int ns
   }
   const double base = block_excl_scan_f64(loc, sh.wred);  // (its barriers publish arr and the resets above)
   if (ev.nlp > 0) {
+    if (tid == 0) sh.lpw = 1;
     const double lS = log(Sm);
     for (int i = tid; i < ev.nlp; i += MT) {
       const uint64_t pk = arr[i];
@@ -482,6 +271,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
     sh.rmkey = 0;
     sh.nh = 0;
     sh.ns = 0;
+    sh.lpw = 0;
   }
   // One round of record loads: thread j holds wave list j (part j / 4), threads j % 4 == 0 the part's record.
   const int prt = tid / PWAVES;
@@ -527,7 +317,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   const uint64_t gtop = sh.rtop;  // greedy argmax; or, for a row without z > -inf, the lowest id of its -inf
   const bool bad = (flags & F_NAN) || !(flags & F_FINITE);
 
-  if ((flags & F_OVERFLOW) && (greedy || bad)) {
+  if ((flags & F_HOVER) && (greedy || bad)) {
     // more distinct history ids than a part can count: the exact path redoes the whole row (flags, argmax, logprobs)
     if (tid == 0) set_info(ri, gtop, 0, 0.0, 0.0, R_HARD | R_FULL | (greedy ? R_GREEDY : 0u), -1);
     return;
@@ -602,7 +392,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
     // z holds +inf: every +inf element is listed; token = the lowest id among them (sampling.py:82, order[0])
     __syncthreads();
     const uint64_t t = sh.rtopL;
-    const bool hard = (flags & F_OVERFLOW) || a.force_exact;
+    const bool hard = (flags & (F_OVERFLOW | F_HOVER)) || a.force_exact;
     if (tid == 0) {
       if (hard) {
         set_info(ri, t, 0, 0.0, 0.0, R_HARD | (greedy ? R_GREEDY : 0u), -1);
@@ -632,7 +422,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   ev.n = (int)min(nh_all, (uint32_t)NH);
   const int n = ev.n;
   int st = EV_HARD;
-  if (!((flags & F_OVERFLOW) || nh_all > (uint32_t)NH || a.force_exact)) {
+  if (!((flags & (F_OVERFLOW | F_HOVER)) || nh_all > (uint32_t)NH || a.force_exact)) {
     if (n <= NSUB) {
       st = evaluate<NSUB / MT>(ev, sh.r.head, n, sh);
     } else {
@@ -647,110 +437,35 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
       }
     }
   }
-  if (st != EV_DONE && tid == 0) {
-    // the exact path finishes the row (for a greedy row: its logprobs; the token is already written)
-    set_info(ri, gtop, 0, ev.S, 0.0, R_HARD | (greedy ? R_GREEDY : 0u), greedy ? (int32_t)pk_id(gtop) : -1);
+  if (st != EV_DONE) {
+    __syncthreads();  // (sh.lpw)
+    if (tid == 0) {
+      // The exact path finishes the row (for a greedy row: its logprobs; the token is already written). A sampled row
+      // whose logprobs are written and whose part lists all fit goes to the split-row finish first.
+      uint32_t fl = R_HARD | (greedy ? R_GREEDY : 0u);
+      // (the split-row finish recomputes z and every mass itself: overflowing wave lists do not matter to it)
+      const bool deep = a.dslices > 0 && !greedy && !(flags & F_HOVER) && !a.force_exact && (nlp == 0 || sh.lpw);
+      if (deep) {
+        const uint32_t slot = atomicAdd(a.dctl, 1u);
+        if (slot < (uint32_t)DEEP_MAX) {
+          DeepSlot *ds = a.dslot + slot;
+          ds->P = P;
+          ds->row = row;
+          ds->M = M;
+          ds->u = a.mode == MODE_SAMPLE ? (a.uni ? a.uni[row] : uniform64(P.seed, P.idx)) : 0.0;
+          ds->status = DS_PENDING;
+          fl |= R_DEEP;
+        }
+      }
+      // cmax: the greedy argmax, or the packed maximum of z (always listed) that the split-row finish reads
+      const uint64_t zmax = pk_key(sh.rtopL) == mk ? sh.rtopL : pack(mk, 0u);  // (a list overflow may drop it)
+      set_info(ri, greedy ? gtop : zmax, 0, ev.S, 0.0, fl, greedy ? (int32_t)pk_id(gtop) : -1);
+    }
   }
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
 // Part streaming.
-
-// Per-lane running state of a wave.
-struct Lane {
-  float m;         // running maximum of this lane's z
-  double s;        // sum of this lane's unlisted exp(z - m) (fp32 terms)
-  double b;        // its error bound
-  uint32_t kap;    // the wave's listing threshold key in force (uniform in the wave; only rises)
-  uint32_t woff;   // elements the wave has listed (uniform)
-  float g;         // greedy rows: largest nan_to_num(x) so far, at token gid (the first one)
-  uint32_t gid;
-  uint32_t fid;    // first token of this lane with z not NaN (the lowest -inf when the row has no z > -inf)
-  bool fnan, ffin;
-};
-
-// Phase 1 of a chunk: penalties, NaN test (before the mask), mask, z in place. Returns the lane's chunk maximum of z.
-template <int DT>
-__device__ __forceinline__ float chunk_phase1(const ScanArgs &a, const RowCtx &c, int row, int cb, int p0, int p1,
-                                              float (&xr)[EPL], const uint32_t (&mw)[Lay<DT>::NV], Lane &ln,
-                                              const Shared &sh) {
-  using L = Lay<DT>;
-  constexpr uint32_t VMASK = (1u << L::VEC) - 1u;
-  const int l = lane_id();
-  const bool divide = c.divide;
-  const double Rd = c.Rd;
-  float *proc = a.processed ? a.processed + (int64_t)row * a.processed_ld : nullptr;
-  float cmax = -INFINITY;
-#pragma unroll
-  for (int v = 0; v < L::NV; ++v) {
-    const int t0 = cb + v * L::STRIDE + l * L::VEC;
-    uint32_t bits = (mw[v] >> ((l * L::VEC) & 31)) & VMASK;
-    if (t0 + L::VEC > p1) bits &= t0 >= p1 ? 0u : (1u << (p1 - t0)) - 1u;  // past the part end
-    if (c.pen && t0 < p1) {
-      const int o = t0 - p0;
-      const uint32_t hw = sh.h.bits[o >> 5];
-      const uint32_t hb = (hw >> (o & 31)) & VMASK;
-      if (hb) {
-#pragma unroll
-        for (int k = 0; k < L::VEC; ++k) {
-          if ((hb >> k) & 1u) {
-            const int ok = o + k;
-            const uint32_t r = sh.h.pre[ok >> 5] + __popc(sh.h.bits[ok >> 5] & ((1u << (ok & 31)) - 1u));
-            xr[v * L::VEC + k] = penalize(xr[v * L::VEC + k], sh.h.cnt[min(r, (uint32_t)HMAX - 1u)], c.rp, c.fp,
-                                          c.pp);
-          }
-        }
-      }
-    }
-    if (bits == VMASK) {  // every token of the vector allowed
-#pragma unroll
-      for (int k = 0; k < L::VEC; ++k) {
-        const int i = v * L::VEC + k;
-        const float x = xr[i];
-        ln.fnan |= (x != x);
-        ln.ffin |= fabsf(x) < INFINITY;
-        if (proc) proc[t0 + k] = x;
-        const float z = divide ? div_exact(x, Rd) : x;
-        xr[i] = z;
-        cmax = fmaxf(cmax, z);
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < L::VEC; ++k) {
-        const int i = v * L::VEC + k;
-        const float x = xr[i];
-        ln.fnan |= (x != x);  // (a token past the part end loads 0)
-        const bool al = (bits >> k) & 1u;
-        const float xm = al ? x : -INFINITY;
-        ln.ffin |= fabsf(xm) < INFINITY;
-        if (proc && t0 + k < p1) proc[t0 + k] = xm;
-        const float z = (divide && al) ? div_exact(x, Rd) : xm;
-        xr[i] = z;
-        cmax = fmaxf(cmax, z);
-      }
-    }
-  }
-  // the first token with z not NaN (only until this lane has one)
-  if (ln.fid == 0xFFFFFFFFu) {
-#pragma unroll
-    for (int i = EPL - 1; i >= 0; --i) {
-      const int t = cb + (i / L::VEC) * L::STRIDE + l * L::VEC + (i % L::VEC);
-      if (t < p1 && xr[i] == xr[i]) ln.fid = (uint32_t)t;
-    }
-  }
-  if (c.greedy) {  // first maximum of nan_to_num(x) (sampling.py:76), in token order
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      const float g = fminf(fmaxf(xr[i], -FLTMAX), FLTMAX);
-      const int t = cb + (i / L::VEC) * L::STRIDE + l * L::VEC + (i % L::VEC);
-      if (t < p1 && xr[i] == xr[i] && (g > ln.g || ln.gid == 0xFFFFFFFFu)) {
-        ln.g = g;
-        ln.gid = (uint32_t)t;
-      }
-    }
-  }
-  return cmax;
-}
 
 // Phase 2 of a chunk (rows that list): the lane maximum, the threshold valve, the sum of the unlisted elements relative
 // to the lane maximum, the listing.
@@ -841,7 +556,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     sh.next = NWV;
     sh.hover = 0;
   }
-  if (c.pen) build_history(c, a.hist, hid, p0, p1, sh);
+  if (c.pen) build_history(c, a.hist, hid, p0, p1, sh.h, sh.wcnt, sh.hover);
   else __syncthreads();
 
   Lane ln;
@@ -862,7 +577,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   };
   // First chunk of each wave, phase 1; the part's listing threshold from the 256 lane maxima.
   float cmax = -INFINITY;
-  if (ck < nck) cmax = chunk_phase1<DT>(a, c, row, p0 + ck * CHK, p0, p1, xa, ma, ln, sh);
+  if (ck < nck) cmax = chunk_phase1<DT>(a, c, row, p0 + ck * CHK, p0, p1, xa, ma, ln, sh.h);
   if (listing) {
     sh.lmax[tid] = fkey(cmax) >> 16;
     __syncthreads();
@@ -886,13 +601,13 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   while (ck < nck) {
     const int cn = grab();
     if (cn < nck) load_chunk<DT, AL>(c, p0 + cn * CHK, p1, xb, mb);
-    if (!first) cmax = chunk_phase1<DT>(a, c, row, p0 + ck * CHK, p0, p1, xa, ma, ln, sh);
+    if (!first) cmax = chunk_phase1<DT>(a, c, row, p0 + ck * CHK, p0, p1, xa, ma, ln, sh.h);
     first = false;
     if (listing) chunk_phase2<DT>(a, row, wl, p0 + ck * CHK, cmax, xa, ln);
     if (cn >= nck) break;
     const int cn2 = grab();
     if (cn2 < nck) load_chunk<DT, AL>(c, p0 + cn2 * CHK, p1, xa, ma);
-    cmax = chunk_phase1<DT>(a, c, row, p0 + cn * CHK, p0, p1, xb, mb, ln, sh);
+    cmax = chunk_phase1<DT>(a, c, row, p0 + cn * CHK, p0, p1, xb, mb, ln, sh.h);
     if (listing) chunk_phase2<DT>(a, row, wl, p0 + cn * CHK, cmax, xb, ln);
     ck = cn2;
   }
@@ -927,7 +642,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   s = block_sum_f64(s, sh.wred);
   b = block_sum_f64(b, sh.wred);
   if (tid == 0) {
-    uint32_t flags = sh.hover ? F_OVERFLOW : 0u, kap = 0;
+    uint32_t flags = sh.hover ? F_HOVER : 0u, kap = 0;
     uint64_t t = 0;
 #pragma unroll
     for (int k = 0; k < NWV; ++k) {
