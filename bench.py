@@ -3,12 +3,19 @@
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3]
 
-A step is one gse_sample call (scan + exact kernels) over one batch of the selected workload with every input already
-resident in HBM: logits, packed grammar masks, token histories, per-row parameters and shared uniforms. The inputs
-rotate over enough copies to exceed the 256 MB Infinity Cache, so every step reads HBM. The JSON line reports
-whole-job rows/s (wall clock over the K timed steps), the dominant kernel's roofline (algorithmic bytes per launch
-divided by its average duration from HIP events recorded on the launch stream over the timed steps) and the CPU
-oracle timed on this host (1 core) on a bounded sample of the same workload.
+A step is one gse_sample call (main pass, split-row finish of the deep rows, exact fallback) over one batch of the
+selected workload with every input already resident in HBM: logits, packed grammar masks, token histories, per-row
+parameters and shared uniforms. The inputs rotate over enough copies to exceed the 256 MB Infinity Cache, so every step
+reads HBM.
+
+Two timed regions of K steps each, both bracketed by torch.cuda.synchronize():
+  1. plain steps: whole-job rows/s (wall clock) -> "value";
+  2. profiled steps: the library records HIP events on the launch stream around each of its kernels (gse_profile);
+     the dominant kernel's average duration gives the roofline (algorithmic bytes per launch / duration). The events
+     add a few microseconds between kernels, which is why region 1 carries none.
+The roofline's "traffic" (HBM bytes the kernel moves per launch) is read from the committed rocprofv3 counter summary
+profiles/main_kernel_c3_traffic.txt when it exists (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a plain copy's
+reading). The CPU baseline is the numpy oracle timed on this host (1 core) on a bounded sample of the same workload.
 """
 import argparse
 import ctypes as C
@@ -49,6 +56,19 @@ def cpu_model():
     return platform.processor()
 
 
+def read_traffic(config):
+    """HBM bytes per launch of the main kernel from the committed counter summary (a line "traffic_bytes: N"), or
+    None when there is none for this workload."""
+    path = os.path.join(ROOT, "profiles", f"main_kernel_{config}_traffic.txt")
+    try:
+        for ln in open(path):
+            if ln.startswith("traffic_bytes:"):
+                return int(ln.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -56,7 +76,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="c3", choices=sorted(WORKLOADS))
     ap.add_argument("--copies", type=int, default=0, help="input copies to rotate over (0: enough to exceed the MALL)")
-    ap.add_argument("--cpu-passes", type=int, default=2, help="passes of the CPU oracle over the sample rows")
+    ap.add_argument("--cpu-passes", type=int, default=5, help="passes of the CPU oracle over the sample rows")
+    ap.add_argument("--cpu-rows", type=int, default=0, help="rows of the CPU sample (0: the whole batch)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="before the steps, copy a MIB-MiB device buffer 5 times (a plain copy kernel of known size, "
@@ -135,25 +156,32 @@ def main():
     torch.cuda.synchronize()
     gpu_tokens = sets[0]["toks"].cpu().tolist()
 
-    # timed region: K steps with per-kernel HIP events on the launch stream
-    h.profile()
+    # timed region 1: K plain steps -> whole-job throughput
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     w0 = time.perf_counter()
     ev0.record()
     for k in range(args.steps):
-        step(k, profile=True)
+        step(k)
     ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
-    calls, kms = h.profile()
     ev_ms = ev0.elapsed_time(ev1)
+    # timed region 2: K profiled steps -> per-kernel durations from HIP events on the launch stream
+    h.profile()
+    torch.cuda.synchronize()
+    for k in range(args.steps):
+        step(k, profile=True)
+    torch.cuda.synchronize()
+    calls, kms = h.profile()
+    kern = ["main_kernel", "deep (count + pick + finish)", "exact_kernel"]
+    per = {kern[i]: kms[i] / calls * 1e3 for i in range(min(len(kern), len(kms)))}
     ms_per_step = wall * 1e3 / args.steps
     value = rows * args.steps / wall
-    scan_ms = kms[0] / calls
-    exact_ms = kms[1] / calls
-    log(f"[bench] {args.steps} steps: wall {wall * 1e3:.2f} ms, events {ev_ms:.2f} ms; per call scan {scan_ms * 1e3:.2f} us,"
-        f" exact {exact_ms * 1e3:.2f} us")
+    main_us = per["main_kernel"]
+    log(f"[bench] {args.steps} steps: wall {wall * 1e3:.2f} ms, events {ev_ms:.2f} ms; per call (profiled) " +
+        ", ".join(f"{k} {v:.2f} us" for k, v in per.items()))
+    traffic = read_traffic(args.config)
 
     result = {
         "metric": METRIC if args.config == "c3" else f"rows/sec, {args.config}",
@@ -170,11 +198,11 @@ def main():
         "data": "synthetic (seeded splitmix64 workload generator, goethe-engine_amd/workloads.py)",
         "config": {"workload": f"{args.config}: {WORKLOADS[args.config]}", "rows": rows, "vocab": vocab,
                    "input_copies": copies, "algorithmic_bytes_per_step": a_bytes},
-        "roofline": {"bound": "hbm", "achieved": round(a_bytes / (scan_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": round(a_bytes / (scan_ms * 1e-3) / PEAK_HBM, 4), "traffic": None,
-                     "kernel": "scan_kernel", "kernel_us": round(scan_ms * 1e3, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(a_bytes / (main_us * 1e-6) / 1e9, 1), "peak": PEAK_HBM / 1e9,
+                     "unit": "GB/s", "frac": round(a_bytes / (main_us * 1e-6) / PEAK_HBM, 4), "traffic": traffic,
+                     "kernel": "main_kernel", "kernel_us": round(main_us, 3)},
+        "kernels_us": {k: round(v, 3) for k, v in per.items()},
         "end_to_end": {"step_us_wall": round(ms_per_step * 1e3, 3), "step_us_events": round(ev_ms * 1e3 / args.steps, 3),
-                       "exact_kernel_us": round(exact_ms * 1e3, 3),
                        "hbm_frac": round(a_bytes / (ms_per_step * 1e-3) / PEAK_HBM, 4)},
     }
 
@@ -182,19 +210,23 @@ def main():
         from oracle import sampling_ref as ora
         masks = None if batch.masks is None else [ora.unpack_mask(m, vocab) for m in batch.masks]
         lf = batch.logits_f32()
+        n = min(rows, args.cpu_rows) if args.cpu_rows > 0 else rows
+        sub = lambda v: None if v is None else v[:n]
         ora.sample(lf[:1], batch.params[:1], None, None, None if masks is None else masks[:1],
                    None if batch.history is None else batch.history[:1], batch.uniforms[:1])
         t = time.perf_counter()
         cpu_tokens = None
         for _ in range(args.cpu_passes):
-            cpu_tokens = ora.sample(lf, batch.params, None, None, masks, batch.history, batch.uniforms)
+            cpu_tokens = ora.sample(lf[:n], batch.params[:n], None, None, sub(masks), sub(batch.history),
+                                    batch.uniforms[:n])
         dt = time.perf_counter() - t
-        result["cpu_baseline"] = {"value": round(rows * args.cpu_passes / dt, 2), "unit": "rows/s", "cores": 1,
+        what = f"the full {rows}-row batch" if n == rows else f"the first {n} of the {rows} rows"
+        result["cpu_baseline"] = {"value": round(n * args.cpu_passes / dt, 2), "unit": "rows/s", "cores": 1,
                                   "kind": "port",
-                                  "sample": f"the full {rows}-row batch of the same workload, {args.cpu_passes} passes "
-                                            f"({dt:.1f} s, numpy oracle, {cpu_model()}, {os.cpu_count()} host cores)"}
-        result["parity"] = {"rows": rows, "tokens_equal": gpu_tokens == cpu_tokens,
-                            "mismatches": int(sum(a != b for a, b in zip(gpu_tokens, cpu_tokens)))}
+                                  "sample": f"{what} of the same workload, {args.cpu_passes} pass(es) in {dt:.1f} s "
+                                            f"(numpy oracle on one core, {cpu_model()}, {os.cpu_count()} host cores)"}
+        result["parity"] = {"rows": n, "tokens_equal": gpu_tokens[:n] == cpu_tokens,
+                            "mismatches": int(sum(a != b for a, b in zip(gpu_tokens[:n], cpu_tokens)))}
     print(json.dumps(result), flush=True)
 
 
