@@ -11,7 +11,8 @@ import threading
 import numpy as np
 import torch
 
-ABI_MAJOR, ABI_MINOR = 1, 0
+ABI_MAJOR, ABI_MINOR = 1, 1
+PATH_MAIN, PATH_DEEP, PATH_EXACT = 0, 1, 2  # gse_row_paths codes
 OK, E_ARG, E_DEVICE, E_UNSUPPORTED, E_CAPACITY = 0, -1, -4, -5, -7
 F32, BF16 = 0, 1
 ROW_TEMP_UNDERFLOW = 1
@@ -67,6 +68,7 @@ SIGNATURES = dict(
     gse_pack_mask=(C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_uint32, C.c_uint32, C.c_void_p, C.c_int64,
                              C.c_void_p]),
     gse_profile=(C.c_int, [C.c_void_p, P_(C.c_float), C.c_uint32, P_(C.c_uint32)]),
+    gse_row_paths=(C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p]),
     gse_last_error=(C.c_char_p, [C.c_void_p]),
     gse_close=(None, [C.c_void_p]),
 )
@@ -116,9 +118,16 @@ class Handle:
             why = (self.L.gse_last_error(self.h) or b"").decode()
             raise RuntimeError(f"{what} failed ({rc}): {why}")
 
+    def row_paths(self, rows):
+        """uint8 [rows]: which path finished each row of the last sample / dist call (PATH_MAIN, PATH_DEEP,
+        PATH_EXACT). Waits for the device."""
+        out = np.zeros(rows, np.uint8)
+        self.ck(self.L.gse_row_paths(self.h, rows, out.ctypes.data), "gse_row_paths")
+        return out
+
     def profile(self):
-        """(calls, total milliseconds per kernel: scan, exact[, dist]) of the calls made with BATCH_PROFILE since the
-        last read; clears the record."""
+        """(calls, total milliseconds per kernel: main, deep, exact[, dist]) of the calls made with BATCH_PROFILE
+        since the last read; clears the record."""
         ms = (C.c_float * 4)()
         calls = C.c_uint32()
         n = self.L.gse_profile(self.h, ms, 4, C.byref(calls))

@@ -5,6 +5,7 @@
 
 #include <new>
 #include <string>
+#include <vector>
 
 #include "gse_dev.h"
 #include "gse_int.h"
@@ -331,6 +332,22 @@ GSE_API int gse_profile(gse_handle *h, float *ms, uint32_t n, uint32_t *calls) {
   const int k = h->nprof;
   h->nring = 0;
   return k;
+}
+
+GSE_API int gse_row_paths(gse_handle *h, uint32_t rows, uint8_t *paths) {
+  if (!h) return fail(nullptr, GSE_E_ARG, "null handle");
+  if (!paths && rows) return fail(h, GSE_E_ARG, "paths is required");
+  if (rows > h->max_rows) return fail(h, GSE_E_CAPACITY, "%u rows, the handle was opened for %u", rows, h->max_rows);
+  if (rows == 0) return GSE_OK;
+  DeviceGuard g(h->device);
+  std::vector<gse::RowInfo> info(rows);
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(info.data(), h->info, rows * sizeof(gse::RowInfo), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(h, e, "row paths");
+  for (uint32_t r = 0; r < rows; ++r)
+    paths[r] = (info[r].flags & gse::R_BY_EXACT) ? GSE_PATH_EXACT : (info[r].flags & gse::R_BY_DEEP) ? GSE_PATH_DEEP
+                                                                                                   : GSE_PATH_MAIN;
+  return GSE_OK;
 }
 
 GSE_API const char *gse_last_error(gse_handle *h) { return h ? h->err.c_str() : g_open_err.c_str(); }

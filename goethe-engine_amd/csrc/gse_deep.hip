@@ -28,9 +28,8 @@ using namespace strm;
 
 constexpr float BSC = 32.0f;    // bins per unit of d
 constexpr int BPT = DNB / MT;   // planner: bins per thread (contiguous)
-constexpr int LPT = DCAP / MT;  // finisher: list entries per thread (contiguous)
 constexpr int WLC = 512;        // window elements a slice gathers in LDS before one global reservation
-static_assert(BPT * MT == DNB && LPT * MT == DCAP, "");
+static_assert(BPT * MT == DNB, "");
 
 struct DeepShared {
   HistTab h;                    // the slice's history tables while streaming
@@ -40,7 +39,6 @@ struct DeepShared {
       uint64_t mass[DNB];
     } c;
     uint64_t wl[WLC];           // pick pass: the slice's window elements
-    uint64_t list[DCAP];        // pick finisher: the row's window elements, sorted
   };
   uint32_t next, hover, ticket, nwl, wbase;
   uint32_t wsum[NWV];
@@ -400,7 +398,7 @@ __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 // sorted and walked.
 
 constexpr int NSB = 256;       // sub-bins (128 per window)
-constexpr int SUBC = DCAP;     // entries of one sub-bin that can be collected
+constexpr int SUBC = 2048;     // entries of one sub-bin that can be collected
 
 struct FinShared {
   uint64_t list[DCAP];         // the window entries (unsorted)
@@ -667,7 +665,7 @@ __device__ __forceinline__ void finish_row(const ScanArgs &a, DeepSlot *ds, FinS
       r.kkeep = kkeep;
       r.S = Sd;
       r.Z = clast;
-      r.flags = R_DONE;
+      r.flags = R_DONE | R_BY_DEEP;
       r.token = tok;
       *ri = r;
       if (a.mode == MODE_SAMPLE) a.tokens[row] = tok;

@@ -523,11 +523,11 @@ __global__ __launch_bounds__(XT) void exact_kernel(ScanArgs a) {
           a.lp_ids[(int64_t)row * a.lp_ld + i] = -1;
           a.lps[(int64_t)row * a.lp_ld + i] = __builtin_nanf("");
         }
-        if (tid == 0) ri->flags = R_DONE | (bad ? R_BAD : 0u) | (greedy ? R_GREEDY : 0u);
+        if (tid == 0) ri->flags = R_DONE | R_BY_EXACT | (bad ? R_BAD : 0u) | (greedy ? R_GREEDY : 0u);
         return;
       }
     } else if (anynan) {  // dist of a NaN row is NaN everywhere
-      if (tid == 0) ri->flags = R_DONE | R_SPECIAL;
+      if (tid == 0) ri->flags = R_DONE | R_BY_EXACT | R_SPECIAL;
       return;
     }
   }
@@ -547,7 +547,7 @@ __global__ __launch_bounds__(XT) void exact_kernel(ScanArgs a) {
     if (tid == 0) {
       // z holds +inf or its maximum is -inf: token = order[0], the lowest id at the maximum key (sampling.py:82)
       ri->cmax = best;
-      ri->flags = R_DONE | R_SPECIAL | (greedy ? R_GREEDY : 0u);
+      ri->flags = R_DONE | R_BY_EXACT | R_SPECIAL | (greedy ? R_GREEDY : 0u);
       if (a.mode == MODE_SAMPLE && !greedy) a.tokens[row] = (int32_t)pk_id(best);
     }
     return;
@@ -597,13 +597,13 @@ __global__ __launch_bounds__(XT) void exact_kernel(ScanArgs a) {
       r.kkeep = hl.pk;
       r.S = S;
       r.Z = clast;
-      r.flags = R_DONE;
+      r.flags = R_DONE | R_BY_EXACT;
       r.token = tok;
       if (a.mode == MODE_SAMPLE) a.tokens[row] = tok;
       *ri = r;
     }
   } else if (tid == 0) {
-    ri->flags = R_DONE | R_GREEDY;
+    ri->flags = R_DONE | R_BY_EXACT | R_GREEDY;
   }
   if (nlp > 0) {
     const int n_top = (int)min((int64_t)nlp, V);

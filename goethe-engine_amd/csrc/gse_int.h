@@ -24,6 +24,8 @@ enum : uint32_t {
   R_DONE = 16u,
   R_FULL = 32u,    // with R_HARD: the exact path also recomputes the flags and the greedy argmax
   R_DEEP = 64u,    // with R_HARD: the split-row finish (gse_deep.hip) takes the row first
+  R_BY_DEEP = 128u,   // finished by the split-row finish
+  R_BY_EXACT = 256u,  // finished by the exact path
 };
 
 enum { MODE_SAMPLE = 0, MODE_DIST = 1 };
@@ -53,7 +55,7 @@ static_assert(sizeof(SliceRec) == 64, "");
 constexpr int DEEP_MAX = 128;  // deep rows per call (more: the exact path takes them)
 constexpr int DSMAX = 32;      // slices per deep row
 constexpr int DNB = 512;       // histogram bins of d = z_max - z, 1/32 wide (the last one open-ended)
-constexpr int DCAP = 2048;     // window elements listed per deep row
+constexpr int DCAP = 8192;     // window elements listed per deep row
 
 enum : uint32_t { DS_PENDING = 0u, DS_PLANNED = 1u, DS_FAIL = 2u };
 

@@ -24,7 +24,7 @@ extern "C" {
 #endif
 
 #define GSE_ABI_MAJOR 1
-#define GSE_ABI_MINOR 0
+#define GSE_ABI_MINOR 1
 #define GSE_ABI_VERSION ((GSE_ABI_MAJOR << 16) | GSE_ABI_MINOR)
 
 #if defined(__GNUC__)
@@ -164,10 +164,17 @@ GSE_API int gse_pack_mask(gse_handle *h, const uint8_t *bools, int64_t bool_ld, 
 /* Replaces: nothing (measurement; the reference has no profiler). Calls made with GSE_BATCH_PROFILE record HIP events
  * around each of their kernels on their stream (no synchronisation), for up to GSE_PROFILE_CALLS calls. gse_profile
  * waits for the last recorded event, writes into ms[i] the total milliseconds of kernel i (launch order: main, deep
- * (its two passes together), exact[, dist]) over the recorded calls and into *calls their number, then clears the
+ * (its three launches together), exact[, dist]) over the recorded calls and into *calls their number, then clears the
  * record. Returns the number of kernels per call (<= n are written) or a negative GSE_E_* code. */
 #define GSE_PROFILE_CALLS 512
 GSE_API int gse_profile(gse_handle *h, float *ms, uint32_t n, uint32_t *calls);
+
+/* Replaces: nothing (diagnostics; the reference has one path). Waits for the device, then writes into paths[r] which
+ * path finished row r of the handle's last gse_sample / gse_dist call: GSE_PATH_MAIN (the fused pass), GSE_PATH_DEEP
+ * (the split-row finish of a row whose keep prefix or top-p decision the pass could not settle), GSE_PATH_EXACT (the
+ * exact radix-select path). rows must not exceed that call's rows. */
+enum { GSE_PATH_MAIN = 0, GSE_PATH_DEEP = 1, GSE_PATH_EXACT = 2 };
+GSE_API int gse_row_paths(gse_handle *h, uint32_t rows, uint8_t *paths);
 
 /* Replaces: gc_last_error (abi/gc.h, goethe_engine/gc_c.py:222-227 turns it into RuntimeError). */
 GSE_API const char *gse_last_error(gse_handle *h);

@@ -169,3 +169,43 @@ def test_determinism_and_batch_invariance_full_c3(ge, gpu):
     pb = ge.workloads.Batch(b.name, b.logits[perm], [b.params[i] for i in perm], b.uniforms[perm], b.masks[perm],
                             [b.history[i] for i in perm])
     assert _run(ge, pb, gpu).tolist() == [a1[i] for i in perm]
+
+
+def test_c3_full_batch_matches_oracle(ge, gpu):
+    """The whole 256-row C3 batch: the main pass resolves most rows and the split-row finish the deep ones (30 or so
+    flat, hot nucleus rows); every token equals the oracle's."""
+    b = ge.workloads.c3()
+    want = [w["token"] for w in _oracle(b)]
+    got = _run(ge, b, gpu).tolist()
+    assert got == want
+    paths = ge._lib.handle(gpu.index, b.rows, b.vocab).row_paths(b.rows)
+    assert (paths == ge._lib.PATH_DEEP).sum() > 0  # the split-row finish took part
+    assert (paths == ge._lib.PATH_EXACT).sum() == 0
+
+
+def _flat_rows(ge, n, v, seed):
+    """Hot rows over a flat distribution: the keep prefix of top-p runs to thousands of elements."""
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0.0, 1.0, size=(n, v)).astype(np.float32)
+    P = ge.sampling.SamplingParams
+    tp = [0.8, 0.9, 0.95, 0.99, 0.999]
+    params = [P(temperature=[1.0, 1.3, 1.7][r % 3], top_p=tp[r % 5], top_k=[0, 0, 0, 5000][r % 4],
+                min_p=[0.0, 0.0, 0.0, 0.0, 0.01][r % 5]) for r in range(n)]
+    return x, params
+
+
+def test_deep_rows_sample_and_dist(ge, gpu):
+    """Rows settled by the split-row finish: tokens against the oracle under shared uniforms, and the fp64
+    distribution (which reads the finish's keep boundary and sums) against the oracle's dist."""
+    n, v = 24, 151936
+    x, params = _flat_rows(ge, n, v, 7)
+    u = np.array([ora.uniform(1000 + r, 3) for r in range(n)], np.float64)
+    xt = torch.from_numpy(x).to(gpu)
+    got = ge.sampling.sample_ex(xt, params, None, None, None, uniforms=u).tolist()
+    paths = ge._lib.handle(gpu.index, n, v).row_paths(n)
+    want = ora.sample(x, params, None, None, None, uniforms=u)
+    assert got == want
+    assert (paths == ge._lib.PATH_DEEP).sum() >= n // 2, paths
+    d = ge.sampling.dist_batch(xt, params).cpu().numpy()
+    for r in range(0, n, 5):
+        np.testing.assert_allclose(d[r], ora.dist(x[r], params[r]), rtol=DIST_RTOL, atol=1e-300)
