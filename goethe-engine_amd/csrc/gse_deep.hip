@@ -262,23 +262,36 @@ __device__ __forceinline__ void plan_row(const ScanArgs &a, DeepSlot *ds, const 
   const double delta = 1e-4 * S;
   const uint64_t K = P.top_k > 0 ? (uint64_t)P.top_k : ~0ull;
   const double tS = P.top_p * S;
-  if (tid < 8) sh.q[tid] = DNB - 1;
+  // min-p keeps exp(z - M) >= min_p, i.e. d <= -ln(min_p): bins below bm - 1 are all kept, bins above bm + 1 all cut
+  const bool mp = P.min_p > 0.0;
+  uint32_t bm = 0;
+  if (mp) {
+    const double dm = -log(P.min_p) * (double)BSC;
+    bm = dm >= (double)(DNB - 1) ? (uint32_t)(DNB - 1) : (uint32_t)dm;
+  }
+  if (tid < 8) sh.q[tid] = tid == 5 ? 0u : DNB - 1;
   __syncthreads();
   // round 1: the windows of the cuts
   //   q[0], q[1]: first bins with Pincl >= tS - delta, >= tS + delta (top-p: the bin of the last kept element)
   //   q[2]:       first bin with Cincl >= K (top-k: the bin of rank K - 1)
+  //   q[5] - 1:   last non-empty bin below bm - 1 (min-p: holds a kept element, so the last kept one is at or after it)
+  //   q[6]:       first non-empty bin above bm + 1 (min-p: holds a cut element)
   {
-    uint32_t b0 = DNB - 1, b1 = DNB - 1, b2 = DNB - 1;
+    uint32_t b0 = DNB - 1, b1 = DNB - 1, b2 = DNB - 1, b5 = 0, b6 = DNB - 1;
 #pragma unroll
     for (int j = BPT - 1; j >= 0; --j) {
       const uint32_t b = tid * BPT + j;
       if (pin[j] >= tS - delta) b0 = b;
       if (pin[j] >= tS + delta) b1 = b;
       if (cin[j] >= K) b2 = b;
+      if (mp && c[j] && b + 1 < bm) b5 = max(b5, b + 1);
+      if (mp && c[j] && b > bm + 1) b6 = b;
     }
     atomicMin(&sh.q[0], b0);
     atomicMin(&sh.q[1], b1);
     atomicMin(&sh.q[2], b2);
+    atomicMax(&sh.q[5], b5);
+    atomicMin(&sh.q[6], b6);
   }
   __syncthreads();
   uint32_t w1lo = sh.q[0], w1hi = sh.q[1];
@@ -286,11 +299,11 @@ __device__ __forceinline__ void plan_row(const ScanArgs &a, DeepSlot *ds, const 
     w1lo = min(w1lo, sh.q[2]);
     w1hi = min(w1hi, sh.q[2]);
   }
-  if (P.min_p > 0.0) {  // the last element with exp(z - M) >= min_p has d <= -ln(min_p)
-    const double dm = -log(P.min_p) * (double)BSC;
-    const uint32_t bm = dm >= (double)(DNB - 1) ? (uint32_t)(DNB - 1) : (uint32_t)dm;
-    w1lo = min(w1lo, bm > 0 ? bm - 1 : 0u);
-    w1hi = min(w1hi, min(bm + 1, (uint32_t)(DNB - 1)));
+  if (mp) {
+    const uint32_t lo = sh.q[5] ? sh.q[5] - 1u : 0u, hi = sh.q[6];
+    w1lo = min(w1lo, lo);
+    // when min-p may bind, the window reaches its first cut element (the finish cannot test min-p unlisted)
+    w1hi = lo <= w1hi ? max(w1hi, min(hi, (uint32_t)(DNB - 1))) : min(w1hi, hi);
   }
   // masses before w1lo and through w1hi (approximate)
   if (tid == (int)(w1lo / BPT)) sh.qd[0] = pex[w1lo % BPT];

@@ -1,5 +1,5 @@
 // The fused selection pass. One 256-thread workgroup per (row, part), a part being a contiguous run of at most 40960
-// tokens of the row. Its four waves stream the part in 1024-token chunks (64 lanes x 16 tokens), each wave on its own:
+// tokens of the row. Its four waves stream the part in 512-token chunks (64 lanes x 8 tokens), each wave on its own:
 // chunks are taken from an LDS counter, the next chunk's loads are in flight while the current one is processed, and
 // no barrier separates two chunks. One HBM read of the logits, the packed mask words and the row's history ids; the
 // last workgroup of each row to finish (atomic ticket, nothing waits) resolves the row.
@@ -10,20 +10,24 @@
 //   T > 0 -> z = x / float32(T); stable descending order; fp64 softmax q; keep = rank < top_k AND cumsum(q) - q < top_p
 //            (AND q >= min_p * q_0); c = cumsum(q * keep); token = order[count(c < u * c[-1])]   (sampling.py:59-83)
 //
-// Per chunk, in registers: penalties (history counts from an LDS bitset of the part's tokens, indexed by rank), the NaN
-// test, the mask, z = RN(x / T) computed as RN32(x * RN64(1 / T)) (exact, see div_exact), each lane's running maximum,
-// and the softmax sum of the elements the wave does not list, from v_exp_f32 with a rigorous error bound (rescaled in
-// fp64 when a lane's maximum rises). The part's listing threshold is the 24th largest of the 256 lane maxima of its
-// waves' first chunks (to 16 key bits; the rank scaled down by the share of lanes that saw a z > -inf); a wave whose list passes half its capacity raises its own to the 8th largest of
-// its running lane maxima. Every element at or above the threshold in force for its chunk is listed (exact key, id);
-// thresholds only rise, so a wave's list certifies its top elements down to its final threshold.
+// Per chunk, in registers: the NaN test, the mask and the history exclusion (one select), z = RN(x / T) computed as
+// RN32(x * RN64(1 / T)) (exact, see div_exact), each lane's running maximum, and the softmax sum of the elements the
+// wave does not list, from v_exp_f32 with a rigorous error bound (rescaled in fp64 when a lane's maximum rises). The
+// row history's tokens of the part (penalties: counts from an LDS table indexed by rank) take a side pass with the same
+// arithmetic. The part's listing threshold is the 12th largest of the 256 lane maxima of its waves' first chunks (to 16
+// key bits; the rank scaled down by the share of lanes that saw a z > -inf); a wave whose list passes half its capacity
+// raises its own to the 8th largest of its running lane maxima. Every element at or above the threshold in force when
+// it is processed is listed (exact key, id); thresholds only rise, so a wave's list certifies its top elements down to
+// its final threshold.
 //
 // Row resolve: the union of the waves' lists cut at the largest certified key is the row's certified head: exactly its
 // top elements, stable order included. The resolve sorts the top ~256 of the head (the whole head when the keep prefix
 // runs past them), takes exact fp64 masses of it (and of every listed element for S), and decides the keep prefix and
 // the draw. Top-k, min-p and the draw do not depend on S (they compare masses with masses); top-p uses the S bounds.
-// A decision inside the bound, a keep prefix that runs past the head, or an overflow marks the row hard: the exact
-// path (gse_exact.hip) finishes it.
+// A decision inside the bound, a keep prefix that runs past the head, or an overflowing list marks the row hard: the
+// split-row finish (gse_deep.hip) or, failing that, the exact path (gse_exact.hip) finishes it.
+#include <utility>
+
 #include "gse_stream.h"
 
 namespace gse {
@@ -32,7 +36,7 @@ namespace {
 
 using namespace strm;
 
-constexpr int KP = 24;                 // rank, among the part's 256 first-chunk lane maxima, of its listing threshold
+constexpr int KP = 12;                 // rank, among the part's 256 first-chunk lane maxima, of its listing threshold
 constexpr int KV = 8;                  // rank, among a wave's running lane maxima, of its raised threshold (when its
                                        // list passes half its capacity)
 constexpr int NH = 2048;               // certified head capacity of the row resolve
@@ -466,78 +470,231 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
 
 // ---------------------------------------------------------------------------------------------------------------------
 // Part streaming.
+//
+// The stream carries every token of the part except the tokens of the row's history: those (at most a few hundred per
+// part) are penalized, masked and divided by a side pass with exactly the same arithmetic, and enter the same running
+// state out of order. The stream itself then needs no per-element branch: the mask and the history exclusion are one
+// bit select per element, the listing is skipped for a whole chunk when the lane maxima lie below the threshold, and
+// the unlisted exp terms are summed in fp32 per chunk.
 
-// Phase 2 of a chunk (rows that list): the lane maximum, the threshold valve, the sum of the unlisted elements relative
-// to the lane maximum, the listing.
-template <int DT>
-__device__ __forceinline__ void chunk_phase2(const ScanArgs &a, int row, int wl, int cb, float cmax, float (&xr)[EPL],
-                                              Lane &ln) {
+// Per-lane running state of a wave.
+struct Run {
+  float m;         // running maximum of this lane's z
+  double s;        // sum of this lane's unlisted exp(z - m) (fp32 terms)
+  double b;        // its error bound
+  uint32_t kap;    // the wave's listing threshold key in force (uniform in the wave; only rises)
+  uint32_t woff;   // elements the wave has listed (uniform)
+  float g;         // greedy rows: largest nan_to_num(x) so far, at the lowest token gid holding it
+  uint32_t gid;
+  uint32_t fid;    // lowest token of this lane with z not NaN (found in the lane's first chunk)
+  float fin;       // smallest |x| after the mask: the row has a finite value iff some lane's fin is finite
+  uint64_t nanm;   // lanes that saw a NaN before the mask (wave-uniform)
+};
+
+constexpr int KH = HMAX / MT;  // history tokens a thread carries in the side pass
+
+// z of one chunk in place: the mask and the history exclusion (one select), the NaN and finiteness flags, the
+// division by T (div_exact), the lane's chunk maximum; greedy rows track the first maximum of nan_to_num(x).
+// Selects x where bit k of keep is set, -inf elsewhere: one bit-field insert (v_bfi_b32).
+__device__ __forceinline__ float keep_or_ninf(float x, uint32_t keep, int k) {
+  const uint32_t sel = (uint32_t)(((int32_t)(keep << (31 - k))) >> 31);  // all ones when bit k is set
+  return __uint_as_float((__float_as_uint(x) & sel) | (0xFF800000u & ~sel));
+}
+
+template <int DT, bool MASKED, bool GREEDY, bool DIV>
+__device__ __forceinline__ float stream_z(const RowCtx &c, int cb, int p0, int p1, float (&xr)[EPL],
+                                          const uint32_t (&mw)[Lay<DT>::NV], const HistTab &h, Run &rn, float *proc) {
   using L = Lay<DT>;
+  constexpr uint32_t VMASK = (1u << L::VEC) - 1u;
   const int l = lane_id();
-  const float mnew = fmaxf(ln.m, cmax);
-  if (ln.woff > (uint32_t)(CAPW / 2)) ln.kap = max(ln.kap, wave_kth_largest_u16(fkey(mnew) >> 16, KV) << 16);
-  const float tauf = fkey_inv(ln.kap);
-  if (mnew > ln.m && ln.m > -INFINITY) {  // rescale the lane's sum to its new maximum (fp64)
-    const double f = exp((double)ln.m - (double)mnew);
-    ln.s *= f;
-    ln.b *= f;
-  }
-  ln.m = mnew;
-  const bool dosum = fabsf(mnew) < INFINITY;
-  double s64 = 0.0;
-  float mom = 0.0f;
-  uint32_t woff = ln.woff;
-  uint64_t *cl = a.cand + ((size_t)row * a.nparts * PWAVES + wl) * CAPW;
+  const bool tail = cb + CHK > p1;
+  // per vector: the lane's history bits (tokens that the side pass takes) and in-range bits
+  uint32_t hb[L::NV], inr[L::NV];
 #pragma unroll
   for (int v = 0; v < L::NV; ++v) {
-    float ev[L::VEC];
+    const int t0 = cb + v * L::STRIDE + l * L::VEC;
+    hb[v] = 0;
+    if (c.pen) {
+      const int o = min(t0, p1 - 1) - p0;  // (a vector past the part end reads a valid word; its bits are cleared)
+      hb[v] = (h.bits[o >> 5] >> (o & 31)) & VMASK;
+    }
+    inr[v] = (tail ? (t0 >= p1 ? 0u : (t0 + L::VEC <= p1 ? VMASK : (1u << (p1 - t0)) - 1u)) : VMASK) & ~hb[v];
+  }
+  if (proc) {  // processed logits (after penalties and mask, before T) of the streamed tokens
+#pragma unroll
+    for (int v = 0; v < L::NV; ++v) {
+      const int t0 = cb + v * L::STRIDE + l * L::VEC;
+      const uint32_t al = MASKED ? (mw[v] >> ((l * L::VEC) & 31)) & VMASK : VMASK;
+#pragma unroll
+      for (int k = 0; k < L::VEC; ++k)
+        if ((inr[v] >> k) & 1u) proc[t0 + k] = keep_or_ninf(xr[v * L::VEC + k], al, k);
+    }
+  }
+  float cmax = -INFINITY;
+#pragma unroll
+  for (int v = 0; v < L::NV; ++v) {
+    const int t0 = cb + v * L::STRIDE + l * L::VEC;
+    const uint32_t keep = (MASKED ? (mw[v] >> ((l * L::VEC) & 31)) & VMASK : VMASK) & inr[v];
 #pragma unroll
     for (int k = 0; k < L::VEC; ++k) {
       const int i = v * L::VEC + k;
-      const float z = xr[i];
-      const bool p = z >= tauf;
-      float e = 0.0f;
-      if (dosum) {  // -inf (masked) gives t = -inf, e = 0, and 0 * 1e4 in the moment; NaN rows are bad anyway
-        const float t = (z - mnew) * LOG2E;
-        const float ex = __builtin_amdgcn_exp2f(t);
-        e = p ? 0.0f : ex;
-        mom = fmaf(e, fminf(-t, 1.0e4f), mom);
+      const float x = xr[i];
+      rn.nanm |= ballot64(x != x);  // (past the end x = 0)
+      const float xm = keep_or_ninf(x, keep, k);
+      rn.fin = fminf(rn.fin, fabsf(xm));
+      if constexpr (GREEDY) {  // masked tokens take part in the argmax as -FLT_MAX
+        const float g = fminf(fmaxf(xm, -FLTMAX), FLTMAX);
+        if (((inr[v] >> k) & 1u) && xm == xm && (g > rn.g || rn.gid == 0xFFFFFFFFu)) {
+          rn.g = g;
+          rn.gid = (uint32_t)(t0 + k);
+        }
       }
-      ev[k] = e;
+      const float z = DIV ? div_exact(xm, c.Rd) : xm;
+      xr[i] = z;
+      cmax = fmaxf(cmax, z);
+    }
+  }
+  if (rn.fid == 0xFFFFFFFFu) {  // the lane's first chunk: its lowest token whose value is not NaN
+#pragma unroll
+    for (int i = EPL - 1; i >= 0; --i) {
+      const int t = cb + (i / L::VEC) * L::STRIDE + l * L::VEC + (i % L::VEC);
+      if (t < p1 && xr[i] == xr[i]) rn.fid = (uint32_t)t;
+    }
+  }
+  return cmax;
+}
+
+// Fixed pairwise sum ((f(0) + f(1)) + (f(2) + f(3))) + ... of f over [LO, HI), evaluating f(LO), f(LO + 1), ... in
+// order with log2(HI - LO) partial sums live.
+template <int LO, int HI, typename F>
+__device__ __forceinline__ float pairwise(F &f) {
+  if constexpr (HI - LO == 1) {
+    return f(std::integral_constant<int, LO>{});
+  } else {
+    constexpr int MID = (LO + HI) / 2;
+    const float x = pairwise<LO, MID>(f);
+    const float y = pairwise<MID, HI>(f);
+    return x + y;
+  }
+}
+
+// The lane maximum, the threshold valve, the unlisted exp terms (fp32 per chunk, fp64 across chunks), the listing.
+// tok(i) gives the token of slot i.
+template <int N, typename Tok>
+__device__ __forceinline__ void stream_sum(const ScanArgs &a, int row, int wl, float cmax, const float (&zr)[N],
+                                           Run &rn, Tok tok) {
+  static_assert((N & (N - 1)) == 0 && N <= 256, "");
+  const float mnew = fmaxf(rn.m, cmax);
+  if (rn.woff > (uint32_t)(CAPW / 2)) rn.kap = max(rn.kap, wave_kth_largest_u16(fkey(mnew) >> 16, KV) << 16);
+  const float tauf = fkey_inv(rn.kap);
+  if (mnew > rn.m && rn.m > -INFINITY) {  // rescale the lane's sum to its new maximum (fp64)
+    const double f = exp((double)rn.m - (double)mnew);
+    rn.s *= f;
+    rn.b *= f;
+  }
+  rn.m = mnew;
+  // -inf (masked, excluded) gives t = -inf, e = 0 and 0 * 1e4 in the moment
+  float e[N], t[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    t[i] = (zr[i] - mnew) * LOG2E;
+    e[i] = __builtin_amdgcn_exp2f(t[i]);
+  }
+  if (ballot64(cmax >= tauf)) {  // some lane holds an element at or above the threshold: list them (they leave the sum)
+    uint64_t *cl = a.cand + ((size_t)row * a.nparts * PWAVES + wl) * CAPW;
+    uint32_t woff = rn.woff;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const bool p = zr[i] >= tauf;
       const uint64_t bl = ballot64(p);
       if (bl) {
         if (p) {
           const uint32_t pos = woff + lanes_below(bl);
-          const int t = cb + v * L::STRIDE + l * L::VEC + k;
-          if (pos < (uint32_t)CAPW) st_ag(&cl[pos], pack(fkey(z), (uint32_t)t));
+          if (pos < (uint32_t)CAPW) st_ag(&cl[pos], pack(fkey(zr[i]), tok(i)));
+          e[i] = 0.0f;
         }
         woff += (uint32_t)__popcll(bl);
       }
     }
-    // fixed pairwise order inside the vector, fp64 across vectors
-    if constexpr (L::VEC == 4) {
-      s64 += (double)((ev[0] + ev[1]) + (ev[2] + ev[3]));
-    } else {
-      s64 += (double)(((ev[0] + ev[1]) + (ev[2] + ev[3])) + ((ev[4] + ev[5]) + (ev[6] + ev[7])));
+    rn.woff = woff;
+  }
+  float mom = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) mom = fmaf(e[i], fminf(-t[i], 1.0e4f), mom);
+  auto term = [&](auto ic) __attribute__((always_inline)) { return e[decltype(ic)::value]; };
+  float s = pairwise<0, N>(term);
+  if (!(fabsf(mnew) < INFINITY)) {  // nothing above -inf yet (or +inf): no sum
+    s = 0.0f;
+    mom = 0.0f;
+  }
+  // error bound: v_exp_f32 (2 ulp), the argument's three roundings (2.6 ulp of |t|, times ln 2), log2(N) fp32 pairwise
+  // additions; flushed subnormal results
+  constexpr double LV = N >= 16 ? 4.0 : N >= 8 ? 3.0 : N >= 4 ? 2.0 : 1.0;
+  rn.s += (double)s;
+  rn.b += (double)s * (2.4e-7 + LV * 6.0e-8 + 5e-8) + (double)mom * 1.12e-7 + 1e-36;
+}
+
+// The row history's distinct tokens of the part (ranks tid, tid + MT, ... of the part's history table): logit,
+// penalties, NaN test, mask, z, then the same running state as the stream (tokens out of order: ties go to the lower
+// id). Every thread takes part, with empty slots where it has no token.
+template <int DT, bool GREEDY>
+__device__ __forceinline__ void history_pass(const ScanArgs &a, const RowCtx &c, int row, int wl, int p0,
+                                             bool listing, const Shared &sh, Run &rn, float *proc) {
+  const int tid = threadIdx.x;
+  const uint32_t nd = sh.h.nd;
+  int ids[KH];
+  float x0[KH];
+  bool al[KH];
+#pragma unroll
+  for (int k = 0; k < KH; ++k) {  // the loads first
+    const uint32_t r = (uint32_t)(tid + k * MT);
+    ids[k] = r < nd ? (int)sh.h.off[r] : -1;
+    x0[k] = ids[k] >= 0 ? load_one(c, p0 + ids[k]) : 0.0f;
+    al[k] = ids[k] >= 0 && mask_bit(c, p0 + ids[k]);
+  }
+  float zr[KH];
+  float cmax = -INFINITY;
+  bool hnan = false;
+#pragma unroll
+  for (int k = 0; k < KH; ++k) {
+    zr[k] = -INFINITY;
+    if (ids[k] >= 0) {
+      const int t = p0 + ids[k];
+      const float x = penalize(x0[k], sh.h.cnt[tid + k * MT], c.rp, c.fp, c.pp);
+      hnan |= x != x;
+      const float xm = al[k] ? x : -INFINITY;
+      rn.fin = fminf(rn.fin, fabsf(xm));
+      if (proc) proc[t] = xm;
+      if (x == x && (uint32_t)t < rn.fid) rn.fid = (uint32_t)t;
+      if constexpr (GREEDY) {
+        const float g = fminf(fmaxf(xm, -FLTMAX), FLTMAX);
+        if (xm == xm && (g > rn.g || (g == rn.g && (uint32_t)t < rn.gid) || rn.gid == 0xFFFFFFFFu)) {
+          rn.g = g;
+          rn.gid = (uint32_t)t;
+        }
+        zr[k] = xm;
+      } else {
+        zr[k] = c.divide ? div_exact(xm, c.Rd) : xm;
+      }
+      cmax = fmaxf(cmax, zr[k]);
     }
   }
-  ln.woff = woff;
-  // error bound: v_exp_f32 (2 ulp), the argument's three roundings (2.6 ulp of |t|, times ln 2), two fp32 pairwise
-  // additions; flushed subnormal results
-  ln.s += s64;
-  ln.b += s64 * 4.2e-7 + (double)mom * 1.12e-7 + 1e-36;
+  rn.nanm |= ballot64(hnan);
+  if (listing) stream_sum<KH>(a, row, wl, cmax, zr, rn, [&](int i) { return (uint32_t)(p0 + ids[i]); });
+  else rn.m = fmaxf(rn.m, cmax);
 }
 
 // One part [p0, p1) of the row. Returns true in the workgroup that finished the row last (it then resolves the row).
-template <int DT, bool AL>
+template <int DT, bool AL, bool MASKED, bool GREEDY, bool DIV>
 __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, const RowCtx &c, int row, int part,
                                           Shared &sh) {
   using L = Lay<DT>;
   const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
   const int p0 = part * a.plen, p1 = min(a.V, p0 + a.plen);
   const int nck = (p1 - p0 + CHK - 1) / CHK;
-  const bool listing = !c.greedy || nlp_of(a, P) > 0;  // candidates and the softmax sum are needed
-  const int wl = part * PWAVES + w;                     // this wave's list
+  const bool listing = !GREEDY || nlp_of(a, P) > 0;  // candidates and the softmax sum are needed
+  const int wl = part * PWAVES + w;                  // this wave's list
+  float *proc = a.processed ? a.processed + (int64_t)row * a.processed_ld : nullptr;
 
   // History ids first, then the wave's first chunk: the history tables build while the logits stream in.
   int hid[HPT];
@@ -559,25 +716,28 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   if (c.pen) build_history(c, a.hist, hid, p0, p1, sh.h, sh.wcnt, sh.hover);
   else __syncthreads();
 
-  Lane ln;
-  ln.m = -INFINITY;
-  ln.s = 0.0;
-  ln.b = 0.0;
-  ln.kap = 0;
-  ln.woff = 0;
-  ln.g = -INFINITY;
-  ln.gid = 0xFFFFFFFFu;
-  ln.fid = 0xFFFFFFFFu;
-  ln.fnan = false;
-  ln.ffin = false;
+  Run rn;
+  rn.m = -INFINITY;
+  rn.s = 0.0;
+  rn.b = 0.0;
+  rn.kap = 0;
+  rn.woff = 0;
+  rn.g = -INFINITY;
+  rn.gid = 0xFFFFFFFFu;
+  rn.fid = 0xFFFFFFFFu;
+  rn.fin = INFINITY;
+  rn.nanm = 0;
   auto grab = [&]() -> int {
     uint32_t n = 0;
     if (lane == 0) n = atomicAdd(&sh.next, 1u);
     return __shfl((int)n, 0, WAVE);
   };
-  // First chunk of each wave, phase 1; the part's listing threshold from the 256 lane maxima.
+  auto tok_of = [&](int cb) {
+    return [=](int i) { return (uint32_t)(cb + (i / L::VEC) * L::STRIDE + lane * L::VEC + (i % L::VEC)); };
+  };
+  // First chunk of each wave; the part's listing threshold from the 256 lane maxima.
   float cmax = -INFINITY;
-  if (ck < nck) cmax = chunk_phase1<DT>(a, c, row, p0 + ck * CHK, p0, p1, xa, ma, ln, sh.h);
+  if (ck < nck) cmax = stream_z<DT, MASKED, GREEDY, DIV>(c, p0 + ck * CHK, p0, p1, xa, ma, sh.h, rn, proc);
   if (listing) {
     sh.lmax[tid] = fkey(cmax) >> 16;
     __syncthreads();
@@ -595,49 +755,53 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
       for (int q = 0; q < NWV; ++q) cnt += (uint32_t)__popcll(ballot64(sh.lmax[q * WAVE + lane] >= cand));
       if (cnt >= kp) r = cand;
     }
-    ln.kap = max(r << 16, KEY_NEGINF + 1u);
+    rn.kap = max(r << 16, KEY_NEGINF + 1u);
   }
   bool first = true;
   while (ck < nck) {
     const int cn = grab();
     if (cn < nck) load_chunk<DT, AL>(c, p0 + cn * CHK, p1, xb, mb);
-    if (!first) cmax = chunk_phase1<DT>(a, c, row, p0 + ck * CHK, p0, p1, xa, ma, ln, sh.h);
+    if (!first) cmax = stream_z<DT, MASKED, GREEDY, DIV>(c, p0 + ck * CHK, p0, p1, xa, ma, sh.h, rn, proc);
     first = false;
-    if (listing) chunk_phase2<DT>(a, row, wl, p0 + ck * CHK, cmax, xa, ln);
+    if (listing) stream_sum<EPL>(a, row, wl, cmax, xa, rn, tok_of(p0 + ck * CHK));
+    else rn.m = fmaxf(rn.m, cmax);
     if (cn >= nck) break;
     const int cn2 = grab();
     if (cn2 < nck) load_chunk<DT, AL>(c, p0 + cn2 * CHK, p1, xa, ma);
-    cmax = chunk_phase1<DT>(a, c, row, p0 + cn * CHK, p0, p1, xb, mb, ln, sh.h);
-    if (listing) chunk_phase2<DT>(a, row, wl, p0 + cn * CHK, cmax, xb, ln);
+    cmax = stream_z<DT, MASKED, GREEDY, DIV>(c, p0 + cn * CHK, p0, p1, xb, mb, sh.h, rn, proc);
+    if (listing) stream_sum<EPL>(a, row, wl, cmax, xb, rn, tok_of(p0 + cn * CHK));
+    else rn.m = fmaxf(rn.m, cmax);
     ck = cn2;
   }
+  // the history tokens of the part (the tables are still in LDS: the resolve has not started)
+  if (c.pen) history_pass<DT, GREEDY>(a, c, row, wl, p0, listing, sh, rn, proc);
 
   // Part record: the part maximum, then every lane's sum rescaled to it (fp64, fixed order).
-  const float wm = wave_max_f32(ln.m);
-  const uint64_t bn = ballot64(ln.fnan), bf = ballot64(ln.ffin);
+  const float wm = wave_max_f32(rn.m);
+  const uint64_t bf = ballot64(rn.fin < INFINITY);
   uint64_t top;
-  if (c.greedy) {
-    top = ln.gid != 0xFFFFFFFFu ? pack(fkey(ln.g), ln.gid) : 0ull;
+  if (GREEDY) {
+    top = rn.gid != 0xFFFFFFFFu ? pack(fkey(rn.g), rn.gid) : 0ull;
   } else {
-    top = ln.fid != 0xFFFFFFFFu ? pack(KEY_NEGINF, ln.fid) : 0ull;
+    top = rn.fid != 0xFFFFFFFFu ? pack(KEY_NEGINF, rn.fid) : 0ull;
   }
   top = wave_max_u64(top);
   if (lane == 0) {
     sh.wmax[w] = wm;
-    sh.wflags[w] = (bn ? F_NAN : 0u) | (bf ? F_FINITE : 0u);
+    sh.wflags[w] = (rn.nanm ? F_NAN : 0u) | (bf ? F_FINITE : 0u);
     sh.wtop[w] = top;
-    sh.wkap[w] = ln.kap;
-    sh.wcnt[w] = ln.woff;
+    sh.wkap[w] = rn.kap;
+    sh.wcnt[w] = rn.woff;
   }
   __syncthreads();
   float M = sh.wmax[0];
 #pragma unroll
   for (int k = 1; k < NWV; ++k) M = fmaxf(M, sh.wmax[k]);
   double s = 0.0, b = 0.0;
-  if (ln.m > -INFINITY && fabsf(M) < INFINITY) {
-    const double f = exp((double)ln.m - (double)M);
-    s = ln.s * f;
-    b = ln.b * f;
+  if (rn.m > -INFINITY && fabsf(M) < INFINITY) {
+    const double f = exp((double)rn.m - (double)M);
+    s = rn.s * f;
+    b = rn.b * f;
   }
   s = block_sum_f64(s, sh.wred);
   b = block_sum_f64(b, sh.wred);
@@ -687,7 +851,28 @@ __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
   const gse_row P = a.params[row];
   const RowCtx c = make_ctx(a, row, P);
   const bool aligned = (((uintptr_t)c.base) & 15u) == 0;
-  const bool last = aligned ? part_body<DT, true>(a, P, c, row, part, sh) : part_body<DT, false>(a, P, c, row, part, sh);
+  // variants: alignment (16-byte vector loads), mask, greedy (no division), division by T (T != 1)
+  bool last;
+  if (c.greedy) {
+    last = aligned ? part_body<DT, true, true, true, false>(a, P, c, row, part, sh)
+                   : part_body<DT, false, true, true, false>(a, P, c, row, part, sh);
+  } else if (c.mw) {
+    if (c.divide) {
+      last = aligned ? part_body<DT, true, true, false, true>(a, P, c, row, part, sh)
+                     : part_body<DT, false, true, false, true>(a, P, c, row, part, sh);
+    } else {
+      last = aligned ? part_body<DT, true, true, false, false>(a, P, c, row, part, sh)
+                     : part_body<DT, false, true, false, false>(a, P, c, row, part, sh);
+    }
+  } else {
+    if (c.divide) {
+      last = aligned ? part_body<DT, true, false, false, true>(a, P, c, row, part, sh)
+                     : part_body<DT, false, false, false, true>(a, P, c, row, part, sh);
+    } else {
+      last = aligned ? part_body<DT, true, false, false, false>(a, P, c, row, part, sh)
+                     : part_body<DT, false, false, false, false>(a, P, c, row, part, sh);
+    }
+  }
   if (!last) return;
   resolve_row(a, row, P, sh);
   if (threadIdx.x == 0) a.done[row] = 0u;

@@ -9,7 +9,7 @@ namespace strm {
 
 constexpr int MT = 256;                // threads per part workgroup
 constexpr int NWV = MT / WAVE;         // waves
-constexpr int EPL = 16;                // tokens per lane per chunk
+constexpr int EPL = 8;                 // tokens per lane per chunk
 constexpr int CHK = WAVE * EPL;        // tokens per chunk
 constexpr int PMAX = PTOK;             // tokens per part, at most
 constexpr int PWORDS = PMAX / 32;      // history bitset words of a part
@@ -29,10 +29,12 @@ struct Lay<GSE_BF16> {  // token cb + v * 512 + l * 8 + k
   static constexpr int VEC = 8, NV = EPL / 8, STRIDE = WAVE * 8;
 };
 
-struct HistTab {  // history of a part's tokens: bitset, prefix popcounts of its words, counts by rank
+struct HistTab {  // history of a part's tokens: bitset, prefix popcounts of its words, counts and offsets by rank
   uint32_t bits[PWORDS];
   uint32_t pre[PWORDS];
   uint32_t cnt[HMAX];
+  uint16_t off[HMAX];   // offset in the part of the token of each rank
+  uint32_t nd;          // distinct tokens (ranks), at most HMAX
 };
 
 // z = RN32(x / T) as RN32(x * Rd), Rd = RN64(1 / T). |x * Rd - x / T| <= 2^-51 |x / T| (two fp64 roundings), while
@@ -93,11 +95,17 @@ __device__ __forceinline__ void build_history(const RowCtx &c, const int32_t *hi
     }
   const uint32_t nd = min(tot, (uint32_t)HMAX);
   for (uint32_t i = tid; i < nd; i += MT) h.cnt[i] = 0;
-  if (tid == 0 && tot > (uint32_t)HMAX) hover = 1;
+  if (tid == 0) {
+    h.nd = nd;
+    if (tot > (uint32_t)HMAX) hover = 1;
+  }
   __syncthreads();
   each([&](int o) {
     const uint32_t r = h.pre[o >> 5] + __popc(h.bits[o >> 5] & ((1u << (o & 31)) - 1u));
-    if (r < (uint32_t)HMAX) atomicAdd(&h.cnt[r], 1u);
+    if (r < (uint32_t)HMAX) {
+      atomicAdd(&h.cnt[r], 1u);
+      h.off[r] = (uint16_t)o;  // (a repeated id writes the same offset)
+    }
   });
   __syncthreads();
 }
