@@ -119,18 +119,11 @@ void parts(const gse_handle *h, uint32_t rows, uint32_t vocab, int *nparts, int 
   *nparts = (int)((vocab + len - 1) / len);
 }
 
-// Slices of a deep row for the split-row finish: at most DSMAX of them, each a multiple of PCHUNK long and at most PTOK
-// (a vocabulary too long for that leaves deep rows to the exact path).
-void deep_slices(const gse_handle *h, uint32_t rows, uint32_t vocab, int *nsl, int *len, int *grid) {
-  uint32_t l = ((vocab + gse::DSMAX - 1) / gse::DSMAX + gse::PCHUNK - 1) / gse::PCHUNK * gse::PCHUNK;
-  if (l > (uint32_t)gse::PTOK) {
-    *nsl = *len = *grid = 0;
-    return;
-  }
-  *len = (int)l;
-  *nsl = (int)((vocab + l - 1) / l);
+// Workgroups of the split-row finish launches: one resident round (the kernels slice the deep rows to fit it).
+void deep_grid(const gse_handle *h, uint32_t rows, int *nsl, int *grid) {
   const uint32_t slots = rows < (uint32_t)gse::DEEP_MAX ? rows : (uint32_t)gse::DEEP_MAX;
-  const uint32_t items = (slots + 7) / 8 * 8 * (uint32_t)*nsl;
+  const uint32_t items = slots * (uint32_t)gse::DSMAX;
+  *nsl = gse::DSMAX;
   *grid = (int)(items < h->target ? items : h->target);
 }
 
@@ -159,7 +152,7 @@ gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   a.dslot = h->dslot;
   a.dhist = h->dhist;
   a.dlist = h->dlist;
-  deep_slices(h, b.rows, b.vocab, &a.dslices, &a.dlen, &a.dgrid);
+  deep_grid(h, b.rows, &a.dslices, &a.dgrid);
   return a;
 }
 

@@ -1,20 +1,21 @@
 // Split-row finish of the rows the main pass could not decide from its certified head: a keep prefix that runs past
 // the listed elements (the nucleus of a flat, hot row), or a top-p decision that fell inside the main pass's bound on
-// S. Three launches, back to back on the stream: two passes over each such row, each spread over dslices workgroups
-// (slices of dlen tokens), then one workgroup per row. No workgroup waits for another: slices add their results into
-// the row's record with integer atomics (the same sums in any order).
+// S. Two launches, back to back on the stream, each a pass over every such row spread over S slices (S and the slice
+// length follow from the number of deep rows so that one launch is one round of resident workgroups). No workgroup
+// waits for another: slices add their results into the row's record with integer atomics (the same sums in any order),
+// and the last slice of a row to finish (atomic ticket) carries on with the row.
 //
 //   count:  each slice recomputes z exactly as the main pass does and adds a 512-bin histogram of d = z_max - z
 //           (counts, and masses exp2 in fp32 summed as 2^-40 fixed point; bins 1/32 wide, the last one open-ended). d
-//           is monotone in z, so the bins follow the stable order and ties share a bin.
-//   pick:   each slice plans from the histogram (the same deterministic plan in every slice, overlapped with its first
-//           loads): the bins that may hold the last kept element (top-p, top-k and min-p cuts, with a margin for the
-//           fp32 masses), the bins that may hold the draw, and whether they hold at most DCAP elements. It then adds the
-//           exact fixed-point mass of every element (fp64 exp, 2^-64 resolution) to S and to the regions before and
-//           between the two windows, and lists the window elements.
-//   finish: sorts the list, walks exact prefixes, and checks that the cut and the draw fall inside it at contiguous
-//           ranks; then it writes the token and the row's dist data, and clears the row's records for the next call. A
-//           failed check leaves the row to the exact path (gse_exact.hip).
+//           is monotone in z, so the bins follow the stable order and ties share a bin. The row's last slice plans:
+//           the bins that may hold the last kept element (top-p, top-k and min-p cuts, with a margin for the fp32
+//           masses), the bins that may hold the draw, and whether they hold at most DCAP elements.
+//   pick:   each slice adds the exact fixed-point mass of every element (fp64 exp, 2^-64 resolution) to S and to the
+//           regions before and between the two windows, and lists the window elements. The row's last slice finishes:
+//           exact sub-bin counts and masses over the list locate the cut and the draw, only the sub-bins holding them
+//           are sorted, and their exact prefixes (one scan) give the last kept element, c_last and the token. A failed
+//           check leaves the row to the exact path (gse_exact.hip). It then clears the row's records for the next
+//           call.
 //
 // Semantics (goethe_engine/sampling.py:77-83): keep_r = r < top_k AND cumsum(q)_r - q_r < top_p (AND q_r >= min_p q_0);
 // c = cumsum(q keep); token = order[min(count(c < u c[-1]), m - 1)], m = keep.sum().
@@ -45,11 +46,44 @@ struct DeepShared {
   uint64_t wred[NWV], wred2[NWV];
   double dred[NWV];
   uint32_t q[8];                // first-bin / first-index queries (atomicMin)
-  uint32_t plan[5];             // w2lo, w2hi, w1lo, w1hi, status
   double qd[2];
   uint64_t acc[DA_N];
   uint64_t pub[6];
 };
+
+// 2^(j / 64), j = 0..63, correctly rounded.
+__constant__ double EXP2_64[64] = {
+    0x1.0000000000000p+0, 0x1.02c9a3e778061p+0, 0x1.059b0d3158574p+0, 0x1.0874518759bc8p+0,
+    0x1.0b5586cf9890fp+0, 0x1.0e3ec32d3d1a2p+0, 0x1.11301d0125b51p+0, 0x1.1429aaea92de0p+0,
+    0x1.172b83c7d517bp+0, 0x1.1a35beb6fcb75p+0, 0x1.1d4873168b9aap+0, 0x1.2063b88628cd6p+0,
+    0x1.2387a6e756238p+0, 0x1.26b4565e27cddp+0, 0x1.29e9df51fdee1p+0, 0x1.2d285a6e4030bp+0,
+    0x1.306fe0a31b715p+0, 0x1.33c08b26416ffp+0, 0x1.371a7373aa9cbp+0, 0x1.3a7db34e59ff7p+0,
+    0x1.3dea64c123422p+0, 0x1.4160a21f72e2ap+0, 0x1.44e086061892dp+0, 0x1.486a2b5c13cd0p+0,
+    0x1.4bfdad5362a27p+0, 0x1.4f9b2769d2ca7p+0, 0x1.5342b569d4f82p+0, 0x1.56f4736b527dap+0,
+    0x1.5ab07dd485429p+0, 0x1.5e76f15ad2148p+0, 0x1.6247eb03a5585p+0, 0x1.6623882552225p+0,
+    0x1.6a09e667f3bcdp+0, 0x1.6dfb23c651a2fp+0, 0x1.71f75e8ec5f74p+0, 0x1.75feb564267c9p+0,
+    0x1.7a11473eb0187p+0, 0x1.7e2f336cf4e62p+0, 0x1.82589994cce13p+0, 0x1.868d99b4492edp+0,
+    0x1.8ace5422aa0dbp+0, 0x1.8f1ae99157736p+0, 0x1.93737b0cdc5e5p+0, 0x1.97d829fde4e50p+0,
+    0x1.9c49182a3f090p+0, 0x1.a0c667b5de565p+0, 0x1.a5503b23e255dp+0, 0x1.a9e6b5579fdbfp+0,
+    0x1.ae89f995ad3adp+0, 0x1.b33a2b84f15fbp+0, 0x1.b7f76f2fb5e47p+0, 0x1.bcc1e904bc1d2p+0,
+    0x1.c199bdd85529cp+0, 0x1.c67f12e57d14bp+0, 0x1.cb720dcef9069p+0, 0x1.d072d4a07897cp+0,
+    0x1.d5818dcfba487p+0, 0x1.da9e603db3285p+0, 0x1.dfc97337b9b5fp+0, 0x1.e502ee78b3ff6p+0,
+    0x1.ea4afa2a490dap+0, 0x1.efa1bee615a27p+0, 0x1.f50765b6e4540p+0, 0x1.fa7c1819e90d8p+0,
+};
+
+// e^d in fp64 for d <= 0, within about 1.5 ulp (the sums below are exact sums of these values): d = k ln2/64 + r with
+// |r| <= ln2/128 (ln2/64 split in two, k * hi exact), e^r - 1 by its degree-5 Taylor polynomial (remainder < 4e-17),
+// 2^(k/64) from the table tab (in LDS). 0 below -45, where the 2^-64 fixed point of the sums is 0 anyway.
+__device__ __forceinline__ double exp_nonpos(double d, const double *tab) {
+  const double kd = rint(d * 92.33248261689366);  // 64 / ln 2
+  double r = fma(-kd, 0x1.62e42ffp-7, d);
+  r = fma(-kd, -6.563929801064195e-13, r);
+  const double q = r * fma(r, fma(r, fma(r, fma(r, 1.0 / 120.0, 1.0 / 24.0), 1.0 / 6.0), 0.5), 1.0);
+  const int k = (int)kd;
+  const double t = tab[k & 63];
+  const double e = ldexp(fma(t, q, t), k >> 6);
+  return d >= -45.0 ? e : 0.0;
+}
 
 // Bin of z (z > -inf, z <= M): monotone non-increasing in z.
 __device__ __forceinline__ uint32_t dbin(float z, float M) {
@@ -206,58 +240,50 @@ __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c,
   __syncthreads();
 }
 
-// Work items (deep row slot, slice) of a pass: the slices of a slot on one XCD (workgroups go round-robin over the 8
-// XCDs and the grid is a multiple of 8).
-__device__ __forceinline__ bool item_of(const ScanArgs &a, int i, int nd, int &slot, int &slice) {
-  slot = (i & 7) + 8 * ((i >> 3) / a.dslices);
-  slice = (i >> 3) % a.dslices;
-  return slot < nd;
+// Slices of the deep rows: as many per row as one round of the grid holds (the grid is resident at once), at most
+// DSMAX, each a multiple of CHK long and at most PTOK. Both launches see the same grid and row count, so they slice
+// alike. Item i of a launch is slice i % S of slot i / S.
+struct DGeom {
+  int S, len;
+};
+__device__ __forceinline__ DGeom deep_geom(const ScanArgs &a, int nd) {
+  int S = min(max(1, (int)gridDim.x / nd), DSMAX);
+  S = max(S, (a.V + PTOK - 1) / PTOK);
+  int len = ((a.V + S - 1) / S + CHK - 1) / CHK * CHK;
+  len = min(len, PTOK);
+  return DGeom{(a.V + len - 1) / len, len};
 }
-
-__device__ __forceinline__ int items_of(const ScanArgs &a, int nd) { return (nd + 7) / 8 * 8 * a.dslices; }
 
 // ---------------------------------------------------------------------------------------------------------------------
 // Pass 1: histogram and plan.
 
-// The plan of a row from its histogram (written by the previous launch): sh.plan = {w2lo, w2hi, w1lo, w1hi, status}.
-// The slice that stores it (slice 0) also writes it into the row's slot for the finish launch.
-__device__ __forceinline__ void plan_row(const ScanArgs &a, DeepSlot *ds, const gse_row &P, float M, bool store,
-                                         DeepShared &sh) {
-  const int tid = threadIdx.x;
-  const uint64_t *gh = a.dhist + (size_t)(ds - a.dslot) * 2 * DNB;
-  uint64_t c[BPT], q[BPT];
-#pragma unroll
-  for (int j = 0; j < BPT; ++j) {
-    c[j] = gh[tid * BPT + j];
-    q[j] = gh[DNB + tid * BPT + j];
-  }
-  double m[BPT];
-  uint64_t cl = 0, dummy = 0;
+// The plan of a row from its histogram (added by every slice of this launch), into the row's slot: {w2lo, w2hi, w1lo,
+// w1hi, status} and the element counts of the regions outside the windows. Run by wave 0 of the row's last slice:
+// lane l holds bins [8l, 8l + 8), prefixes by wave scans, "first bin with" queries by wave minima. Compact code (it
+// runs once per row, cold).
+constexpr int PBL = DNB / WAVE;  // bins per lane
+static_assert(PBL * WAVE == DNB, "");
+
+__device__ __forceinline__ uint32_t first_bin(bool hit, uint32_t b) { return wave_min_u32(hit ? b : (uint32_t)DNB - 1u); }
+
+__device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode) {
+  const int l = lane_id();
+  const gse_row &P = ds->P;
+  const float M = ds->M;
+  uint64_t c[PBL];
+  double m[PBL];
+  uint64_t cl = 0;
   double ml = 0.0;
-#pragma unroll
-  for (int j = 0; j < BPT; ++j) {
-    m[j] = (double)q[j] * 9.094947017729282e-13;  // 2^-40
+  for (int j = 0; j < PBL; ++j) {
+    c[j] = ld_ag(&gh[l * PBL + j]);
+    m[j] = (double)ld_ag(&gh[DNB + l * PBL + j]) * 9.094947017729282e-13;  // 2^-40
     cl += c[j];
     ml += m[j];
   }
-  double S;
-  const double mpre = block_excl_scan_f64(ml, S, sh);
-  const uint64_t ctot = block_sum_u64(cl, sh);
-  block_excl_scan2(cl, dummy, sh);
-  double pin[BPT], pex[BPT];
-  uint64_t cin[BPT];
-  {
-    double p = mpre;
-    uint64_t n = cl;
-#pragma unroll
-    for (int j = 0; j < BPT; ++j) {
-      pex[j] = p;
-      p += m[j];
-      pin[j] = p;
-      n += c[j];
-      cin[j] = n;
-    }
-  }
+  const double mi = wave_incl_scan_f64(ml);
+  const double S = shfl_f64(mi, WAVE - 1);
+  const uint64_t ci = wave_incl_scan_u64(cl);
+  const uint64_t ctot = shfl_u64(ci, WAVE - 1);
   // the fp32 exp2 terms (2 ulp) and the 2^-40 floors stay far inside this margin
   const double delta = 1e-4 * S;
   const uint64_t K = P.top_k > 0 ? (uint64_t)P.top_k : ~0ull;
@@ -269,62 +295,71 @@ __device__ __forceinline__ void plan_row(const ScanArgs &a, DeepSlot *ds, const 
     const double dm = -log(P.min_p) * (double)BSC;
     bm = dm >= (double)(DNB - 1) ? (uint32_t)(DNB - 1) : (uint32_t)dm;
   }
-  if (tid < 8) sh.q[tid] = tid == 5 ? 0u : DNB - 1;
-  __syncthreads();
-  // round 1: the windows of the cuts
-  //   q[0], q[1]: first bins with Pincl >= tS - delta, >= tS + delta (top-p: the bin of the last kept element)
-  //   q[2]:       first bin with Cincl >= K (top-k: the bin of rank K - 1)
-  //   q[5] - 1:   last non-empty bin below bm - 1 (min-p: holds a kept element, so the last kept one is at or after it)
-  //   q[6]:       first non-empty bin above bm + 1 (min-p: holds a cut element)
+  // the windows of the cuts:
+  //   b0, b1: first bins with inclusive mass >= tS - delta, >= tS + delta (top-p: the bin of the last kept element)
+  //   b2:     first bin with inclusive count >= K (top-k: the bin of rank K - 1)
+  //   b5 - 1: last non-empty bin below bm - 1 (min-p: holds a kept element, so the last kept one is at or after it)
+  //   b6:     first non-empty bin above bm + 1 (min-p: holds a cut element)
+  uint32_t b0 = DNB - 1, b1 = DNB - 1, b2 = DNB - 1, b5 = 0, b6 = DNB - 1;
   {
-    uint32_t b0 = DNB - 1, b1 = DNB - 1, b2 = DNB - 1, b5 = 0, b6 = DNB - 1;
-#pragma unroll
-    for (int j = BPT - 1; j >= 0; --j) {
-      const uint32_t b = tid * BPT + j;
-      if (pin[j] >= tS - delta) b0 = b;
-      if (pin[j] >= tS + delta) b1 = b;
-      if (cin[j] >= K) b2 = b;
+    double pin = mi - ml;
+    uint64_t cin = ci - cl;
+    for (int j = 0; j < PBL; ++j) {
+      const uint32_t b = l * PBL + j;
+      pin += m[j];
+      cin += c[j];
+      if (pin >= tS - delta) b0 = min(b0, b);
+      if (pin >= tS + delta) b1 = min(b1, b);
+      if (cin >= K) b2 = min(b2, b);
       if (mp && c[j] && b + 1 < bm) b5 = max(b5, b + 1);
-      if (mp && c[j] && b > bm + 1) b6 = b;
+      if (mp && c[j] && b > bm + 1) b6 = min(b6, b);
     }
-    atomicMin(&sh.q[0], b0);
-    atomicMin(&sh.q[1], b1);
-    atomicMin(&sh.q[2], b2);
-    atomicMax(&sh.q[5], b5);
-    atomicMin(&sh.q[6], b6);
   }
-  __syncthreads();
-  uint32_t w1lo = sh.q[0], w1hi = sh.q[1];
+  b0 = wave_min_u32(b0);
+  b1 = wave_min_u32(b1);
+  b2 = wave_min_u32(b2);
+  b5 = wave_max_u32(b5);
+  b6 = wave_min_u32(b6);
+  uint32_t w1lo = b0, w1hi = b1;
   if (K < ctot) {
-    w1lo = min(w1lo, sh.q[2]);
-    w1hi = min(w1hi, sh.q[2]);
+    w1lo = min(w1lo, b2);
+    w1hi = min(w1hi, b2);
   }
   if (mp) {
-    const uint32_t lo = sh.q[5] ? sh.q[5] - 1u : 0u, hi = sh.q[6];
+    const uint32_t lo = b5 ? b5 - 1u : 0u, hi = b6;
     w1lo = min(w1lo, lo);
     // when min-p may bind, the window reaches its first cut element (the finish cannot test min-p unlisted)
     w1hi = lo <= w1hi ? max(w1hi, min(hi, (uint32_t)(DNB - 1))) : min(w1hi, hi);
   }
-  // masses before w1lo and through w1hi (approximate)
-  if (tid == (int)(w1lo / BPT)) sh.qd[0] = pex[w1lo % BPT];
-  if (tid == (int)(w1hi / BPT)) sh.qd[1] = pin[w1hi % BPT];
-  __syncthreads();
-  uint32_t w2lo = w1lo, w2hi = w1hi;
-  if (a.mode == MODE_SAMPLE) {
-    const double u = ds->u;  // (P and u: the slot copy)
-    const double tlo = u * (sh.qd[0] - delta) - delta, thi = u * (sh.qd[1] + delta) + delta;
-    uint32_t b3 = DNB - 1, b4 = DNB - 1;
-#pragma unroll
-    for (int j = BPT - 1; j >= 0; --j) {
-      const uint32_t b = tid * BPT + j;
-      if (pin[j] >= tlo) b3 = b;
-      if (pin[j] >= thi) b4 = b;
+  // masses before w1lo and through w1hi (approximate), then the windows of the draw
+  double qd0 = 0.0, qd1 = 0.0;
+  {
+    double pin = mi - ml;
+    for (int j = 0; j < PBL; ++j) {
+      const uint32_t b = l * PBL + j;
+      if (b == w1lo) qd0 = pin;
+      pin += m[j];
+      if (b == w1hi) qd1 = pin;
     }
-    atomicMin(&sh.q[3], b3);
-    atomicMin(&sh.q[4], b4);
-    __syncthreads();
-    w2hi = min(sh.q[4], w1hi);
-    w2lo = min(sh.q[3], w2hi);
+  }
+  qd0 = wave_sum_f64(qd0);  // (one lane holds each)
+  qd1 = wave_sum_f64(qd1);
+  uint32_t w2lo = w1lo, w2hi = w1hi;
+  if (mode == MODE_SAMPLE) {
+    const double u = ds->u;
+    const double tlo = u * (qd0 - delta) - delta, thi = u * (qd1 + delta) + delta;
+    uint32_t b3 = DNB - 1, b4 = DNB - 1;
+    double pin = mi - ml;
+    for (int j = 0; j < PBL; ++j) {
+      const uint32_t b = l * PBL + j;
+      pin += m[j];
+      if (pin >= tlo) b3 = min(b3, b);
+      if (pin >= thi) b4 = min(b4, b);
+    }
+    b3 = wave_min_u32(b3);
+    b4 = wave_min_u32(b4);
+    w2hi = min(b4, w1hi);
+    w2lo = min(b3, w2hi);
   }
   if (w2hi + 1 >= w1lo) {  // touching or overlapping windows: one window
     w2lo = min(w2lo, w1lo);
@@ -332,40 +367,40 @@ __device__ __forceinline__ void plan_row(const ScanArgs &a, DeepSlot *ds, const 
     w1lo = w2lo;
     w1hi = w2hi;
   }
-  uint64_t inw = 0;
-#pragma unroll
-  for (int j = 0; j < BPT; ++j) {
-    const uint32_t b = tid * BPT + j;
+  uint64_t inw = 0, n0 = 0, n1 = 0, n2 = 0;
+  for (int j = 0; j < PBL; ++j) {
+    const uint32_t b = l * PBL + j;
     if ((b >= w2lo && b <= w2hi) || (b >= w1lo && b <= w1hi)) inw += c[j];
+    else if (b < w2lo) n0 += c[j];
+    else if (b < w1lo) n1 += c[j];
+    else n2 += c[j];
   }
-  inw = block_sum_u64(inw, sh);
+  inw = wave_sum_u64(inw);
+  n0 = wave_sum_u64(n0);
+  n1 = wave_sum_u64(n1);
+  n2 = wave_sum_u64(n2);
   const uint32_t status = (inw > 0 && inw <= (uint64_t)DCAP && S > 0.0 && fabsf(M) < INFINITY) ? DS_PLANNED : DS_FAIL;
-  if (tid == 0) {
-    sh.plan[0] = w2lo;
-    sh.plan[1] = w2hi;
-    sh.plan[2] = w1lo;
-    sh.plan[3] = w1hi;
-    sh.plan[4] = status;
-    if (store) {
-      ds->w2lo = w2lo;
-      ds->w2hi = w2hi;
-      ds->w1lo = w1lo;
-      ds->w1hi = w1hi;
-      ds->status = status;
-    }
+  if (l == 0) {
+    ds->w2lo = w2lo;
+    ds->w2hi = w2hi;
+    ds->w1lo = w1lo;
+    ds->w1hi = w1hi;
+    ds->status = status;
+    ds->acc[DA_C0] = n0;  // (the element counts of the regions the pick pass sums without listing)
+    ds->acc[DA_C1] = n1;
+    ds->acc[DA_C2] = n2;
   }
-  __syncthreads();
 }
 
 template <int DT, bool AL>
-__device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slice, DeepShared &sh) {
+__device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slice, const DGeom &g, DeepShared &sh) {
   const int tid = threadIdx.x;
   DeepSlot *ds = a.dslot + slot;
   const int row = ds->row;
   const gse_row P = ds->P;
   const float M = ds->M;
   const RowCtx c = make_ctx(a, row, P);
-  const int p0 = slice * a.dlen, p1 = min(a.V, p0 + a.dlen);
+  const int p0 = slice * g.len, p1 = min(a.V, p0 + g.len);
   __syncthreads();  // (LDS of the previous item)
   for (int b = tid; b < DNB; b += MT) {
     sh.c.cnt[b] = 0;
@@ -386,6 +421,15 @@ __device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slic
       atomic_add_ag(&gh[DNB + b], sh.c.mass[b]);
     }
   }
+  // Ticket: the row's last slice plans it.
+  store_wait();
+  __syncthreads();
+  if (tid == 0) sh.ticket = ticket_add(&ds->cdone);
+  __syncthreads();
+  if (sh.ticket == (uint32_t)(g.S - 1) && tid < WAVE) {
+    plan_row(gh, ds, a.mode);
+    if (tid == 0) ds->cdone = 0u;
+  }
 }
 
 // Four waves per SIMD: every workgroup of the grid resident at once.
@@ -393,11 +437,9 @@ template <int DT, bool AL>
 __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void deep_count_kernel(ScanArgs a) {
   __shared__ DeepShared sh;
   const int nd = (int)min(a.dctl[0], (uint32_t)DEEP_MAX);
-  const int ni = items_of(a, nd);
-  for (int i = blockIdx.x; i < ni; i += gridDim.x) {
-    int slot, slice;
-    if (item_of(a, i, nd, slot, slice)) count_item<DT, AL>(a, slot, slice, sh);
-  }
+  if (nd == 0) return;
+  const DGeom g = deep_geom(a, nd);
+  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) count_item<DT, AL>(a, i / g.S, i % g.S, g, sh);
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -408,17 +450,18 @@ __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 // equal key width; counts and fixed-point masses, order-independent) gives the rank and exclusive prefix at the head of
 // every sub-bin. The keep cut lies in the last non-empty sub-bin before the first one whose head is cut (s0); the draw
 // in the first sub-bin whose inclusive prefix reaches u * c_last (sj). Only the entries of those two sub-bins are
-// sorted and walked.
+// sorted; their exact prefixes come from one scan of their fixed-point masses.
 
-constexpr int NSB = 256;       // sub-bins (128 per window)
-constexpr int SUBC = 2048;     // entries of one sub-bin that can be collected
+constexpr int NSB = 256;        // sub-bins (128 per window)
+constexpr int SUBC = 2048;      // entries of one sub-bin that can be collected
+constexpr int SW = SUBC / MT;   // sorted entries per thread in the walks
+constexpr uint32_t NONE = 0xFFFFFFFFu;
 
 struct FinShared {
-  uint64_t list[DCAP];         // the window entries (unsorted)
-  uint64_t sub[SUBC];          // the collected entries of one sub-bin, sorted
-  uint32_t scnt[NSB];          // sub-bin counts, then their exclusive prefix
-  uint32_t stop[NSB];          // sub-bin head keys (largest key)
-  uint64_t shi[NSB], slo[NSB]; // sub-bin masses, then their exclusive prefix
+  uint64_t sub[SUBC];           // the collected entries of one sub-bin, sorted
+  uint32_t scnt[NSB];           // sub-bin counts, then their exclusive prefix
+  uint32_t stop[NSB];           // sub-bin head keys (largest key)
+  uint64_t shi[NSB], slo[NSB];  // sub-bin masses
   uint32_t kmax[2], kmin[2];
   uint32_t q[4];
   uint32_t ns;
@@ -427,42 +470,77 @@ struct FinShared {
   uint64_t pub[8];
 };
 
-template <int S>
-__device__ __forceinline__ void sort_sub(int n, FinShared &sh) {
-  const int tid = threadIdx.x;
-  uint64_t v[S];
-#pragma unroll
-  for (int s = 0; s < S; ++s) v[s] = tid * S + s < n ? sh.sub[tid * S + s] : 0ull;
+// Exclusive prefix of two u64 values per thread, in thread order; ta, tb receive the totals.
+__device__ __forceinline__ void excl_scan2(uint64_t &a, uint64_t &b, uint64_t &ta, uint64_t &tb, FinShared &sh) {
+  const uint64_t ia = wave_incl_scan_u64(a), ib = wave_incl_scan_u64(b);
   __syncthreads();
-  sort_regs<S>(v, sh.sub);
-#pragma unroll
-  for (int s = 0; s < S; ++s) sh.sub[tid * S + s] = v[s];
-  __syncthreads();
-}
-
-// Collects the entries of sub-bin sb into sh.sub and sorts them (descending). Returns their number (0 when more than
-// SUBC; the caller then gives up).
-__device__ __forceinline__ int collect_sub(int n, int sb, uint32_t cnt, const uint32_t (&shift)[2], bool sep,
-                                           uint32_t w1lo, float Mf, FinShared &sh) {
-  const int tid = threadIdx.x;
-  if (cnt > (uint32_t)SUBC) return 0;
-  if (tid == 0) sh.ns = 0;
-  __syncthreads();
-  for (int i = tid; i < n; i += MT) {
-    const uint64_t pk = sh.list[i];
-    const uint32_t k = pk_key(pk);
-    const int g = (sep && dbin(fkey_inv(k), Mf) >= w1lo) ? 1 : 0;
-    const int b = g * (NSB / 2) + (int)min((sh.kmax[g] - k) >> shift[g], (uint32_t)(NSB / 2 - 1));
-    if (b == sb) sh.sub[atomicAdd(&sh.ns, 1u)] = pk;
+  if (lane_id() == WAVE - 1) {
+    sh.wred[threadIdx.x >> 6] = ia;
+    sh.wred2[threadIdx.x >> 6] = ib;
   }
   __syncthreads();
-  const int m = (int)cnt;
-  if (m <= MT) sort_sub<1>(m, sh);
-  else sort_sub<SUBC / MT>(m, sh);
-  return m;
+  uint64_t pa = 0, pb = 0, sa = 0, sb = 0;
+  const int w = threadIdx.x >> 6;
+  for (int k = 0; k < NWV; ++k) {
+    pa += k < w ? sh.wred[k] : 0ull;
+    pb += k < w ? sh.wred2[k] : 0ull;
+    sa += sh.wred[k];
+    sb += sh.wred2[k];
+  }
+  a = pa + ia - a;
+  b = pb + ib - b;
+  ta = sa;
+  tb = sb;
+  __syncthreads();
 }
 
-__device__ __forceinline__ void finish_row(const ScanArgs &a, DeepSlot *ds, FinShared &sh) {
+// Sorts sh.sub[0, n) descending (bitonic over the next power of two, zero padded). Rolled loops: it runs once per
+// row, cold, so its code is kept small.
+__device__ __forceinline__ void sort_sub(int n, FinShared &sh) {
+  const int tid = threadIdx.x;
+  int N = 2;
+  while (N < n) N <<= 1;
+  for (int i = n + tid; i < N; i += MT) sh.sub[i] = 0ull;
+  __syncthreads();
+#pragma unroll 1
+  for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll 1
+    for (int j = k >> 1; j > 0; j >>= 1) {
+#pragma unroll 1
+      for (int i = tid; i < N / 2; i += MT) {
+        const int lo = ((i & ~(j - 1)) << 1) | (i & (j - 1)), hi = lo + j;
+        const uint64_t x = sh.sub[lo], y = sh.sub[hi];
+        if ((lo & k) == 0 ? x < y : x > y) {
+          sh.sub[lo] = y;
+          sh.sub[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Sub-bin of a window entry.
+__device__ __forceinline__ int sub_of(uint32_t k, const uint32_t (&shift)[2], bool sep, uint32_t w1lo, float Mf,
+                                      const FinShared &sh) {
+  const int g = (sep && dbin(fkey_inv(k), Mf) >= w1lo) ? 1 : 0;
+  return g * (NSB / 2) + (int)min((sh.kmax[g] - k) >> shift[g], (uint32_t)(NSB / 2 - 1));
+}
+
+__device__ __forceinline__ Fx mass_of(uint32_t key, double M, const double *etab) {
+  return fx_of(exp_nonpos((double)fkey_inv(key) - M, etab));
+}
+
+// What the finish uses of the launch arguments (by value: the pick kernel keeps its arguments in registers).
+struct FinArgs {
+  const uint64_t *lst;  // the row's window list
+  RowInfo *info;
+  int32_t *tokens;
+  int mode;
+};
+
+// (not inlined: its registers are allocated apart from the streaming code of the pick pass)
+__device__ __noinline__ void finish_row(const FinArgs a, DeepSlot *ds, FinShared &sh, const double *etab) {
   const int tid = threadIdx.x;
   const gse_row &P = ds->P;
   const int row = ds->row;
@@ -470,22 +548,20 @@ __device__ __forceinline__ void finish_row(const ScanArgs &a, DeepSlot *ds, FinS
   const double M = (double)Mf;
   const uint32_t w2hi = ds->w2hi, w1lo = ds->w1lo;
   const bool sep = w1lo > w2hi;  // an unlisted gap (region 1) between the draw window and the cut window
-  uint64_t acc[DA_N];
-#pragma unroll
-  for (int k = 0; k < DA_N; ++k) acc[k] = ds->acc[k];
-  const uint32_t nraw = ds->lcnt;
-  const Fx X0{acc[DA_X0HI], acc[DA_X0LO]}, X1{acc[DA_X1HI], acc[DA_X1LO]}, SF{acc[DA_SHI], acc[DA_SLO]};
-  const uint64_t c0 = acc[DA_C0], c1 = acc[DA_C1], tail = acc[DA_C2];
+  const Fx X0{ld_ag(&ds->acc[DA_X0HI]), ld_ag(&ds->acc[DA_X0LO])}, X1{ld_ag(&ds->acc[DA_X1HI]), ld_ag(&ds->acc[DA_X1LO])};
+  const Fx SF = fx_add(fx_add(X0, X1), Fx{ld_ag(&ds->acc[DA_RHI]), ld_ag(&ds->acc[DA_RLO])});
+  const uint64_t c0 = ds->acc[DA_C0], c1 = ds->acc[DA_C1], tail = ds->acc[DA_C2];
+  const uint32_t nraw = ld_ag(&ds->lcnt);
   const double Sd = fx_val(SF);
   const uint64_t K = P.top_k > 0 ? (uint64_t)P.top_k : ~0ull;
   const double topp = P.top_p, minp = P.min_p, q0 = 1.0 / Sd;
   const bool ok0 = nraw > 0 && nraw <= (uint32_t)DCAP && Sd > 0.0;
   const int n = ok0 ? (int)nraw : 0;
-  const uint64_t *lst = a.dlist + (size_t)(ds - a.dslot) * DCAP;
-  // entries into LDS; key ranges of the two windows
+  const uint64_t *lst = a.lst;
+  // key ranges of the two windows
   if (tid < 2) {
     sh.kmax[tid] = 0;
-    sh.kmin[tid] = 0xFFFFFFFFu;
+    sh.kmin[tid] = NONE;
   }
   sh.scnt[tid] = 0;
   sh.stop[tid] = 0;
@@ -493,16 +569,13 @@ __device__ __forceinline__ void finish_row(const ScanArgs &a, DeepSlot *ds, FinS
   sh.slo[tid] = 0;
   __syncthreads();
   for (int i = tid; i < n; i += MT) {
-    const uint64_t pk = lst[i];
-    sh.list[i] = pk;
-    const uint32_t k = pk_key(pk);
+    const uint32_t k = pk_key(ld_ag(&lst[i]));
     const int g = (sep && dbin(fkey_inv(k), Mf) >= w1lo) ? 1 : 0;
     atomicMax(&sh.kmax[g], k);
     atomicMin(&sh.kmin[g], k);
   }
   __syncthreads();
   uint32_t shift[2];
-#pragma unroll
   for (int g = 0; g < 2; ++g) {
     const uint32_t span = sh.kmax[g] >= sh.kmin[g] ? sh.kmax[g] - sh.kmin[g] : 0u;
     uint32_t sft = 0;
@@ -511,12 +584,9 @@ __device__ __forceinline__ void finish_row(const ScanArgs &a, DeepSlot *ds, FinS
   }
   // exact sub-bin counts, masses and head keys
   for (int i = tid; i < n; i += MT) {
-    const uint64_t pk = sh.list[i];
-    const uint32_t k = pk_key(pk);
-    const float z = fkey_inv(k);
-    const int g = (sep && dbin(z, Mf) >= w1lo) ? 1 : 0;
-    const int b = g * (NSB / 2) + (int)min((sh.kmax[g] - k) >> shift[g], (uint32_t)(NSB / 2 - 1));
-    const Fx f = fx_of(exp((double)z - M));
+    const uint32_t k = pk_key(ld_ag(&lst[i]));
+    const int b = sub_of(k, shift, sep, w1lo, Mf, sh);
+    const Fx f = mass_of(k, M, etab);
     atomicAdd(&sh.scnt[b], 1u);
     atomicMax(&sh.stop[b], k);
     atomicAdd((unsigned long long *)&sh.shi[b], (unsigned long long)f.hi);
@@ -528,36 +598,23 @@ __device__ __forceinline__ void finish_row(const ScanArgs &a, DeepSlot *ds, FinS
   const Fx mym{sh.shi[tid], sh.slo[tid]};
   uint64_t ph = mym.hi, pl = mym.lo;
   {
-    const uint64_t ia = wave_incl_scan_u64(ph), ib = wave_incl_scan_u64(pl);
+    uint64_t th, tl;
     const uint32_t ic = wave_incl_scan_u32(mycnt);
-    __syncthreads();
-    if (lane_id() == WAVE - 1) {
-      sh.wred[tid >> 6] = ia;
-      sh.wred2[tid >> 6] = ib;
-      sh.wsum[tid >> 6] = ic;
-    }
-    __syncthreads();
-    uint64_t pa = 0, pb = 0;
+    if (lane_id() == WAVE - 1) sh.wsum[tid >> 6] = ic;
+    excl_scan2(ph, pl, th, tl, sh);  // (its barriers publish wsum)
     uint32_t pc = 0;
-#pragma unroll
-    for (int k = 0; k < NWV; ++k) {
-      pa += k < (tid >> 6) ? sh.wred[k] : 0ull;
-      pb += k < (tid >> 6) ? sh.wred2[k] : 0ull;
-      pc += k < (tid >> 6) ? sh.wsum[k] : 0u;
-    }
-    ph = pa + ia - ph;
-    pl = pb + ib - pl;
+    for (int k = 0; k < NWV; ++k) pc += k < (tid >> 6) ? sh.wsum[k] : 0u;
     sh.scnt[tid] = pc + ic - mycnt;  // (now the exclusive count prefix)
   }
   const bool seg1 = sep && tid >= NSB / 2;
   const Fx pbase = fx_add(fx_add(X0, Fx{ph, pl}), seg1 ? X1 : Fx{0, 0});
   const uint64_t rbase = c0 + sh.scnt[tid] + (seg1 ? c1 : 0ull);
-  if (tid < 4) sh.q[tid] = tid == 1 ? 0u : 0xFFFFFFFFu;
+  if (tid < 4) sh.q[tid] = tid == 1 ? 0u : NONE;
   __syncthreads();
   // s1: the first non-empty sub-bin whose head entry is cut
   if (ok0 && mycnt) {
-    const double e0 = exp((double)fkey_inv(mytop) - M);
-    const bool cut = rbase >= K || (minp > 0.0 && !(fx_val(fx_of(e0)) / Sd >= minp * q0)) || fx_val(pbase) / Sd >= topp;
+    const Fx f0 = mass_of(mytop, M, etab);
+    const bool cut = rbase >= K || (minp > 0.0 && !(fx_val(f0) / Sd >= minp * q0)) || fx_val(pbase) / Sd >= topp;
     if (cut) atomicMin(&sh.q[0], (uint32_t)tid);
   }
   __syncthreads();
@@ -566,128 +623,162 @@ __device__ __forceinline__ void finish_row(const ScanArgs &a, DeepSlot *ds, FinS
   if (ok0 && mycnt && (uint32_t)tid < s1) atomicMax(&sh.q[1], (uint32_t)tid + 1u);
   __syncthreads();
   const int s0 = (int)sh.q[1] - 1;
-  bool ok = ok0 && s0 >= 0;
-  if (ok && tid == s0) {
+  if (ok0 && s0 >= 0 && tid == s0) {
     sh.pub[0] = rbase;
     sh.pub[1] = pbase.hi;
     sh.pub[2] = pbase.lo;
     sh.pub[3] = mycnt;
     sh.pub[4] = seg1 ? 1u : 0u;
   }
-  if (ok && s1 != 0xFFFFFFFFu && tid == (int)s1) sh.pub[5] = rbase;
+  if (ok0 && s1 != NONE && tid == (int)s1) sh.pub[5] = rbase;
   __syncthreads();
-  // walk s0's sorted entries: the last kept entry and c_last
-  double clast = 0.0;
+  bool ok = ok0 && s0 >= 0;
+  const uint64_t r_s1 = sh.pub[5];
+  const bool g0 = sh.pub[4] != 0;
+  // Two walks over the sorted entries of one sub-bin, with exact prefixes: walk 0 finds the first cut entry of s0 (the
+  // last kept entry is the one before it, c_last its inclusive prefix), walk 1 the first entry of sj whose inclusive
+  // prefix reaches u * c_last (the token).
+  uint64_t r0 = sh.pub[0];
+  Fx base{sh.pub[1], sh.pub[2]};
+  uint32_t cnt = (uint32_t)sh.pub[3];
+  int sb = s0;
+  double clast = 0.0, thr = 0.0;
   uint64_t kkeep = 0;
-  if (ok) {
-    const uint64_t r0 = sh.pub[0];
-    const Fx b0{sh.pub[1], sh.pub[2]};
-    const uint32_t cnt0 = (uint32_t)sh.pub[3];
-    const bool g0 = sh.pub[4] != 0;
-    const uint64_t r_s1 = sh.pub[5];
-    const int m0 = collect_sub(n, s0, cnt0, shift, sep, w1lo, Mf, sh);
-    ok = m0 == (int)cnt0;
-    if (ok && tid == 0) {
-      // sequential over the (few) entries of one sub-bin: exact prefixes in sorted order
-      Fx A = b0;
-      int last = m0 - 1;  // the last kept entry, unless a cut falls inside the sub-bin
-      bool inside = false;
-      for (int k = 0; k < m0; ++k) {
-        const double e = exp((double)fkey_inv(pk_key(sh.sub[k])) - M);
-        const Fx f = fx_of(e);
-        const bool cut = r0 + (uint64_t)k >= K || (minp > 0.0 && !(fx_val(f) / Sd >= minp * q0)) ||
-                         fx_val(A) / Sd >= topp;
-        if (cut) {
-          last = k - 1;
-          inside = true;
-          break;
-        }
-        A = fx_add(A, f);
-        if (k == m0 - 1) break;
-      }
-      // A = exclusive prefix of entry last + 1 = inclusive prefix of entry last
-      bool good = last >= 0;
-      if (good && !inside) {
-        // the next rank is s1's head (cut by definition) when directly adjacent, else past the list
-        const uint64_t rl = r0 + (uint64_t)last;
-        if (s1 != 0xFFFFFFFFu) {
-          good = r_s1 == rl + 1;
-        } else {
-          const uint64_t after = (!sep || g0) ? tail : c1 + tail;
-          good = after == 0 || rl + 1 >= K || fx_val(A) / Sd >= topp;
-        }
-      }
-      sh.pub[6] = good ? 1u : 0u;
-      sh.pub[1] = A.hi;
-      sh.pub[2] = A.lo;
-      sh.pub[7] = good ? sh.sub[last] : 0ull;
-    }
-    __syncthreads();
-    ok = ok && sh.pub[6] != 0;
-    if (ok) {
-      clast = fx_val(Fx{sh.pub[1], sh.pub[2]}) / Sd;
-      kkeep = sh.pub[7];
-    }
-  }
-  __syncthreads();
   int32_t tok = -1;
-  if (ok && a.mode == MODE_SAMPLE) {
-    // sj: the first non-empty sub-bin whose last entry's inclusive prefix reaches u * c_last; its head's exclusive
-    // prefix must be below it (else the draw falls in an unlisted region)
-    const double thr = ds->u * clast;
-    if (tid == 0) sh.q[2] = 0xFFFFFFFFu;
-    __syncthreads();
-    if (mycnt && fx_val(fx_add(pbase, mym)) / Sd >= thr) atomicMin(&sh.q[2], (uint32_t)tid);
-    __syncthreads();
-    const uint32_t sj = sh.q[2];
-    if (sj != 0xFFFFFFFFu && tid == (int)sj) {
-      sh.pub[0] = pbase.hi;
-      sh.pub[1] = pbase.lo;
-      sh.pub[3] = mycnt;
-    }
-    __syncthreads();
-    ok = sj != 0xFFFFFFFFu && !(fx_val(Fx{sh.pub[0], sh.pub[1]}) / Sd >= thr);
-    if (ok) {
-      const uint32_t cj = (uint32_t)sh.pub[3];
-      const Fx bj{sh.pub[0], sh.pub[1]};
-      const int mj = collect_sub(n, (int)sj, cj, shift, sep, w1lo, Mf, sh);
-      ok = mj == (int)cj;
-      if (ok && tid == 0) {
-        Fx A = bj;
-        int j = -1;
-        for (int k = 0; k < mj; ++k) {
-          A = fx_add(A, fx_of(exp((double)fkey_inv(pk_key(sh.sub[k])) - M)));
-          if (fx_val(A) / Sd >= thr) {
-            j = k;
-            break;
-          }
-        }
-        sh.pub[5] = j >= 0 ? (uint64_t)pk_id(sh.sub[j]) : 0xFFFFFFFFFFFFFFFFull;
+#pragma unroll 1
+  for (int w = 0; w < 2 && ok; ++w) {
+    if (w == 1) {
+      if (a.mode != MODE_SAMPLE) break;
+      // sj: the first non-empty sub-bin whose inclusive prefix reaches u * c_last; its head's exclusive prefix must be
+      // below it (else the draw falls in an unlisted region)
+      thr = ds->u * clast;
+      if (mycnt && fx_val(fx_add(pbase, mym)) / Sd >= thr) atomicMin(&sh.q[2], (uint32_t)tid);
+      __syncthreads();
+      const uint32_t sj = sh.q[2];
+      if (sj != NONE && tid == (int)sj) {
+        sh.pub[0] = pbase.hi;
+        sh.pub[1] = pbase.lo;
+        sh.pub[3] = mycnt;
       }
       __syncthreads();
-      ok = ok && sh.pub[5] != 0xFFFFFFFFFFFFFFFFull;
-      if (ok) tok = (int32_t)sh.pub[5];
+      base = Fx{sh.pub[0], sh.pub[1]};
+      cnt = (uint32_t)sh.pub[3];
+      ok = sj != NONE && !(fx_val(base) / Sd >= thr);
+      if (!ok) break;
+      sb = (int)sj;
     }
-  }
-  __syncthreads();
-  if (tid == 0) {
+    // collect the sub-bin's entries (in list order) and sort them
+    if (cnt > (uint32_t)SUBC) {
+      ok = false;
+      break;
+    }
+    if (tid == 0) sh.ns = 0;
+    __syncthreads();
+    for (int i = tid; i < n; i += MT) {
+      const uint64_t pk = ld_ag(&lst[i]);
+      if (sub_of(pk_key(pk), shift, sep, w1lo, Mf, sh) == sb) {
+        const uint32_t pos = atomicAdd(&sh.ns, 1u);
+        if (pos < (uint32_t)SUBC) sh.sub[pos] = pk;
+      }
+    }
+    __syncthreads();
+    if (sh.ns != cnt) {
+      ok = false;
+      break;
+    }
+    const int m = (int)cnt;
+    sort_sub(m, sh);
+    // exclusive prefix at entry tid * SW, then the first entry that meets the walk's test
+    uint64_t hi = 0, lo = 0, thi, tlo;
+#pragma unroll 1
+    for (int i = 0; i < SW; ++i) {
+      const int k = tid * SW + i;
+      if (k < m) {
+        const Fx f = mass_of(pk_key(sh.sub[k]), M, etab);
+        hi += f.hi;
+        lo += f.lo;
+      }
+    }
+    excl_scan2(hi, lo, thi, tlo, sh);
+    if (tid == 0) sh.q[3] = NONE;
+    __syncthreads();
+    Fx A = fx_add(base, Fx{hi, lo});
+    uint32_t kc = NONE;
+#pragma unroll 1
+    for (int i = 0; i < SW; ++i) {
+      const int k = tid * SW + i;
+      if (k >= m) break;
+      const Fx f = mass_of(pk_key(sh.sub[k]), M, etab);
+      const Fx Ai = fx_add(A, f);
+      const bool hit = w == 0 ? (r0 + (uint64_t)k >= K || (minp > 0.0 && !(fx_val(f) / Sd >= minp * q0)) ||
+                                 fx_val(A) / Sd >= topp)
+                              : fx_val(Ai) / Sd >= thr;
+      if (hit) {
+        kc = (uint32_t)k;
+        break;
+      }
+      A = Ai;
+    }
+    kc = wave_min_u32(kc);
+    if (lane_id() == 0 && kc != NONE) atomicMin(&sh.q[3], kc);
+    __syncthreads();
+    kc = sh.q[3];
+    if (w == 1) {
+      ok = kc != NONE;
+      if (ok) tok = (int32_t)pk_id(sh.sub[kc]);
+      break;
+    }
+    // walk 0: the last kept entry and its inclusive prefix (the exclusive prefix of the first cut entry, or the
+    // sub-bin's total)
+    const bool inside = kc != NONE;
+    const int last = inside ? (int)kc - 1 : m - 1;
+    if (inside && tid == (int)(kc / SW)) {
+      sh.pub[6] = A.hi;  // (the thread stopped at kc: A is its exclusive prefix)
+      sh.pub[7] = A.lo;
+    }
+    __syncthreads();
+    const Fx Al = inside ? Fx{sh.pub[6], sh.pub[7]} : fx_add(base, Fx{thi, tlo});
+    bool good = last >= 0;
+    if (good && !inside) {
+      // the next rank is s1's head (cut by definition) when directly adjacent, else past the list
+      const uint64_t rl = r0 + (uint64_t)last;
+      if (s1 != NONE) {
+        good = r_s1 == rl + 1;
+      } else {
+        const uint64_t after = (!sep || g0) ? tail : c1 + tail;
+        good = after == 0 || rl + 1 >= K || fx_val(Al) / Sd >= topp;
+      }
+    }
+    ok = good;
     if (ok) {
-      RowInfo *ri = a.info + row;
-      RowInfo r = {};
-      r.cmax = ri->cmax;
-      r.kkeep = kkeep;
-      r.S = Sd;
-      r.Z = clast;
-      r.flags = R_DONE | R_BY_DEEP;
-      r.token = tok;
-      *ri = r;
-      if (a.mode == MODE_SAMPLE) a.tokens[row] = tok;
+      clast = fx_val(Al) / Sd;
+      kkeep = sh.sub[last];
     }
+    __syncthreads();  // (sh.pub, sh.sub before walk 1)
+  }
+  if (tid == 0 && ok) {
+    RowInfo *ri = a.info + row;
+    RowInfo r = {};
+    r.cmax = ri->cmax;
+    r.kkeep = kkeep;
+    r.S = Sd;
+    r.Z = clast;
+    r.flags = R_DONE | R_BY_DEEP;
+    r.token = tok;
+    *ri = r;
+    if (a.mode == MODE_SAMPLE) a.tokens[row] = tok;
   }
 }
 
+union PickShared {
+  DeepShared d;
+  FinShared f;
+};
+
 template <int DT, bool AL>
-__device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice, DeepShared &sh) {
+__device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice, const DGeom &g, PickShared &ps,
+                                          const double *etab) {
+  DeepShared &sh = ps.d;
   const int tid = threadIdx.x;
   DeepSlot *ds = a.dslot + slot;
   const int row = ds->row;
@@ -695,95 +786,87 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
   const float Mf = ds->M;
   const double M = (double)Mf;
   const RowCtx c = make_ctx(a, row, P);
-  const int p0 = slice * a.dlen, p1 = min(a.V, p0 + a.dlen);
+  const int p0 = slice * g.len, p1 = min(a.V, p0 + g.len);
+  // the plan (written by the count launch)
+  const uint32_t w2lo = ds->w2lo, w2hi = ds->w2hi, w1lo = ds->w1lo, w1hi = ds->w1hi;
+  const bool planned = ds->status == DS_PLANNED;
   __syncthreads();  // (LDS of the previous item)
   if (tid == 0) sh.nwl = 0;
-  uint64_t acc[DA_N];
+  if (planned) {
+    // per lane, exact fixed-point masses of three regions (before the draw window, between the windows, the rest):
+    // whole multiples of 2^-40 and 2^-64, summed in fp64 (exact below 2^53)
+    double h0 = 0.0, l0 = 0.0, h1 = 0.0, l1 = 0.0, h2 = 0.0, l2 = 0.0;
+    stream_slice<DT, AL>(a, c, row, p0, p1, sh, []() {}, [&](float z, int t, bool ok) __attribute__((always_inline)) {
+      bool inw = false;
+      if (ok && z > -INFINITY) {
+        const uint32_t b = dbin(z, Mf);
+        const double s = exp_nonpos((double)z - M, etab) * 1099511627776.0;  // 2^40
+        const double hi = floor(s), lo = floor((s - hi) * 16777216.0);  // (fx_of)
+        if (b < w2lo) {
+          h0 += hi;
+          l0 += lo;
+        } else if (b > w2hi && b < w1lo) {
+          h1 += hi;
+          l1 += lo;
+        } else {
+          h2 += hi;
+          l2 += lo;
+          inw = b <= w1hi;
+        }
+      }
+      if (inw) {
+        const uint32_t pos = atomicAdd(&sh.nwl, 1u);
+        if (pos < (uint32_t)WLC) sh.wl[pos] = pack(fkey(z), (uint32_t)t);
+      }
+    });
+    // the slice's sums into the row record (per wave; integer adds, any order), its window elements into the row list
+    const uint64_t hv[6] = {(uint64_t)h0, (uint64_t)l0, (uint64_t)h1, (uint64_t)l1, (uint64_t)h2, (uint64_t)l2};
 #pragma unroll
-  for (int k = 0; k < DA_N; ++k) acc[k] = 0;
-  uint32_t w2lo = 0, w2hi = 0, w1lo = 0, w1hi = 0;
-  bool planned = false;
-  auto pre = [&]() __attribute__((always_inline)) {
-    plan_row(a, ds, P, Mf, slice == 0, sh);
-    w2lo = sh.plan[0];
-    w2hi = sh.plan[1];
-    w1lo = sh.plan[2];
-    w1hi = sh.plan[3];
-    planned = sh.plan[4] == DS_PLANNED;
-  };
-  stream_slice<DT, AL>(a, c, row, p0, p1, sh, pre, [&](float z, int t, bool ok) __attribute__((always_inline)) {
-    const bool live = planned && ok && z > -INFINITY;
-    bool inw = false;
-    if (live) {
-      const uint32_t b = dbin(z, Mf);
-      const Fx f = fx_of(exp((double)z - M));
-      acc[DA_SHI] += f.hi;
-      acc[DA_SLO] += f.lo;
-      if (b < w2lo) {
-        acc[DA_X0HI] += f.hi;
-        acc[DA_X0LO] += f.lo;
-        acc[DA_C0] += 1;
-      } else if (b > w2hi && b < w1lo) {
-        acc[DA_X1HI] += f.hi;
-        acc[DA_X1LO] += f.lo;
-        acc[DA_C1] += 1;
-      } else if (b > w1hi) {
-        acc[DA_C2] += 1;
-      } else {
-        inw = true;
+    for (int k = 0; k < 6; ++k) {
+      const uint64_t v = wave_sum_u64(hv[k]);
+      if (lane_id() == 0 && v) atomic_add_ag(&ds->acc[DA_X0HI + k], v);
+    }
+    const uint32_t nw = sh.nwl;
+    if (tid == 0 && nw) {
+      // a slice with more window elements than it can hold spoils the row's count (the row takes the exact path)
+      const uint32_t add = nw <= (uint32_t)WLC ? nw : (uint32_t)DCAP + 1u;
+      sh.wbase = __hip_atomic_fetch_add(&ds->lcnt, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (nw && nw <= (uint32_t)WLC) {
+      uint64_t *lst = a.dlist + (size_t)slot * DCAP;
+      for (uint32_t i = tid; i < nw; i += MT) {
+        const uint32_t pos = sh.wbase + i;
+        if (pos < (uint32_t)DCAP) st_ag(&lst[pos], sh.wl[i]);
       }
     }
-    if (inw) {
-      const uint32_t pos = atomicAdd(&sh.nwl, 1u);
-      if (pos < (uint32_t)WLC) sh.wl[pos] = pack(fkey(z), (uint32_t)t);
-    }
-  });
-  // the slice's sums into the row record (per wave; integer adds, any order), its window elements into the row list
-#pragma unroll
-  for (int k = 0; k < DA_N; ++k) {
-    const uint64_t v = wave_sum_u64(acc[k]);
-    if (lane_id() == 0 && v) atomic_add_ag(&ds->acc[k], v);
   }
-  const uint32_t nw = sh.nwl;
-  if (tid == 0 && nw) {
-    // a slice with more window elements than it can hold spoils the row's count (the row takes the exact path)
-    const uint32_t add = nw <= (uint32_t)WLC ? nw : (uint32_t)DCAP + 1u;
-    sh.wbase = __hip_atomic_fetch_add(&ds->lcnt, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  // Ticket: the row's last slice finishes it, then clears the row's records for the next call.
+  store_wait();
   __syncthreads();
-  if (nw && nw <= (uint32_t)WLC) {
-    uint64_t *lst = a.dlist + (size_t)slot * DCAP;
-    for (uint32_t i = tid; i < nw; i += MT) {
-      const uint32_t pos = sh.wbase + i;
-      if (pos < (uint32_t)DCAP) st_ag(&lst[pos], sh.wl[i]);
-    }
+  if (tid == 0) sh.ticket = ticket_add(&ds->pdone);
+  __syncthreads();
+  if (sh.ticket != (uint32_t)(g.S - 1)) return;
+  if (planned) finish_row(FinArgs{a.dlist + (size_t)slot * DCAP, a.info, a.tokens, a.mode}, ds, ps.f, etab);
+  __syncthreads();  // (every thread has read the row's sums)
+  uint64_t *gh = a.dhist + (size_t)slot * 2 * DNB;
+  for (int b = tid; b < 2 * DNB; b += MT) gh[b] = 0;
+  if (tid < DA_N) ds->acc[tid] = 0;
+  if (tid == 0) {
+    ds->lcnt = 0;
+    ds->pdone = 0;
   }
 }
 
 template <int DT, bool AL>
 __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void deep_pick_kernel(ScanArgs a) {
-  __shared__ DeepShared sh;
+  __shared__ PickShared sh;
+  __shared__ double etab[64];
   const int nd = (int)min(a.dctl[0], (uint32_t)DEEP_MAX);
-  const int ni = items_of(a, nd);
-  for (int i = blockIdx.x; i < ni; i += gridDim.x) {
-    int slot, slice;
-    if (item_of(a, i, nd, slot, slice)) pick_item<DT, AL>(a, slot, slice, sh);
-  }
-}
-
-// One workgroup per deep row: the finish, and the row's histogram cleared for the next call.
-__global__ __launch_bounds__(MT) void deep_finish_kernel(ScanArgs a) {
-  __shared__ FinShared sh;
-  const int nd = (int)min(a.dctl[0], (uint32_t)DEEP_MAX);
-  const int slot = blockIdx.x;
-  if (slot >= nd) return;
-  DeepSlot *ds = a.dslot + slot;
-  uint64_t *gh = a.dhist + (size_t)slot * 2 * DNB;
-  for (int b = threadIdx.x; b < 2 * DNB; b += MT) gh[b] = 0;
-  if (ds->status == DS_PLANNED) finish_row(a, ds, sh);
-  __syncthreads();  // (every thread has read the row's sums)
-  if (threadIdx.x < DA_N) ds->acc[threadIdx.x] = 0;
-  if (threadIdx.x == 0) ds->lcnt = 0;
+  if (nd == 0) return;
+  if (threadIdx.x < 64) etab[threadIdx.x] = EXP2_64[threadIdx.x];  // (published by the first barrier of an item)
+  const DGeom g = deep_geom(a, nd);
+  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) pick_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab);
 }
 
 template <int DT, bool AL>
@@ -791,7 +874,6 @@ void launch_all(const ScanArgs &a, hipStream_t s) {
   dim3 grid((unsigned)a.dgrid), block(MT);
   hipLaunchKernelGGL((deep_count_kernel<DT, AL>), grid, block, 0, s, a);
   hipLaunchKernelGGL((deep_pick_kernel<DT, AL>), grid, block, 0, s, a);
-  hipLaunchKernelGGL(deep_finish_kernel, dim3((unsigned)min(a.rows, DEEP_MAX)), block, 0, s, a);
 }
 
 }  // namespace

@@ -53,7 +53,7 @@ static_assert(sizeof(SliceRec) == 64, "");
 
 // Split-row finish of deep rows (gse_deep.hip).
 constexpr int DEEP_MAX = 128;  // deep rows per call (more: the exact path takes them)
-constexpr int DSMAX = 32;      // slices per deep row
+constexpr int DSMAX = 64;      // slices per deep row, at most
 constexpr int DNB = 512;       // histogram bins of d = z_max - z, 1/32 wide (the last one open-ended)
 constexpr int DCAP = 8192;     // window elements listed per deep row
 
@@ -62,9 +62,9 @@ enum : uint32_t { DS_PENDING = 0u, DS_PLANNED = 1u, DS_FAIL = 2u };
 enum {  // DeepSlot.acc: exact fixed-point sums of the pick pass (hi: 2^-40 units, lo: 2^-64 units) and counts
   DA_X0HI, DA_X0LO,  // bins before the draw window
   DA_X1HI, DA_X1LO,  // bins strictly between the two windows
-  DA_SHI, DA_SLO,    // every element (S)
-  DA_C0, DA_C1,      // element counts of those two regions
-  DA_C2,             // elements after the cut window
+  DA_RHI, DA_RLO,    // the other bins (the windows and after)
+  DA_C0, DA_C1,      // element counts of the first two regions (from the count pass)
+  DA_C2,             // elements after the cut window (from the count pass)
   DA_N
 };
 
@@ -75,7 +75,8 @@ struct DeepSlot {    // 256 bytes, one per deep row of a call
   double u;          // the draw's uniform
   uint32_t status;   // DS_*, written by the planner
   uint32_t w2lo, w2hi, w1lo, w1hi;  // bin windows holding the draw and the last kept element (inclusive)
-  uint32_t lcnt, pad0[2];           // listed window elements
+  uint32_t lcnt;                    // listed window elements
+  uint32_t cdone, pdone;            // slice tickets of the two passes (zero between calls)
   uint64_t acc[DA_N];               // pick-pass sums (atomic adds; zero between calls)
   uint64_t pad[8];
 };
@@ -118,7 +119,7 @@ struct ScanArgs {
   DeepSlot *dslot;   // [DEEP_MAX]
   uint64_t *dhist;   // [DEEP_MAX][2][DNB]: per bin, element count and fixed-point mass (2^-40 units), atomic adds
   uint64_t *dlist;   // [DEEP_MAX][DCAP]: packed keys of the window elements
-  int dslices, dlen, dgrid;  // slices per deep row, tokens per slice (a multiple of 1024), workgroups per pass
+  int dslices, dgrid;  // split-row finish enabled (slices per deep row, at most), workgroups per pass
 };
 
 hipError_t launch_main(const ScanArgs &a, hipStream_t s);
