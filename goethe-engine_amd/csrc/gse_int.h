@@ -14,6 +14,7 @@ enum : uint32_t {
   F_FINITE = 2u,    // a finite value after the mask (sampling.py:75)
   F_OVERFLOW = 4u,  // a wave's candidate list did not fit
   F_HOVER = 8u,     // a part with more distinct history ids than its count table holds
+  F_PINF = 16u,     // +inf as the part maximum of z (x = +inf, or x / T overflowing): the exact path decides
 };
 
 enum : uint32_t {

@@ -321,8 +321,12 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   const uint64_t gtop = sh.rtop;  // greedy argmax; or, for a row without z > -inf, the lowest id of its -inf
   const bool bad = (flags & F_NAN) || !(flags & F_FINITE);
 
-  if ((flags & F_HOVER) && (greedy || bad)) {
-    // more distinct history ids than a part can count: the exact path redoes the whole row (flags, argmax, logprobs)
+  // z = x / T: no finite z over the allowed tokens may still hide a finite x whose quotient overflowed
+  const bool divide = !greedy && P.temperature != 1.0f;
+  if (((flags & F_HOVER) && (greedy || bad)) ||
+      (((flags & F_PINF) || (divide && !(flags & F_FINITE))) && !(flags & F_NAN))) {
+    // more distinct history ids than a part can count, or a maximum of z that is not finite (the parts do not know
+    // whether a finite x exists): the exact path redoes the whole row (flags, argmax, logprobs)
     if (tid == 0) set_info(ri, gtop, 0, 0.0, 0.0, R_HARD | R_FULL | (greedy ? R_GREEDY : 0u), -1);
     return;
   }
@@ -471,54 +475,91 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
 // ---------------------------------------------------------------------------------------------------------------------
 // Part streaming.
 //
-// The stream carries every token of the part except the tokens of the row's history: those (at most a few hundred per
-// part) are penalized, masked and divided by a side pass with exactly the same arithmetic, and enter the same running
-// state out of order. The stream itself then needs no per-element branch: the mask and the history exclusion are one
-// bit select per element, the listing is skipped for a whole chunk when the lane maxima lie below the threshold, and
-// the unlisted exp terms are summed in fp32 per chunk.
+// The stream carries every token of the part below pv (the part end, rounded down to a whole vector for aligned rows)
+// except the tokens of the row's history: those (at most a few hundred per part) and the ragged tokens [pv, p1) are
+// penalized and masked by a side pass with exactly the same arithmetic, and enter the same running state out of order.
+// Every chunk issues the same loads (a vector past pv loads the row's first vector and is ignored), so the compiler
+// can count the loads in flight: each wave keeps two chunks loading while it works on a third. The stream needs no
+// per-element branch: the mask and the history exclusion are one bit select per element, the listing is skipped for a
+// whole chunk when the lane maxima lie below the threshold, and the unlisted terms are summed in fp32 per chunk.
 
 // Per-lane running state of a wave.
 struct Run {
   float m;         // running maximum of this lane's z
   double s;        // sum of this lane's unlisted exp(z - m) (fp32 terms)
   double b;        // its error bound
-  uint32_t kap;    // the wave's listing threshold key in force (uniform in the wave; only rises)
+  uint32_t kap;    // the wave's listing threshold key (uniform in the wave; only rises)
   uint32_t woff;   // elements the wave has listed (uniform)
   float g;         // greedy rows: largest nan_to_num(x) so far, at the lowest token gid holding it
   uint32_t gid;
   uint32_t fid;    // lowest token of this lane with z not NaN (found in the lane's first chunk)
-  float fin;       // smallest |x| after the mask: the row has a finite value iff some lane's fin is finite
   uint64_t nanm;   // lanes that saw a NaN before the mask (wave-uniform)
 };
 
 constexpr int KH = HMAX / MT;  // history tokens a thread carries in the side pass
 
-// z of one chunk in place: the mask and the history exclusion (one select), the NaN and finiteness flags, the
-// division by T (div_exact), the lane's chunk maximum; greedy rows track the first maximum of nan_to_num(x).
 // Selects x where bit k of keep is set, -inf elsewhere: one bit-field insert (v_bfi_b32).
 __device__ __forceinline__ float keep_or_ninf(float x, uint32_t keep, int k) {
   const uint32_t sel = (uint32_t)(((int32_t)(keep << (31 - k))) >> 31);  // all ones when bit k is set
   return __uint_as_float((__float_as_uint(x) & sel) | (0xFF800000u & ~sel));
 }
 
-template <int DT, bool MASKED, bool GREEDY, bool DIV>
-__device__ __forceinline__ float stream_z(const RowCtx &c, int cb, int p0, int p1, float (&xr)[EPL],
-                                          const uint32_t (&mw)[Lay<DT>::NV], const HistTab &h, Run &rn, float *proc) {
+// One chunk's logits and mask words, with the same loads for every chunk: a vector that does not lie below pv loads
+// the row's first vector instead (aligned rows); unaligned rows load element by element, clamped to the part.
+template <int DT, bool AL, bool MASKED>
+__device__ __forceinline__ void load_u(const RowCtx &c, int cb, int pv, int p1, float (&x)[EPL],
+                                       uint32_t (&mw)[Lay<DT>::NV]) {
   using L = Lay<DT>;
-  constexpr uint32_t VMASK = (1u << L::VEC) - 1u;
   const int l = lane_id();
-  const bool tail = cb + CHK > p1;
-  // per vector: the lane's history bits (tokens that the side pass takes) and in-range bits
-  uint32_t hb[L::NV], inr[L::NV];
 #pragma unroll
   for (int v = 0; v < L::NV; ++v) {
     const int t0 = cb + v * L::STRIDE + l * L::VEC;
-    hb[v] = 0;
-    if (c.pen) {
-      const int o = min(t0, p1 - 1) - p0;  // (a vector past the part end reads a valid word; its bits are cleared)
-      hb[v] = (h.bits[o >> 5] >> (o & 31)) & VMASK;
+    if constexpr (MASKED) mw[v] = c.mw[min(t0, p1 - 1) >> 5];
+    if constexpr (AL) {
+      const int ts = t0 + L::VEC <= pv ? t0 : 0;
+      if constexpr (DT == GSE_F32) {
+        const float4 f = *reinterpret_cast<const float4 *>((const float *)c.base + ts);
+        x[4 * v] = f.x;
+        x[4 * v + 1] = f.y;
+        x[4 * v + 2] = f.z;
+        x[4 * v + 3] = f.w;
+      } else {
+        const uint4 u = *reinterpret_cast<const uint4 *>((const uint16_t *)c.base + ts);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[8 * v + 2 * i] = __uint_as_float(w[i] << 16);
+          x[8 * v + 2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < L::VEC; ++k) x[v * L::VEC + k] = load_one(c, min(t0 + k, p1 - 1));
     }
-    inr[v] = (tail ? (t0 >= p1 ? 0u : (t0 + L::VEC <= p1 ? VMASK : (1u << (p1 - t0)) - 1u)) : VMASK) & ~hb[v];
+  }
+}
+
+// z of one chunk in place: the mask and the history exclusion (one select; -inf for tokens the stream does not carry),
+// the NaN flag (every loaded value is one of the row's own, so any NaN seen is the row's), the division by T
+// (div_exact), the lane's chunk maximum; greedy rows track the first maximum of nan_to_num(x).
+template <int DT, bool AL, bool MASKED, bool GREEDY, bool DIV>
+__device__ __forceinline__ float chunk_z(const RowCtx &c, int cb, int p0, int pv, int p1, float (&xr)[EPL],
+                                         const uint32_t (&mw)[Lay<DT>::NV], const HistTab &h, Run &rn, float *proc) {
+  using L = Lay<DT>;
+  constexpr uint32_t VMASK = (1u << L::VEC) - 1u;
+  const int l = lane_id();
+  uint32_t inr[L::NV];
+#pragma unroll
+  for (int v = 0; v < L::NV; ++v) {
+    const int t0 = cb + v * L::STRIDE + l * L::VEC;
+    uint32_t in;
+    if constexpr (AL) in = t0 + L::VEC <= pv ? VMASK : 0u;
+    else in = t0 + L::VEC <= pv ? VMASK : (t0 >= pv ? 0u : (1u << (pv - t0)) - 1u);
+    if (c.pen) {
+      const int o = min(t0, p1 - 1) - p0;  // (a vector past the end reads a valid word; its bits are cleared)
+      in &= ~(h.bits[o >> 5] >> (o & 31));
+    }
+    inr[v] = in & VMASK;
   }
   if (proc) {  // processed logits (after penalties and mask, before T) of the streamed tokens
 #pragma unroll
@@ -534,14 +575,13 @@ __device__ __forceinline__ float stream_z(const RowCtx &c, int cb, int p0, int p
 #pragma unroll
   for (int v = 0; v < L::NV; ++v) {
     const int t0 = cb + v * L::STRIDE + l * L::VEC;
-    const uint32_t keep = (MASKED ? (mw[v] >> ((l * L::VEC) & 31)) & VMASK : VMASK) & inr[v];
+    const uint32_t keep = (MASKED ? (mw[v] >> ((l * L::VEC) & 31)) : VMASK) & inr[v];
 #pragma unroll
     for (int k = 0; k < L::VEC; ++k) {
       const int i = v * L::VEC + k;
       const float x = xr[i];
-      rn.nanm |= ballot64(x != x);  // (past the end x = 0)
+      rn.nanm |= ballot64(x != x);
       const float xm = keep_or_ninf(x, keep, k);
-      rn.fin = fminf(rn.fin, fabsf(xm));
       if constexpr (GREEDY) {  // masked tokens take part in the argmax as -FLT_MAX
         const float g = fminf(fmaxf(xm, -FLTMAX), FLTMAX);
         if (((inr[v] >> k) & 1u) && xm == xm && (g > rn.g || rn.gid == 0xFFFFFFFFu)) {
@@ -578,11 +618,11 @@ __device__ __forceinline__ float pairwise(F &f) {
   }
 }
 
-// The lane maximum, the threshold valve, the unlisted exp terms (fp32 per chunk, fp64 across chunks), the listing.
-// tok(i) gives the token of slot i.
+// The lane maximum, the threshold valve, the unlisted terms exp2(t), t = (z - m) log2(e) (fp32 per chunk, fp64 across
+// chunks), the listing. tok(i) gives the token of slot i.
 template <int N, typename Tok>
-__device__ __forceinline__ void stream_sum(const ScanArgs &a, int row, int wl, float cmax, const float (&zr)[N],
-                                           Run &rn, Tok tok) {
+__device__ __forceinline__ void chunk_sum(const ScanArgs &a, int row, int wl, float cmax, const float (&zr)[N],
+                                          Run &rn, Tok tok) {
   static_assert((N & (N - 1)) == 0 && N <= 256, "");
   const float mnew = fmaxf(rn.m, cmax);
   if (rn.woff > (uint32_t)(CAPW / 2)) rn.kap = max(rn.kap, wave_kth_largest_u16(fkey(mnew) >> 16, KV) << 16);
@@ -593,11 +633,11 @@ __device__ __forceinline__ void stream_sum(const ScanArgs &a, int row, int wl, f
     rn.b *= f;
   }
   rn.m = mnew;
-  // -inf (masked, excluded) gives t = -inf, e = 0 and 0 * 1e4 in the moment
+  // -inf (masked, excluded) gives t = -256 and e = 0
   float e[N], t[N];
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    t[i] = (zr[i] - mnew) * LOG2E;
+    t[i] = fmaxf((zr[i] - mnew) * LOG2E, -256.0f);
     e[i] = __builtin_amdgcn_exp2f(t[i]);
   }
   if (ballot64(cmax >= tauf)) {  // some lane holds an element at or above the threshold: list them (they leave the sum)
@@ -620,67 +660,60 @@ __device__ __forceinline__ void stream_sum(const ScanArgs &a, int row, int wl, f
   }
   float mom = 0.0f;
 #pragma unroll
-  for (int i = 0; i < N; ++i) mom = fmaf(e[i], fminf(-t[i], 1.0e4f), mom);
+  for (int i = 0; i < N; ++i) mom = fmaf(e[i], t[i], mom);
   auto term = [&](auto ic) __attribute__((always_inline)) { return e[decltype(ic)::value]; };
   float s = pairwise<0, N>(term);
   if (!(fabsf(mnew) < INFINITY)) {  // nothing above -inf yet (or +inf): no sum
     s = 0.0f;
     mom = 0.0f;
   }
-  // error bound: v_exp_f32 (2 ulp), the argument's three roundings (2.6 ulp of |t|, times ln 2), log2(N) fp32 pairwise
-  // additions; flushed subnormal results
+  // error bound: v_exp_f32 (2 ulp), log2(N) fp32 pairwise additions, flushed subnormal results; the exponent's three
+  // roundings (3 ulp of |t|, times ln 2; mom = -sum e |t|)
   constexpr double LV = N >= 16 ? 4.0 : N >= 8 ? 3.0 : N >= 4 ? 2.0 : 1.0;
   rn.s += (double)s;
-  rn.b += (double)s * (2.4e-7 + LV * 6.0e-8 + 5e-8) + (double)mom * 1.12e-7 + 1e-36;
+  rn.b += (double)s * (2.4e-7 + LV * 6.0e-8 + 5e-8) - (double)mom * 1.25e-7 + 1e-36;
 }
 
-// The row history's distinct tokens of the part (ranks tid, tid + MT, ... of the part's history table): logit,
-// penalties, NaN test, mask, z, then the same running state as the stream (tokens out of order: ties go to the lower
-// id). Every thread takes part, with empty slots where it has no token.
-template <int DT, bool GREEDY>
-__device__ __forceinline__ void history_pass(const ScanArgs &a, const RowCtx &c, int row, int wl, int p0,
-                                             bool listing, const Shared &sh, Run &rn, float *proc) {
-  const int tid = threadIdx.x;
-  const uint32_t nd = sh.h.nd;
-  int ids[KH];
-  float x0[KH];
-  bool al[KH];
+// Tokens outside the stream (history tokens with their counts, ragged tokens with count 0; tok < 0: empty slot): logit,
+// penalties, NaN test, mask, z, then the same running state as the stream (tokens out of order: ties go to the lower id).
+// Every thread of the wave takes part, with empty slots where it has no token.
+template <int N, bool GREEDY, bool DIV>
+__device__ __forceinline__ void side_tokens(const ScanArgs &a, const RowCtx &c, int row, int wl,
+                                            bool listing, const int (&tk)[N], const uint32_t (&cnt)[N], Run &rn,
+                                            float *proc) {
+  float x0[N];
+  bool al[N];
 #pragma unroll
-  for (int k = 0; k < KH; ++k) {  // the loads first
-    const uint32_t r = (uint32_t)(tid + k * MT);
-    ids[k] = r < nd ? (int)sh.h.off[r] : -1;
-    x0[k] = ids[k] >= 0 ? load_one(c, p0 + ids[k]) : 0.0f;
-    al[k] = ids[k] >= 0 && mask_bit(c, p0 + ids[k]);
+  for (int k = 0; k < N; ++k) {  // the loads first
+    x0[k] = tk[k] >= 0 ? load_one(c, tk[k]) : 0.0f;
+    al[k] = tk[k] >= 0 && mask_bit(c, tk[k]);
   }
-  float zr[KH];
+  float xr[N];
   float cmax = -INFINITY;
   bool hnan = false;
 #pragma unroll
-  for (int k = 0; k < KH; ++k) {
-    zr[k] = -INFINITY;
-    if (ids[k] >= 0) {
-      const int t = p0 + ids[k];
-      const float x = penalize(x0[k], sh.h.cnt[tid + k * MT], c.rp, c.fp, c.pp);
+  for (int k = 0; k < N; ++k) {
+    xr[k] = -INFINITY;
+    if (tk[k] >= 0) {
+      const uint32_t t = (uint32_t)tk[k];
+      const float x = cnt[k] ? penalize(x0[k], cnt[k], c.rp, c.fp, c.pp) : x0[k];
       hnan |= x != x;
       const float xm = al[k] ? x : -INFINITY;
-      rn.fin = fminf(rn.fin, fabsf(xm));
       if (proc) proc[t] = xm;
-      if (x == x && (uint32_t)t < rn.fid) rn.fid = (uint32_t)t;
+      if (x == x && t < rn.fid) rn.fid = t;
       if constexpr (GREEDY) {
         const float g = fminf(fmaxf(xm, -FLTMAX), FLTMAX);
-        if (xm == xm && (g > rn.g || (g == rn.g && (uint32_t)t < rn.gid) || rn.gid == 0xFFFFFFFFu)) {
+        if (xm == xm && (g > rn.g || (g == rn.g && t < rn.gid) || rn.gid == 0xFFFFFFFFu)) {
           rn.g = g;
-          rn.gid = (uint32_t)t;
+          rn.gid = t;
         }
-        zr[k] = xm;
-      } else {
-        zr[k] = c.divide ? div_exact(xm, c.Rd) : xm;
       }
-      cmax = fmaxf(cmax, zr[k]);
+      xr[k] = DIV ? div_exact(xm, c.Rd) : xm;
+      cmax = fmaxf(cmax, xr[k]);
     }
   }
   rn.nanm |= ballot64(hnan);
-  if (listing) stream_sum<KH>(a, row, wl, cmax, zr, rn, [&](int i) { return (uint32_t)(p0 + ids[i]); });
+  if (listing) chunk_sum<N>(a, row, wl, cmax, xr, rn, [&](int i) { return (uint32_t)tk[i]; });
   else rn.m = fmaxf(rn.m, cmax);
 }
 
@@ -691,12 +724,13 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   using L = Lay<DT>;
   const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
   const int p0 = part * a.plen, p1 = min(a.V, p0 + a.plen);
-  const int nck = (p1 - p0 + CHK - 1) / CHK;
+  const int pv = AL ? max(p0, p1 & ~(L::VEC - 1)) : p1;  // the stream's end; [pv, p1) go to the side pass
+  const int nck = (pv - p0 + CHK - 1) / CHK;
   const bool listing = !GREEDY || nlp_of(a, P) > 0;  // candidates and the softmax sum are needed
   const int wl = part * PWAVES + w;                  // this wave's list
   float *proc = a.processed ? a.processed + (int64_t)row * a.processed_ld : nullptr;
 
-  // History ids first, then the wave's first chunk: the history tables build while the logits stream in.
+  // History ids first, then the wave's first two chunks: the history tables build while the logits stream in.
   int hid[HPT];
   if (c.pen) {
 #pragma unroll
@@ -705,12 +739,13 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
       hid[k] = j < c.he ? a.hist[j] : -1;
     }
   }
-  float xa[EPL], xb[EPL];
-  uint32_t ma[L::NV], mb[L::NV];
-  int ck = w;  // chunks 0..3 go to waves 0..3; later ones from the LDS counter
-  if (ck < nck) load_chunk<DT, AL>(c, p0 + ck * CHK, p1, xa, ma);
+  float xa[EPL], xb[EPL], xc[EPL];
+  uint32_t ma[L::NV], mb[L::NV], mcw[L::NV];
+  int c0 = w, c1 = w + NWV;  // chunks 0..7 go to waves 0..3 two by two; later ones from the LDS counter
+  load_u<DT, AL, MASKED>(c, p0 + c0 * CHK, pv, p1, xa, ma);
+  load_u<DT, AL, MASKED>(c, p0 + c1 * CHK, pv, p1, xb, mb);
   if (tid == 0) {
-    sh.next = NWV;
+    sh.next = 2 * NWV;
     sh.hover = 0;
   }
   if (c.pen) build_history(c, a.hist, hid, p0, p1, sh.h, sh.wcnt, sh.hover);
@@ -725,19 +760,18 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   rn.g = -INFINITY;
   rn.gid = 0xFFFFFFFFu;
   rn.fid = 0xFFFFFFFFu;
-  rn.fin = INFINITY;
   rn.nanm = 0;
   auto grab = [&]() -> int {
     uint32_t n = 0;
     if (lane == 0) n = atomicAdd(&sh.next, 1u);
-    return __shfl((int)n, 0, WAVE);
+    return __builtin_amdgcn_readfirstlane((int)n);
   };
   auto tok_of = [&](int cb) {
     return [=](int i) { return (uint32_t)(cb + (i / L::VEC) * L::STRIDE + lane * L::VEC + (i % L::VEC)); };
   };
   // First chunk of each wave; the part's listing threshold from the 256 lane maxima.
   float cmax = -INFINITY;
-  if (ck < nck) cmax = stream_z<DT, MASKED, GREEDY, DIV>(c, p0 + ck * CHK, p0, p1, xa, ma, sh.h, rn, proc);
+  if (c0 < nck) cmax = chunk_z<DT, AL, MASKED, GREEDY, DIV>(c, p0 + c0 * CHK, p0, pv, p1, xa, ma, sh.h, rn, proc);
   if (listing) {
     sh.lmax[tid] = fkey(cmax) >> 16;
     __syncthreads();
@@ -753,32 +787,63 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
       uint32_t cnt = 0;
 #pragma unroll
       for (int q = 0; q < NWV; ++q) cnt += (uint32_t)__popcll(ballot64(sh.lmax[q * WAVE + lane] >= cand));
-      if (cnt >= kp) r = cand;
+      if ((int)cnt >= (int)kp) r = cand;
     }
     rn.kap = max(r << 16, KEY_NEGINF + 1u);
   }
-  bool first = true;
-  while (ck < nck) {
-    const int cn = grab();
-    if (cn < nck) load_chunk<DT, AL>(c, p0 + cn * CHK, p1, xb, mb);
-    if (!first) cmax = stream_z<DT, MASKED, GREEDY, DIV>(c, p0 + ck * CHK, p0, p1, xa, ma, sh.h, rn, proc);
-    first = false;
-    if (listing) stream_sum<EPL>(a, row, wl, cmax, xa, rn, tok_of(p0 + ck * CHK));
+  int c2 = grab();
+  load_u<DT, AL, MASKED>(c, p0 + c2 * CHK, pv, p1, xc, mcw);
+  if (c0 < nck) {
+    if (listing) chunk_sum<EPL>(a, row, wl, cmax, xa, rn, tok_of(p0 + c0 * CHK));
     else rn.m = fmaxf(rn.m, cmax);
-    if (cn >= nck) break;
-    const int cn2 = grab();
-    if (cn2 < nck) load_chunk<DT, AL>(c, p0 + cn2 * CHK, p1, xa, ma);
-    cmax = stream_z<DT, MASKED, GREEDY, DIV>(c, p0 + cn * CHK, p0, p1, xb, mb, sh.h, rn, proc);
-    if (listing) stream_sum<EPL>(a, row, wl, cmax, xb, rn, tok_of(p0 + cn * CHK));
-    else rn.m = fmaxf(rn.m, cmax);
-    ck = cn2;
   }
-  // the history tokens of the part (the tables are still in LDS: the resolve has not started)
-  if (c.pen) history_pass<DT, GREEDY>(a, c, row, wl, p0, listing, sh, rn, proc);
+  // Steady state: two chunks loading while the wave works on a third (chunk indices rise, so the first past the end
+  // ends the wave's stream).
+  auto step = [&](int ck, float(&x)[EPL], const uint32_t(&mw)[L::NV]) __attribute__((always_inline)) {
+    const float cm = chunk_z<DT, AL, MASKED, GREEDY, DIV>(c, p0 + ck * CHK, p0, pv, p1, x, mw, sh.h, rn, proc);
+    if (listing) chunk_sum<EPL>(a, row, wl, cm, x, rn, tok_of(p0 + ck * CHK));
+    else rn.m = fmaxf(rn.m, cm);
+  };
+  while (true) {
+    c0 = grab();
+    load_u<DT, AL, MASKED>(c, p0 + c0 * CHK, pv, p1, xa, ma);
+    if (c1 >= nck) break;
+    step(c1, xb, mb);
+    c1 = grab();
+    load_u<DT, AL, MASKED>(c, p0 + c1 * CHK, pv, p1, xb, mb);
+    if (c2 >= nck) break;
+    step(c2, xc, mcw);
+    c2 = grab();
+    load_u<DT, AL, MASKED>(c, p0 + c2 * CHK, pv, p1, xc, mcw);
+    if (c0 >= nck) break;
+    step(c0, xa, ma);
+  }
+  // the history tokens of the part (the tables are still in LDS: the resolve has not started), then the ragged ones
+  if (c.pen) {
+    const uint32_t nd = sh.h.nd;
+    int tk[KH];
+    uint32_t cn[KH];
+#pragma unroll
+    for (int k = 0; k < KH; ++k) {
+      const uint32_t r = (uint32_t)(tid + k * MT);
+      tk[k] = r < nd ? p0 + (int)sh.h.off[r] : -1;
+      cn[k] = r < nd ? sh.h.cnt[r] : 0u;
+    }
+    side_tokens<KH, GREEDY, DIV>(a, c, row, wl, listing, tk, cn, rn, proc);
+  }
+  if (AL && pv < p1 && w == 0) {  // (uniform: at most VEC - 1 tokens, wave 0)
+    const int t = pv + lane;
+    int tk[1] = {-1};
+    const uint32_t cn[1] = {0u};
+    if (t < p1) {
+      const int o = t - p0;
+      if (!(c.pen && ((sh.h.bits[o >> 5] >> (o & 31)) & 1u))) tk[0] = t;
+    }
+    side_tokens<1, GREEDY, DIV>(a, c, row, wl, listing, tk, cn, rn, proc);
+  }
 
   // Part record: the part maximum, then every lane's sum rescaled to it (fp64, fixed order).
   const float wm = wave_max_f32(rn.m);
-  const uint64_t bf = ballot64(rn.fin < INFINITY);
   uint64_t top;
   if (GREEDY) {
     top = rn.gid != 0xFFFFFFFFu ? pack(fkey(rn.g), rn.gid) : 0ull;
@@ -788,7 +853,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   top = wave_max_u64(top);
   if (lane == 0) {
     sh.wmax[w] = wm;
-    sh.wflags[w] = (rn.nanm ? F_NAN : 0u) | (bf ? F_FINITE : 0u);
+    sh.wflags[w] = rn.nanm ? F_NAN : 0u;
     sh.wtop[w] = top;
     sh.wkap[w] = rn.kap;
     sh.wcnt[w] = rn.woff;
@@ -806,7 +871,10 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   s = block_sum_f64(s, sh.wred);
   b = block_sum_f64(b, sh.wred);
   if (tid == 0) {
-    uint32_t flags = sh.hover ? F_HOVER : 0u, kap = 0;
+    // flags: a finite value exists if the maximum of z over the allowed tokens is finite; a maximum of +inf (x = +inf,
+    // or x / T overflowing) leaves the row to the exact path
+    uint32_t flags = (sh.hover ? F_HOVER : 0u) | (fabsf(M) < INFINITY ? F_FINITE : 0u) | (M == INFINITY ? F_PINF : 0u);
+    uint32_t kap = 0;
     uint64_t t = 0;
 #pragma unroll
     for (int k = 0; k < NWV; ++k) {
@@ -850,12 +918,20 @@ __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
   if (row >= a.rows) return;
   const gse_row P = a.params[row];
   const RowCtx c = make_ctx(a, row, P);
-  const bool aligned = (((uintptr_t)c.base) & 15u) == 0;
+  // 16-byte vector loads: the row start is 16-byte aligned and the row holds a whole vector (a vector past the stream's
+  // end loads the row's first one)
+  const bool aligned = (((uintptr_t)c.base) & 15u) == 0 && a.V >= Lay<DT>::VEC;
   // variants: alignment (16-byte vector loads), mask, greedy (no division), division by T (T != 1)
   bool last;
+  // (MASKED variants read the row's mask words unconditionally: only rows with a mask take them)
   if (c.greedy) {
-    last = aligned ? part_body<DT, true, true, true, false>(a, P, c, row, part, sh)
-                   : part_body<DT, false, true, true, false>(a, P, c, row, part, sh);
+    if (c.mw) {
+      last = aligned ? part_body<DT, true, true, true, false>(a, P, c, row, part, sh)
+                     : part_body<DT, false, true, true, false>(a, P, c, row, part, sh);
+    } else {
+      last = aligned ? part_body<DT, true, false, true, false>(a, P, c, row, part, sh)
+                     : part_body<DT, false, false, true, false>(a, P, c, row, part, sh);
+    }
   } else if (c.mw) {
     if (c.divide) {
       last = aligned ? part_body<DT, true, true, false, true>(a, P, c, row, part, sh)
