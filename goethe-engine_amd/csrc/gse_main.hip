@@ -40,9 +40,9 @@ constexpr int KP = 12;                 // rank, among the part's 256 first-chunk
 constexpr int KV = 8;                  // rank, among a wave's running lane maxima, of its raised threshold (when its
                                        // list passes half its capacity)
 constexpr int NH = 2048;               // certified head capacity of the row resolve
-constexpr int NSUB = 512;              // sorted sub-head capacity
-constexpr int SUBT = 256;              // sub-head target size
-constexpr int NSUB2 = 1024;            // the larger sorted top
+constexpr int HPR = NH / MT;           // sorted head ranks per resolve thread
+constexpr int NBK = 512;               // key buckets of the head sort
+constexpr int BKT = 64;                // largest bucket the head sort ranks by counting (else: bitonic)
 constexpr int GPT = 8;                 // listed entries per thread per gather round
 constexpr int NSL = MAXP * PWAVES;     // wave lists of a row, at most (one per resolve thread)
 static_assert(NWV == PWAVES, "");
@@ -52,8 +52,10 @@ struct Shared {
   union {
     HistTab h;                 // history of the part's tokens
     struct {
-      uint64_t head[NH];       // listed elements at or above the certified key
-      uint64_t sub[NSUB2];     // the top of the head
+      uint64_t head[NH];       // listed elements at or above the certified key; then sorted (descending)
+      uint64_t tmp[NH];        // the head grouped by bucket
+      uint32_t bcnt[NBK];      // bucket counts, then their running ends
+      uint32_t bofs[NBK];      // bucket starts
     } r;
   };
   uint32_t next;               // next chunk of the part
@@ -66,10 +68,10 @@ struct Shared {
   double wred[NWV], wred2[NWV];
   // resolve
   uint32_t loff[NSL];
-  uint32_t bins[256];
   uint64_t rtop, rtopL;
-  uint32_t rflags, rkappa, rmkey, ltot, nh, ns, mfail_sure, mfail_maybe, jcount, bsel, lpw;
+  uint32_t rflags, rkappa, rmkey, ltot, nh, mfail_sure, mfail_maybe, jcount, bmax, lpw;
   double rsc;
+  double etab[64];             // 2^(j / 64) for exp_nonpos
 };
 
 __device__ __forceinline__ void lp_invalid(const ScanArgs &a, int row, int nlp) {
@@ -105,40 +107,109 @@ struct RowEval {
   const gse_row *P;
 };
 
-// Sorts the top arr[0, ns) of the head (ns <= MT * S; ns == n: the whole head) and decides the keep prefix, the draw
-// and the logprobs over it. arr is overwritten with the sorted ranks.
-template <int S>
-__device__ __forceinline__ int evaluate(const RowEval &ev, uint64_t *arr, int ns, Shared &sh) {
+// Sorts the head sh.r.head[0, n) descending in place. Keys lie in [kappa, mk]: a counting sort over NBK buckets of
+// equal key width (count, scan, scatter), then each element's rank inside its bucket by counting; a bucket larger than
+// BKT (many equal or close keys) makes the whole head take a bitonic sort instead. Rolled loops: compact code.
+__device__ __forceinline__ void sort_head(Shared &sh, int n, uint32_t mk, uint32_t kappa) {
+  const int tid = threadIdx.x;
+  const uint32_t span = mk - kappa;
+  int shift = 0;
+  while ((span >> shift) >= (uint32_t)NBK) ++shift;
+  for (int b = tid; b < NBK; b += MT) sh.r.bcnt[b] = 0;
+  if (tid == 0) sh.bmax = 0;
+  __syncthreads();
+#pragma unroll 1
+  for (int i = tid; i < n; i += MT) atomicAdd(&sh.r.bcnt[(mk - pk_key(sh.r.head[i])) >> shift], 1u);
+  __syncthreads();
+  // bucket starts: NBK / MT buckets per thread, contiguous
+  constexpr int BPT = NBK / MT;
+  uint32_t c[BPT], loc = 0, mx = 0;
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    c[j] = sh.r.bcnt[tid * BPT + j];
+    loc += c[j];
+    mx = max(mx, c[j]);
+  }
+  const uint32_t inc = wave_incl_scan_u32(loc);
+  mx = wave_max_u32(mx);
+  if (lane_id() == WAVE - 1) sh.wcnt[tid >> 6] = inc;
+  if (lane_id() == 0) atomicMax(&sh.bmax, mx);
+  __syncthreads();
+  uint32_t run = inc - loc;
+  for (int w = 0; w < NWV; ++w) run += w < (tid >> 6) ? sh.wcnt[w] : 0u;
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    sh.r.bofs[tid * BPT + j] = run;
+    sh.r.bcnt[tid * BPT + j] = run;  // (the running end while scattering)
+    run += c[j];
+  }
+  __syncthreads();
+  if (sh.bmax <= (uint32_t)BKT) {
+#pragma unroll 1
+    for (int i = tid; i < n; i += MT) {
+      const uint64_t v = sh.r.head[i];
+      sh.r.tmp[atomicAdd(&sh.r.bcnt[(mk - pk_key(v)) >> shift], 1u)] = v;
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int i = tid; i < n; i += MT) {
+      const uint64_t v = sh.r.tmp[i];
+      const uint32_t b = (mk - pk_key(v)) >> shift;
+      const uint32_t b0 = sh.r.bofs[b], b1 = sh.r.bcnt[b];
+      uint32_t r = b0;
+#pragma unroll 1
+      for (uint32_t q = b0; q < b1; ++q) r += sh.r.tmp[q] > v ? 1u : 0u;
+      sh.r.head[r] = v;
+    }
+    __syncthreads();
+  } else {
+    int N = 2;
+    while (N < n) N <<= 1;
+    for (int i = n + tid; i < N; i += MT) sh.r.head[i] = 0ull;
+    __syncthreads();
+#pragma unroll 1
+    for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll 1
+      for (int j = k >> 1; j > 0; j >>= 1) {
+#pragma unroll 1
+        for (int i = tid; i < N / 2; i += MT) {
+          const int lo = ((i & ~(j - 1)) << 1) | (i & (j - 1)), hi = lo + j;
+          const uint64_t x = sh.r.head[lo], y = sh.r.head[hi];
+          if ((lo & k) == 0 ? x < y : x > y) {
+            sh.r.head[lo] = y;
+            sh.r.head[hi] = x;
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
+}
+
+// Decides the keep prefix, the draw and the logprobs over the sorted head arr[0, n) (the whole certified head).
+__device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, Shared &sh) {
   const ScanArgs &a = *ev.a;
   const gse_row &P = *ev.P;
   const int tid = threadIdx.x;
-  const bool all = ns == ev.n;
-  if (ev.nlp > ns && !all) return EV_MORE;
-  if (ev.nlp > ns) return EV_HARD;  // logprobs past the finite elements: -inf ranks in id order
-  uint64_t v[S];
-#pragma unroll
-  for (int s = 0; s < S; ++s) v[s] = tid * S + s < ns ? arr[tid * S + s] : 0ull;
-  __syncthreads();
-  sort_regs<S>(v, arr);
-#pragma unroll
-  for (int s = 0; s < S; ++s) arr[tid * S + s] = v[s];
+  const int n = ev.n;
+  if (ev.nlp > n) return EV_HARD;  // logprobs past the finite elements: -inf ranks in id order
   if (tid == 0) {
     sh.mfail_sure = 0xFFFFFFFFu;
     sh.mfail_maybe = 0xFFFFFFFFu;
     sh.jcount = 0;
   }
-  // ranks tid * S + s: exact masses e; prefixes recomputed from the thread's exclusive base (A_s = base + e_0 + ...
+  // ranks tid * HPR + s: exact masses e; prefixes recomputed from the thread's exclusive base (A_s = base + e_0 + ...
   // + e_{s-1}, I_s = A_s + e_s, the same additions in the same order every time)
-  const int r0 = tid * S;
+  const int r0 = tid * HPR;
   const double M = ev.M, Sm = ev.S;
-  double e[S];
+  double e[HPR];
   double loc = 0.0;
 #pragma unroll
-  for (int s = 0; s < S; ++s) {
-    e[s] = r0 + s < ns ? exp((double)fkey_inv(pk_key(v[s])) - M) : 0.0;
+  for (int s = 0; s < HPR; ++s) {
+    e[s] = r0 + s < n ? exp_nonpos((double)fkey_inv(pk_key(arr[r0 + s])) - M, sh.etab) : 0.0;
     loc += e[s];
   }
-  const double base = block_excl_scan_f64(loc, sh.wred);  // (its barriers publish arr and the resets above)
+  const double base = block_excl_scan_f64(loc, sh.wred);  // (its barriers publish the resets above)
   if (ev.nlp > 0) {
     if (tid == 0) sh.lpw = 1;
     const double lS = log(Sm);
@@ -154,21 +225,27 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, uint64_t *arr, int ns
     return EV_DONE;
   }
   // keep_r = r < K AND A_r / S < top_p AND q_r >= min_p q_0 (sampling.py:80 plus min-p). A top-p decision is sure when
-  // it holds for every S in [S - B, S + B]; the first rank that surely fails and the first that may fail must agree.
+  // it holds for every S in [S - B, S + B] (A / S against top_p as A against top_p S: the margin B covers the
+  // roundings); the first rank that surely fails and the first that may fail must agree. Min-p compares the rounded
+  // quotients as the definition does, where e lies within 1e-12 of min_p (elsewhere e >= min_p decides it).
   const int64_t K = P.top_k > 0 ? (int64_t)P.top_k : (int64_t)0x7FFFFFFFFFFFll;
   const double topp = P.top_p, minp = P.min_p;
-  const double q0 = 1.0 / Sm, Slo = Sm - ev.B, Shi = Sm + ev.B;
+  const double q0 = 1.0 / Sm, tlo = topp * (Sm - ev.B), thi = topp * (Sm + ev.B);
   uint32_t fsure = 0xFFFFFFFFu, fmaybe = 0xFFFFFFFFu;
   {
     double A = base;
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
+    for (int s = 0; s < HPR; ++s) {
       const int r = r0 + s;
-      if (r < ns) {
+      if (r < n) {
         const bool kk = (int64_t)r < K;
-        const bool km = !(minp > 0.0) || (e[s] / Sm >= minp * q0);
-        if ((!kk || !km || (A / Shi >= topp)) && fsure == 0xFFFFFFFFu) fsure = (uint32_t)r;
-        if ((!kk || !km || !(A / Slo < topp)) && fmaybe == 0xFFFFFFFFu) fmaybe = (uint32_t)r;
+        bool km = true;
+        if (minp > 0.0) {
+          km = e[s] >= minp;
+          if (fabs(e[s] - minp) <= 1e-12 * minp) km = e[s] / Sm >= minp * q0;
+        }
+        if ((!kk || !km || A >= thi) && fsure == 0xFFFFFFFFu) fsure = (uint32_t)r;
+        if ((!kk || !km || !(A < tlo)) && fmaybe == 0xFFFFFFFFu) fmaybe = (uint32_t)r;
       }
       A += e[s];
     }
@@ -182,16 +259,15 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, uint64_t *arr, int ns
   __syncthreads();
   uint32_t m = sh.mfail_sure;
   if (m != sh.mfail_maybe) return EV_HARD;
-  if (m == 0xFFFFFFFFu) {  // every sorted rank is kept
-    if (!all) return EV_MORE;
+  if (m == 0xFFFFFFFFu) {  // every rank of the head is kept
     if (!ev.complete) return EV_HARD;  // the keep prefix runs past the certified head
-    m = (uint32_t)ns;
+    m = (uint32_t)n;
   }
   // c_last = I_{m-1}; j = #{r < m : I_r < u c_last}, clamped to [0, m - 1] (sampling.py:81-83)
   {
     double I = base;
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
+    for (int s = 0; s < HPR; ++s) {
       I += e[s];
       if ((uint32_t)(r0 + s) == m - 1) sh.rsc = I;
     }
@@ -205,7 +281,7 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, uint64_t *arr, int ns
     uint32_t cnt = 0;
     double I = base;
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
+    for (int s = 0; s < HPR; ++s) {
       I += e[s];
       if ((uint32_t)(r0 + s) < m && I < thr) ++cnt;
     }
@@ -219,45 +295,6 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, uint64_t *arr, int ns
     if (a.mode == MODE_SAMPLE) a.tokens[ev.row] = tok;
   }
   return EV_DONE;
-}
-
-// Copies into sh.r.sub the elements of the head sh.r.head[0, n) in the bins of a 256-bin count histogram of
-// (mk - key) up to the bin where the count crosses target (or the bin before it when that one would exceed cap).
-// Returns the number copied (more than cap when even that does not fit; then nothing past cap is copied).
-__device__ __forceinline__ int select_top(Shared &sh, int n, uint32_t mk, uint32_t kappa, int target, int cap) {
-  const int tid = threadIdx.x;
-  const uint32_t span = mk - kappa;
-  const int shift = span >> 8 ? 32 - __clz(span) - 8 : 0;
-  __syncthreads();
-  sh.bins[tid] = 0;
-  if (tid == 0) {
-    sh.bsel = 255;
-    sh.ns = 0;
-  }
-  __syncthreads();
-  for (int i = tid; i < n; i += MT) atomicAdd(&sh.bins[(mk - pk_key(sh.r.head[i])) >> shift], 1u);
-  __syncthreads();
-  const uint32_t cb = sh.bins[tid];
-  const uint32_t inc = wave_incl_scan_u32(cb);
-  if (lane_id() == WAVE - 1) sh.wcnt[tid >> 6] = inc;
-  __syncthreads();
-  uint32_t pre = 0;
-#pragma unroll
-  for (int w = 0; w < NWV; ++w) pre += w < (tid >> 6) ? sh.wcnt[w] : 0u;
-  const uint32_t incl = pre + inc;
-  if (incl >= (uint32_t)target && incl - cb < (uint32_t)target)  // the bin that crosses the target
-    atomicMin(&sh.bsel, incl <= (uint32_t)cap || tid == 0 ? (uint32_t)tid : (uint32_t)tid - 1u);
-  __syncthreads();
-  const uint32_t bsel = sh.bsel;
-  for (int i = tid; i < n; i += MT) {
-    const uint64_t pk = sh.r.head[i];
-    if (((mk - pk_key(pk)) >> shift) <= bsel) {
-      const uint32_t pos = atomicAdd(&sh.ns, 1u);
-      if (pos < (uint32_t)cap) sh.r.sub[pos] = pk;
-    }
-  }
-  __syncthreads();
-  return (int)sh.ns;
 }
 
 __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gse_row &P, Shared &sh) {
@@ -274,7 +311,6 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
     sh.rkappa = 0;
     sh.rmkey = 0;
     sh.nh = 0;
-    sh.ns = 0;
     sh.lpw = 0;
   }
   // One round of record loads: thread j holds wave list j (part j / 4), threads j % 4 == 0 the part's record.
@@ -384,13 +420,18 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
     }
 #pragma unroll
     for (int g = 0; g < GPT; ++g) {
-      if (!pk[g]) continue;
       const uint32_t k = pk_key(pk[g]);
       bestL = pk[g] > bestL ? pk[g] : bestL;
-      if (finite_max && k > KEY_NEGINF) scand += exp((double)fkey_inv(k) - M);
-      if (k >= kappa) {
-        const uint32_t pos = atomicAdd(&sh.nh, 1u);
-        if (pos < (uint32_t)NH) sh.r.head[pos] = pk[g];
+      if (pk[g] && finite_max && k > KEY_NEGINF) scand += exp_nonpos((double)fkey_inv(k) - M, sh.etab);
+      // head appends: one LDS atomic per wave
+      const bool h = pk[g] && k >= kappa;
+      const uint64_t bl = ballot64(h);
+      if (bl) {
+        uint32_t base = 0;
+        if (lane_id() == 0) base = atomicAdd(&sh.nh, (uint32_t)__popcll(bl));
+        base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+        const uint32_t pos = base + lanes_below(bl);
+        if (h && pos < (uint32_t)NH) sh.r.head[pos] = pk[g];
       }
     }
   }
@@ -431,19 +472,8 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   const int n = ev.n;
   int st = EV_HARD;
   if (!((flags & (F_OVERFLOW | F_HOVER)) || nh_all > (uint32_t)NH || a.force_exact)) {
-    if (n <= NSUB) {
-      st = evaluate<NSUB / MT>(ev, sh.r.head, n, sh);
-    } else {
-      // The top of the head first (>= 256 elements, <= 512 when the bins allow), then a larger top (<= 1024) when the
-      // keep prefix runs past it; a keep prefix past that takes the exact path.
-      const int ns = select_top(sh, n, mk, kappa, SUBT, NSUB);
-      st = ns <= NSUB ? evaluate<NSUB / MT>(ev, sh.r.sub, ns, sh) : EV_MORE;
-      if (st == EV_MORE) {
-        const int ns2 = select_top(sh, n, mk, kappa, NSUB2 - NSUB2 / 4, NSUB2);
-        st = ns2 <= NSUB2 ? evaluate<NSUB2 / MT>(ev, sh.r.sub, ns2, sh) : EV_HARD;
-        if (st == EV_MORE) st = EV_HARD;
-      }
-    }
+    sort_head(sh, n, mk, kappa);
+    st = evaluate(ev, sh.r.head, sh);
   }
   if (st != EV_DONE) {
     __syncthreads();  // (sh.lpw)
@@ -916,6 +946,7 @@ __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     part = L % a.nparts;
   }
   if (row >= a.rows) return;
+  if (threadIdx.x < 64) sh.etab[threadIdx.x] = EXP2_64[threadIdx.x];  // (published by the first barrier)
   const gse_row P = a.params[row];
   const RowCtx c = make_ctx(a, row, P);
   // 16-byte vector loads: the row start is 16-byte aligned and the row holds a whole vector (a vector past the stream's
@@ -950,6 +981,9 @@ __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     }
   }
   if (!last) return;
+  // the row resolve is a chain of short dependent steps: give its waves issue priority over the streaming waves of the
+  // other workgroups on this CU
+  __builtin_amdgcn_s_setprio(3);
   resolve_row(a, row, P, sh);
   if (threadIdx.x == 0) a.done[row] = 0u;
 }
