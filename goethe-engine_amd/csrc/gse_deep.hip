@@ -136,16 +136,18 @@ __device__ __forceinline__ double block_excl_scan_f64(double v, double &tot, Dee
   return pre + inc - v;
 }
 
-// Streams the slice [p0, p1) of the row through the main pass's element pipeline, double-buffered like the main pass:
-// the history ids and each wave's first chunk are loaded before the history tables are built. f(z, token, valid) is
-// called for every element slot of each chunk by every lane of the wave (valid false past the slice end), so f may use
-// ballots. pre() runs (by the whole workgroup) once the first loads are in flight. Ends with a barrier.
-template <int DT, bool AL, typename Pre, typename F>
+// Streams the slice [p0, p1) of the row through the main pass's element pipeline. The full chunks go through a
+// double-buffered loop whose loads are the same for every chunk (a chunk past the end reads the row's first one), so
+// one chunk stays in flight while the wave works on another; the history ids and each wave's first chunks are loaded
+// before the history tables are built. A partial last chunk is taken by wave 0 afterwards, with bounds checks.
+// f(z, token, valid) is called for every element slot of each chunk by every lane of the wave (valid false past the
+// slice end), so f may use ballots. Ends with a barrier.
+template <int DT, bool AL, typename F>
 __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c, int row, int p0, int p1,
-                                             DeepShared &sh, Pre pre, F f) {
+                                             DeepShared &sh, F f) {
   using L = Lay<DT>;
   const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
-  const int nck = (p1 - p0 + CHK - 1) / CHK;
+  const int nfull = (p1 - p0) / CHK;
   int hid[HPT];
   if (c.pen) {
 #pragma unroll
@@ -157,8 +159,7 @@ __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c,
   float xa[EPL], xb[EPL];
   uint32_t ma[L::NV], mb[L::NV];
   int ck = w;
-  if (ck < nck) load_chunk<DT, AL>(c, p0 + ck * CHK, p1, xa, ma);
-  pre();
+  if (nfull > 0) load_full<DT, AL>(c, p0 + ck * CHK, ck < nfull, xa, ma);
   if (tid == 0) {
     sh.next = NWV;
     sh.hover = 0;
@@ -179,10 +180,16 @@ __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c,
   auto grab = [&]() -> int {
     uint32_t n = 0;
     if (lane == 0) n = atomicAdd(&sh.next, 1u);
-    return __shfl((int)n, 0, WAVE);
+    return __builtin_amdgcn_readfirstlane((int)n);
   };
-  auto body = [&](int k, float(&x)[EPL], const uint32_t(&mw)[L::NV]) __attribute__((always_inline)) {
+  auto body = [&](int k, float(&x)[EPL], uint32_t(&mw)[L::NV]) __attribute__((always_inline)) {
     const int cb = p0 + k * CHK;
+    // take the chunk's registers here, unconditionally: the waits for its loads then sit at this point (counted, with
+    // the next chunk still in flight) rather than inside the rare per-element branches below
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) asm volatile("" : "+v"(x[i]));
+#pragma unroll
+    for (int v = 0; v < L::NV; ++v) asm volatile("" : "+v"(mw[v]));
     (void)chunk_phase1<DT>(a, c, row, cb, p0, p1, x, mw, ln, sh.h);
 #pragma unroll
     for (int v = 0; v < L::NV; ++v) {
@@ -193,15 +200,21 @@ __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c,
       }
     }
   };
-  while (ck < nck) {
-    const int cn = grab();
-    if (cn < nck) load_chunk<DT, AL>(c, p0 + cn * CHK, p1, xb, mb);
-    body(ck, xa, ma);
-    if (cn >= nck) break;
-    const int cn2 = grab();
-    if (cn2 < nck) load_chunk<DT, AL>(c, p0 + cn2 * CHK, p1, xa, ma);
-    body(cn, xb, mb);
-    ck = cn2;
+  if (nfull > 0) {
+    while (true) {
+      const int cn = grab();
+      load_full<DT, AL>(c, p0 + cn * CHK, cn < nfull, xb, mb);
+      if (ck >= nfull) break;
+      body(ck, xa, ma);
+      ck = grab();
+      load_full<DT, AL>(c, p0 + ck * CHK, ck < nfull, xa, ma);
+      if (cn >= nfull) break;
+      body(cn, xb, mb);
+    }
+  }
+  if (nfull * CHK < p1 - p0 && w == 0) {  // the partial last chunk (uniform in wave 0)
+    load_chunk<DT, AL>(c, p0 + nfull * CHK, p1, xa, ma);
+    body(nfull, xa, ma);
   }
   __syncthreads();
 }
@@ -372,7 +385,7 @@ __device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slic
     sh.c.cnt[b] = 0;
     sh.c.mass[b] = 0;
   }
-  stream_slice<DT, AL>(a, c, row, p0, p1, sh, []() {}, [&](float z, int, bool ok) __attribute__((always_inline)) {
+  stream_slice<DT, AL>(a, c, row, p0, p1, sh, [&](float z, int, bool ok) __attribute__((always_inline)) {
     if (ok && z > -INFINITY) {
       const uint32_t b = dbin(z, M);
       atomicAdd(&sh.c.cnt[b], 1u);
@@ -762,7 +775,7 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
     // per lane, exact fixed-point masses of three regions (before the draw window, between the windows, the rest):
     // whole multiples of 2^-40 and 2^-64, summed in fp64 (exact below 2^53)
     double h0 = 0.0, l0 = 0.0, h1 = 0.0, l1 = 0.0, h2 = 0.0, l2 = 0.0;
-    stream_slice<DT, AL>(a, c, row, p0, p1, sh, []() {}, [&](float z, int t, bool ok) __attribute__((always_inline)) {
+    stream_slice<DT, AL>(a, c, row, p0, p1, sh, [&](float z, int t, bool ok) __attribute__((always_inline)) {
       bool inw = false;
       if (ok && z > -INFINITY) {
         const uint32_t b = dbin(z, Mf);

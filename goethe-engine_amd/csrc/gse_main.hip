@@ -198,17 +198,18 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
     sh.mfail_maybe = 0xFFFFFFFFu;
     sh.jcount = 0;
   }
-  // ranks tid * HPR + s: exact masses e; prefixes recomputed from the thread's exclusive base (A_s = base + e_0 + ...
-  // + e_{s-1}, I_s = A_s + e_s, the same additions in the same order every time)
-  const int r0 = tid * HPR;
+  // exact masses of the sorted ranks (in LDS: the loops below stay rolled, this code runs once per row with a cold
+  // instruction cache); thread tid takes ranks tid * HPR + s, with prefixes recomputed from its exclusive base
+  // (A_s = base + e_0 + ... + e_{s-1}, I_s = A_s + e_s, the same additions in the same order every time)
+  double *ee = reinterpret_cast<double *>(sh.r.tmp);
   const double M = ev.M, Sm = ev.S;
-  double e[HPR];
+#pragma unroll 1
+  for (int i = tid; i < n; i += MT) ee[i] = exp_nonpos((double)fkey_inv(pk_key(arr[i])) - M, sh.etab);
+  __syncthreads();
+  const int r0 = tid * HPR, r1 = min(n, r0 + HPR);
   double loc = 0.0;
-#pragma unroll
-  for (int s = 0; s < HPR; ++s) {
-    e[s] = r0 + s < n ? exp_nonpos((double)fkey_inv(pk_key(arr[r0 + s])) - M, sh.etab) : 0.0;
-    loc += e[s];
-  }
+#pragma unroll 1
+  for (int r = r0; r < r1; ++r) loc += ee[r];
   const double base = block_excl_scan_f64(loc, sh.wred);  // (its barriers publish the resets above)
   if (ev.nlp > 0) {
     if (tid == 0) sh.lpw = 1;
@@ -234,20 +235,18 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
   uint32_t fsure = 0xFFFFFFFFu, fmaybe = 0xFFFFFFFFu;
   {
     double A = base;
-#pragma unroll
-    for (int s = 0; s < HPR; ++s) {
-      const int r = r0 + s;
-      if (r < n) {
-        const bool kk = (int64_t)r < K;
-        bool km = true;
-        if (minp > 0.0) {
-          km = e[s] >= minp;
-          if (fabs(e[s] - minp) <= 1e-12 * minp) km = e[s] / Sm >= minp * q0;
-        }
-        if ((!kk || !km || A >= thi) && fsure == 0xFFFFFFFFu) fsure = (uint32_t)r;
-        if ((!kk || !km || !(A < tlo)) && fmaybe == 0xFFFFFFFFu) fmaybe = (uint32_t)r;
+#pragma unroll 1
+    for (int r = r0; r < r1; ++r) {
+      const double e = ee[r];
+      const bool kk = (int64_t)r < K;
+      bool km = true;
+      if (minp > 0.0) {
+        km = e >= minp;
+        if (fabs(e - minp) <= 1e-12 * minp) km = e / Sm >= minp * q0;
       }
-      A += e[s];
+      if ((!kk || !km || A >= thi) && fsure == 0xFFFFFFFFu) fsure = (uint32_t)r;
+      if ((!kk || !km || !(A < tlo)) && fmaybe == 0xFFFFFFFFu) fmaybe = (uint32_t)r;
+      A += e;
     }
   }
   fsure = wave_min_u32(fsure);
@@ -266,10 +265,10 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
   // c_last = I_{m-1}; j = #{r < m : I_r < u c_last}, clamped to [0, m - 1] (sampling.py:81-83)
   {
     double I = base;
-#pragma unroll
-    for (int s = 0; s < HPR; ++s) {
-      I += e[s];
-      if ((uint32_t)(r0 + s) == m - 1) sh.rsc = I;
+#pragma unroll 1
+    for (int r = r0; r < r1; ++r) {
+      I += ee[r];
+      if ((uint32_t)r == m - 1) sh.rsc = I;
     }
   }
   __syncthreads();
@@ -280,10 +279,10 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
     const double thr = u * clast;
     uint32_t cnt = 0;
     double I = base;
-#pragma unroll
-    for (int s = 0; s < HPR; ++s) {
-      I += e[s];
-      if ((uint32_t)(r0 + s) < m && I < thr) ++cnt;
+#pragma unroll 1
+    for (int r = r0; r < r1; ++r) {
+      I += ee[r];
+      if ((uint32_t)r < m && I < thr) ++cnt;
     }
     cnt = wave_incl_scan_u32(cnt);
     if (lane_id() == WAVE - 1 && cnt) atomicAdd(&sh.jcount, cnt);
@@ -418,20 +417,25 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
         pk[g] = ld_ag(&cl0[(size_t)lo * CAPW + (f - sh.loff[lo])]);
       }
     }
+    // (through LDS, so that the processing loop stays rolled: this code runs once per row, with a cold instruction
+    // cache, and its length is its cost)
 #pragma unroll
+    for (int g = 0; g < GPT; ++g) sh.r.tmp[g * MT + tid] = pk[g];
+#pragma unroll 1
     for (int g = 0; g < GPT; ++g) {
-      const uint32_t k = pk_key(pk[g]);
-      bestL = pk[g] > bestL ? pk[g] : bestL;
-      if (pk[g] && finite_max && k > KEY_NEGINF) scand += exp_nonpos((double)fkey_inv(k) - M, sh.etab);
+      const uint64_t v = sh.r.tmp[g * MT + tid];
+      const uint32_t k = pk_key(v);
+      bestL = v > bestL ? v : bestL;
+      if (v && finite_max && k > KEY_NEGINF) scand += exp_nonpos((double)fkey_inv(k) - M, sh.etab);
       // head appends: one LDS atomic per wave
-      const bool h = pk[g] && k >= kappa;
+      const bool h = v && k >= kappa;
       const uint64_t bl = ballot64(h);
       if (bl) {
         uint32_t base = 0;
         if (lane_id() == 0) base = atomicAdd(&sh.nh, (uint32_t)__popcll(bl));
         base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
         const uint32_t pos = base + lanes_below(bl);
-        if (h && pos < (uint32_t)NH) sh.r.head[pos] = pk[g];
+        if (h && pos < (uint32_t)NH) sh.r.head[pos] = v;
       }
     }
   }
@@ -809,7 +813,11 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     uint32_t act = 0;
 #pragma unroll
     for (int q = 0; q < NWV; ++q) act += (uint32_t)__popcll(ballot64(sh.lmax[q * WAVE + lane] > (KEY_NEGINF >> 16)));
-    const uint32_t kp = max(1u, (KP * act + MT - 1) / MT);
+    // rows that keep at most top_k elements need only about that many certified: the threshold rank follows top_k
+    // (the rank-r lane maximum of the 2048-token sample bounds about 18 r of the part's tokens; twice that for slack)
+    int kpr = KP;
+    if (P.top_k > 0) kpr = min(KP, max(3, (2 * max(P.top_k, nlp_of(a, P)) + 17) / 18));
+    const uint32_t kp = max(1u, (kpr * act + MT - 1) / MT);
     uint32_t r = 0;
 #pragma unroll
     for (int b = 15; b >= 0; --b) {

@@ -232,6 +232,51 @@ __device__ __forceinline__ void sort_regs(uint64_t (&v)[S], uint64_t *buf) {
   }
 }
 
+// An all-ones mask word: what unmasked rows read in place of their mask words in load_full.
+static __device__ const uint32_t ONES_WORD[1] = {0xFFFFFFFFu};
+
+// A full chunk [cb, cb + CHK) of the row (every token inside the slice) into registers, with no bounds branches, so that
+// the compiler can count the loads in flight: every call issues the same loads. valid false reads the row's first chunk
+// instead (the row must hold CHK tokens) and the caller ignores it. Unmasked rows read ONES_WORD as their mask words.
+template <int DT, bool AL>
+__device__ __forceinline__ void load_full(const RowCtx &c, int cb, bool valid, float (&x)[EPL],
+                                          uint32_t (&mw)[Lay<DT>::NV]) {
+  using L = Lay<DT>;
+  const int l = lane_id();
+  const int b = valid ? cb : 0;
+  const uint32_t *mp = c.mw ? c.mw : ONES_WORD;
+#pragma unroll
+  for (int v = 0; v < L::NV; ++v) {
+    const int t0 = b + v * L::STRIDE + l * L::VEC;
+    mw[v] = mp[c.mw ? t0 >> 5 : 0];
+    if constexpr (DT == GSE_F32) {
+      if constexpr (AL) {
+        const float4 f = *reinterpret_cast<const float4 *>((const float *)c.base + t0);
+        x[4 * v] = f.x;
+        x[4 * v + 1] = f.y;
+        x[4 * v + 2] = f.z;
+        x[4 * v + 3] = f.w;
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x[4 * v + k] = ((const float *)c.base)[t0 + k];
+      }
+    } else {
+      if constexpr (AL) {
+        const uint4 u = *reinterpret_cast<const uint4 *>((const uint16_t *)c.base + t0);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[8 * v + 2 * i] = __uint_as_float(w[i] << 16);
+          x[8 * v + 2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[8 * v + k] = bf16_to_f32(((const uint16_t *)c.base)[t0 + k]);
+      }
+    }
+  }
+}
+
 // Per-lane running state of a wave.
 struct Lane {
   float m;         // running maximum of this lane's z
