@@ -172,7 +172,7 @@ __device__ __forceinline__ uint32_t wave_kth_largest_u32(uint32_t v, int k) {
 #pragma unroll
   for (int b = 31; b >= 0; --b) {
     const uint32_t c = r | (1u << b);
-    if (__popcll(ballot64(v >= c)) >= (uint64_t)k) r = c;
+    if ((int)__popcll(ballot64(v >= c)) >= k) r = c;
   }
   return r;
 }
@@ -183,13 +183,17 @@ __device__ __forceinline__ uint32_t wave_kth_largest_u16(uint32_t v, int k) {
 #pragma unroll
   for (int b = 15; b >= 0; --b) {
     const uint32_t c = r | (1u << b);
-    if (__popcll(ballot64(v >= c)) >= (uint64_t)k) r = c;
+    if ((int)__popcll(ballot64(v >= c)) >= k) r = c;
   }
   return r;
 }
 
 __device__ __forceinline__ float wave_max_f32(float v) {
   for (int m = 32; m; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, WAVE));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+  for (int m = 32; m; m >>= 1) v += shfl_xor_u32(v, m);
   return v;
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {

@@ -36,9 +36,9 @@ namespace {
 
 using namespace strm;
 
-constexpr int KP = 12;                 // rank, among the part's 256 first-chunk lane maxima, of its listing threshold
-constexpr int KV = 8;                  // rank, among a wave's running lane maxima, of its raised threshold (when its
-                                       // list passes half its capacity)
+constexpr int KT = 222;                // tokens of a part its listing threshold aims to leave above it
+constexpr int KV = 32;                 // rank, among a wave's running lane maxima, of its raised threshold (when its
+                                       // list passes a quarter of its capacity)
 constexpr int NH = 2048;               // certified head capacity of the row resolve
 constexpr int HPR = NH / MT;           // sorted head ranks per resolve thread
 constexpr int NBK = 512;               // key buckets of the head sort
@@ -659,7 +659,7 @@ __device__ __forceinline__ void chunk_sum(const ScanArgs &a, int row, int wl, fl
                                           Run &rn, Tok tok) {
   static_assert((N & (N - 1)) == 0 && N <= 256, "");
   const float mnew = fmaxf(rn.m, cmax);
-  if (rn.woff > (uint32_t)(CAPW / 2)) rn.kap = max(rn.kap, wave_kth_largest_u16(fkey(mnew) >> 16, KV) << 16);
+  if (rn.woff > (uint32_t)(CAPW / 4)) rn.kap = max(rn.kap, wave_kth_largest_u16(fkey(mnew) >> 16, KV) << 16);
   const float tauf = fkey_inv(rn.kap);
   if (mnew > rn.m && rn.m > -INFINITY) {  // rescale the lane's sum to its new maximum (fp64)
     const double f = exp((double)rn.m - (double)mnew);
@@ -773,6 +773,19 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
       hid[k] = j < c.he ? a.hist[j] : -1;
     }
   }
+  // allowed tokens of the part's stream range (masked rows: popcounts of its mask words; they load with the history)
+  uint32_t apc = 0;
+  if constexpr (MASKED) {
+    const int nw = (pv - p0 + 31) >> 5;
+    for (int i = tid; i < nw; i += MT) {
+      uint32_t word = c.mw[(p0 >> 5) + i];
+      const int below = pv - (p0 + 32 * i);  // tokens of this word below pv (>= 1)
+      if (below < 32) word &= (1u << below) - 1u;
+      apc += (uint32_t)__popc(word);
+    }
+  } else {
+    apc = tid == 0 ? (uint32_t)(pv - p0) : 0u;
+  }
   float xa[EPL], xb[EPL], xc[EPL];
   uint32_t ma[L::NV], mb[L::NV], mcw[L::NV];
   int c0 = w, c1 = w + NWV;  // chunks 0..7 go to waves 0..3 two by two; later ones from the LDS counter
@@ -807,17 +820,32 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   float cmax = -INFINITY;
   if (c0 < nck) cmax = chunk_z<DT, AL, MASKED, GREEDY, DIV>(c, p0 + c0 * CHK, p0, pv, p1, xa, ma, sh.h, rn, proc);
   if (listing) {
+    // The listing threshold: the rank-kp largest of the 256 lane maxima of the waves' first chunks (a 2048-token
+    // sample). kp is scaled so that about T tokens of the part lie above it: kp = T * (allowed tokens in the sample) /
+    // (allowed tokens in the part), counted exactly, so that a mask whose allowed tokens cluster in runs does not skew
+    // it. T = 222, or 3 top_k + 32 (at most 444) for rows that keep at most top_k elements.
+    uint32_t as = 0;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) as += xa[i] > -INFINITY ? 1u : 0u;
+    if (c0 >= nck) as = 0;
+    as = wave_sum_u32(as);
+    apc = wave_sum_u32(apc);
+    if (lane == 0) {
+      sh.wkap[w] = as;
+      sh.wflags[w] = apc;
+    }
     sh.lmax[tid] = fkey(cmax) >> 16;
     __syncthreads();
-    // the rank scales with the lanes that saw a z > -inf (a sparse mask leaves most lanes without one)
-    uint32_t act = 0;
+    uint32_t act = 0, As = 0, Ap = 0;
 #pragma unroll
-    for (int q = 0; q < NWV; ++q) act += (uint32_t)__popcll(ballot64(sh.lmax[q * WAVE + lane] > (KEY_NEGINF >> 16)));
-    // rows that keep at most top_k elements need only about that many certified: the threshold rank follows top_k
-    // (the rank-r lane maximum of the 2048-token sample bounds about 18 r of the part's tokens; twice that for slack)
-    int kpr = KP;
-    if (P.top_k > 0) kpr = min(KP, max(3, (2 * max(P.top_k, nlp_of(a, P)) + 17) / 18));
-    const uint32_t kp = max(1u, (kpr * act + MT - 1) / MT);
+    for (int q = 0; q < NWV; ++q) {
+      act += (uint32_t)__popcll(ballot64(sh.lmax[q * WAVE + lane] > (KEY_NEGINF >> 16)));
+      As += sh.wkap[q];
+      Ap += sh.wflags[q];
+    }
+    const uint32_t T = P.top_k > 0 ? min(2u * KT, (uint32_t)(3 * max(P.top_k, nlp_of(a, P)) + 32)) : (uint32_t)KT;
+    // (a sample with few allowed tokens estimates nothing: then the lowest lane maximum, and the valve bounds the lists)
+    const uint32_t kp = As < 16u ? max(act, 1u) : max(1u, min(act, (uint32_t)(((uint64_t)T * As + Ap - 1) / max(Ap, 1u))));
     uint32_t r = 0;
 #pragma unroll
     for (int b = 15; b >= 0; --b) {
