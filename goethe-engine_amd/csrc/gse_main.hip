@@ -40,7 +40,6 @@ constexpr int KT = 222;                // tokens of a part its listing threshold
 constexpr int KV = 32;                 // rank, among a wave's running lane maxima, of its raised threshold (when its
                                        // list passes a quarter of its capacity)
 constexpr int NH = 2048;               // certified head capacity of the row resolve
-constexpr int HPR = NH / MT;           // sorted head ranks per resolve thread
 constexpr int NBK = 512;               // key buckets of the head sort
 constexpr int BKT = 64;                // largest bucket the head sort ranks by counting (else: bitonic)
 constexpr int GPT = 8;                 // listed entries per thread per gather round
@@ -198,19 +197,37 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
     sh.mfail_maybe = 0xFFFFFFFFu;
     sh.jcount = 0;
   }
-  // exact masses of the sorted ranks (in LDS: the loops below stay rolled, this code runs once per row with a cold
-  // instruction cache); thread tid takes ranks tid * HPR + s, with prefixes recomputed from its exclusive base
-  // (A_s = base + e_0 + ... + e_{s-1}, I_s = A_s + e_s, the same additions in the same order every time)
+  // Exact masses e_r of the sorted ranks, then their inclusive prefixes I_r in place (in LDS). Wave w takes ranks
+  // [512 w, 512 w + 512), 64 consecutive ranks per step: conflict-free LDS accesses and wave scans (the additions are
+  // the same, in the same order, every time). A_r = I_{r-1} is the exclusive prefix.
   double *ee = reinterpret_cast<double *>(sh.r.tmp);
   const double M = ev.M, Sm = ev.S;
+  const int lane = lane_id(), w = tid >> 6;
 #pragma unroll 1
   for (int i = tid; i < n; i += MT) ee[i] = exp_nonpos((double)fkey_inv(pk_key(arr[i])) - M, sh.etab);
   __syncthreads();
-  const int r0 = tid * HPR, r1 = min(n, r0 + HPR);
-  double loc = 0.0;
+  constexpr int RPW = NH / NWV;  // ranks per wave
+  double carry = 0.0;
 #pragma unroll 1
-  for (int r = r0; r < r1; ++r) loc += ee[r];
-  const double base = block_excl_scan_f64(loc, sh.wred);  // (its barriers publish the resets above)
+  for (int s = 0; s < RPW / WAVE; ++s) {
+    const int r = w * RPW + s * WAVE + lane;
+    double v = r < n ? ee[r] : 0.0;
+    v = wave_incl_scan_f64(v) + carry;
+    if (r < n) ee[r] = v;
+    carry = shfl_f64(v, WAVE - 1);
+  }
+  if (lane == 0) sh.wred[w] = carry;
+  __syncthreads();
+  double base = 0.0;
+  for (int q = 0; q < w; ++q) base += sh.wred[q];
+  if (w > 0) {
+#pragma unroll 1
+    for (int s = 0; s < RPW / WAVE; ++s) {
+      const int r = w * RPW + s * WAVE + lane;
+      if (r < n) ee[r] += base;
+    }
+  }
+  __syncthreads();
   if (ev.nlp > 0) {
     if (tid == 0) sh.lpw = 1;
     const double lS = log(Sm);
@@ -233,25 +250,25 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
   const double topp = P.top_p, minp = P.min_p;
   const double q0 = 1.0 / Sm, tlo = topp * (Sm - ev.B), thi = topp * (Sm + ev.B);
   uint32_t fsure = 0xFFFFFFFFu, fmaybe = 0xFFFFFFFFu;
-  {
-    double A = base;
 #pragma unroll 1
-    for (int r = r0; r < r1; ++r) {
-      const double e = ee[r];
+  for (int s = 0; s < RPW / WAVE; ++s) {
+    const int r = w * RPW + s * WAVE + lane;
+    if (r < n) {
+      const double A = r > 0 ? ee[r - 1] : 0.0;
       const bool kk = (int64_t)r < K;
       bool km = true;
       if (minp > 0.0) {
+        const double e = exp_nonpos((double)fkey_inv(pk_key(arr[r])) - M, sh.etab);
         km = e >= minp;
         if (fabs(e - minp) <= 1e-12 * minp) km = e / Sm >= minp * q0;
       }
       if ((!kk || !km || A >= thi) && fsure == 0xFFFFFFFFu) fsure = (uint32_t)r;
       if ((!kk || !km || !(A < tlo)) && fmaybe == 0xFFFFFFFFu) fmaybe = (uint32_t)r;
-      A += e;
     }
   }
   fsure = wave_min_u32(fsure);
   fmaybe = wave_min_u32(fmaybe);
-  if (lane_id() == 0) {
+  if (lane == 0) {
     atomicMin(&sh.mfail_sure, fsure);
     atomicMin(&sh.mfail_maybe, fmaybe);
   }
@@ -263,29 +280,19 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
     m = (uint32_t)n;
   }
   // c_last = I_{m-1}; j = #{r < m : I_r < u c_last}, clamped to [0, m - 1] (sampling.py:81-83)
-  {
-    double I = base;
-#pragma unroll 1
-    for (int r = r0; r < r1; ++r) {
-      I += ee[r];
-      if ((uint32_t)r == m - 1) sh.rsc = I;
-    }
-  }
-  __syncthreads();
-  const double clast = sh.rsc;
+  const double clast = ee[m - 1];
   int32_t tok = -1;
   if (a.mode == MODE_SAMPLE) {
     const double u = a.uni ? a.uni[ev.row] : uniform64(P.seed, P.idx);
     const double thr = u * clast;
     uint32_t cnt = 0;
-    double I = base;
 #pragma unroll 1
-    for (int r = r0; r < r1; ++r) {
-      I += ee[r];
-      if ((uint32_t)r < m && I < thr) ++cnt;
+    for (int s = 0; s < RPW / WAVE; ++s) {
+      const int r = w * RPW + s * WAVE + lane;
+      if ((uint32_t)r < m && ee[r] < thr) ++cnt;
     }
-    cnt = wave_incl_scan_u32(cnt);
-    if (lane_id() == WAVE - 1 && cnt) atomicAdd(&sh.jcount, cnt);
+    cnt = wave_sum_u32(cnt);
+    if (lane == 0 && cnt) atomicAdd(&sh.jcount, cnt);
     __syncthreads();
     tok = (int32_t)pk_id(arr[min(sh.jcount, m - 1u)]);
   }
