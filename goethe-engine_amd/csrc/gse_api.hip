@@ -23,6 +23,8 @@ struct gse_handle {
   gse::DeepSlot *dslot = nullptr;
   uint64_t *dhist = nullptr;
   uint64_t *dlist = nullptr;
+  float *dz = nullptr;
+  int64_t dz_ld = 0;
   hipEvent_t (*ring)[5] = nullptr;  // kernel boundaries of up to GSE_PROFILE_CALLS profiled calls
   int nring = 0;                    // calls recorded
   int nprof = 0;                    // kernels per recorded call
@@ -152,6 +154,8 @@ gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   a.dslot = h->dslot;
   a.dhist = h->dhist;
   a.dlist = h->dlist;
+  a.dz = h->dz;
+  a.dz_ld = h->dz_ld;
   deep_grid(h, b.rows, &a.dslices, &a.dgrid);
   return a;
 }
@@ -186,6 +190,8 @@ GSE_API int gse_open(const gse_open_params *p, gse_handle **out) {
   h->nchmax = (o.max_vocab + gse::CH - 1) / gse::CH;
   h->target = 4u * (uint32_t)(prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256);
   h->nrec = h->max_rows * ((o.max_vocab + gse::PTOK - 1) / gse::PTOK + 1) + h->target;
+  h->dz_ld = ((int64_t)o.max_vocab + 63) / 64 * 64;
+  const size_t dzn = (size_t)(h->max_rows < (uint32_t)gse::DEEP_MAX ? h->max_rows : (uint32_t)gse::DEEP_MAX) * h->dz_ld;
   if ((e = hipMalloc(&h->rec, (size_t)h->nrec * sizeof(gse::SliceRec))) != hipSuccess ||
       (e = hipMalloc(&h->cand, (size_t)h->nrec * gse::PWAVES * gse::CAPW * sizeof(uint64_t))) != hipSuccess ||
       (e = hipMalloc(&h->info, (size_t)h->max_rows * sizeof(gse::RowInfo))) != hipSuccess ||
@@ -198,6 +204,7 @@ GSE_API int gse_open(const gse_open_params *p, gse_handle **out) {
       (e = hipMalloc(&h->dhist, (size_t)gse::DEEP_MAX * 2 * gse::DNB * sizeof(uint64_t))) != hipSuccess ||
       (e = hipMemset(h->dhist, 0, (size_t)gse::DEEP_MAX * 2 * gse::DNB * sizeof(uint64_t))) != hipSuccess ||
       (e = hipMalloc(&h->dlist, (size_t)gse::DEEP_MAX * gse::DCAP * sizeof(uint64_t))) != hipSuccess ||
+      (e = hipMalloc(&h->dz, dzn * sizeof(float))) != hipSuccess ||
       (e = hipDeviceSynchronize()) != hipSuccess) {
     fail(nullptr, GSE_E_DEVICE, "workspace allocation (%u part records): %s", h->nrec, hipGetErrorString(e));
     gse_close(h);
@@ -358,6 +365,7 @@ GSE_API void gse_close(gse_handle *h) {
     if (h->dslot) (void)hipFree(h->dslot);
     if (h->dhist) (void)hipFree(h->dhist);
     if (h->dlist) (void)hipFree(h->dlist);
+    if (h->dz) (void)hipFree(h->dz);
     if (h->ring) {
       for (int c = 0; c < GSE_PROFILE_CALLS; ++c)
         for (int i = 0; i < 4; ++i)

@@ -1,21 +1,23 @@
 // Split-row finish of the rows the main pass could not decide from its certified head: a keep prefix that runs past
 // the listed elements (the nucleus of a flat, hot row), or a top-p decision that fell inside the main pass's bound on
-// S. Two launches, back to back on the stream, each a pass over every such row spread over S slices (S and the slice
-// length follow from the number of deep rows so that one launch is one round of resident workgroups). No workgroup
-// waits for another: slices add their results into the row's record with integer atomics (the same sums in any order),
-// and the last slice of a row to finish (atomic ticket) carries on with the row.
+// S. One launch; each deep row is spread over S slices (S and the slice length follow from the number of deep rows so
+// that the grid is one round of resident workgroups, one slice each). Slices add their results into the row's record
+// with integer atomics (the same sums in any order), and the last slice of a row to finish a phase (atomic ticket)
+// carries on with the row. Every workgroup runs all its count items before any pick item.
 //
-//   count:  each slice recomputes z exactly as the main pass does and adds a 512-bin histogram of d = z_max - z
-//           (counts, and masses exp2 in fp32 summed as 2^-40 fixed point; bins 1/32 wide, the last one open-ended). d
-//           is monotone in z, so the bins follow the stable order and ties share a bin. The row's last slice plans:
-//           the bins that may hold the last kept element (top-p, top-k and min-p cuts, with a margin for the fp32
-//           masses), the bins that may hold the draw, and whether they hold at most DCAP elements.
-//   pick:   each slice adds the exact fixed-point mass of every element (fp64 exp, 2^-64 resolution) to S and to the
-//           regions before and between the two windows, and lists the window elements. The row's last slice finishes:
-//           exact sub-bin counts and masses over the list locate the cut and the draw, only the sub-bins holding them
-//           are sorted, and their exact prefixes (one scan) give the last kept element, c_last and the token. A failed
-//           check leaves the row to the exact path (gse_exact.hip). It then clears the row's records for the next
-//           call.
+//   count:  each slice recomputes z exactly as the main pass does, keeps it (dz), and adds a 512-bin histogram of
+//           d = z_max - z (counts, and masses exp2 in fp32 summed as 2^-40 fixed point; bins 1/32 wide, the last one
+//           open-ended). d is monotone in z, so the bins follow the stable order and ties share a bin. The row's last
+//           slice plans: the bins that may hold the last kept element (top-p, top-k and min-p cuts, with a margin for
+//           the fp32 masses), the bins that may hold the draw, and whether they hold at most DCAP elements; then it
+//           publishes the plan's status.
+//   pick:   each slice waits for its row's plan (a bounded wait: past the limit the slice spoils the row, which then
+//           takes the exact path), reads its z back, adds the exact fixed-point mass of every element (fp64 exp, 2^-64
+//           resolution) to S and to the regions before and between the two windows, and lists the window elements.
+//           The row's last slice finishes: exact sub-bin counts and masses over the list locate the cut and the draw,
+//           only the sub-bins holding them are sorted, and their exact prefixes (one scan) give the last kept element,
+//           c_last and the token. A failed check leaves the row to the exact path (gse_exact.hip). It then clears the
+//           row's records for the next call.
 //
 // Semantics (goethe_engine/sampling.py:77-83): keep_r = r < top_k AND cumsum(q)_r - q_r < top_p (AND q_r >= min_p q_0);
 // c = cumsum(q keep); token = order[min(count(c < u c[-1]), m - 1)], m = keep.sum().
@@ -41,7 +43,7 @@ struct DeepShared {
     } c;
     uint64_t wl[WLC];           // pick pass: the slice's window elements
   };
-  uint32_t next, hover, ticket, nwl, wbase;
+  uint32_t next, hover, ticket, nwl, wbase, pstat;
   uint32_t wsum[NWV];
   uint64_t wred[NWV], wred2[NWV];
   double dred[NWV];
@@ -66,20 +68,6 @@ __device__ __forceinline__ uint64_t q40(float e) {
   return sh >= 0 ? m << sh : (sh > -64 ? m >> -sh : 0ull);
 }
 
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-  for (int m = 32; m; m >>= 1) v += shfl_xor_u64(v, m);
-  return v;
-}
-__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) {
-  const int l = lane_id();
-  for (int d = 1; d < WAVE; d <<= 1) {
-    const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)v, d, WAVE);
-    const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)(v >> 32), d, WAVE);
-    const uint64_t o = ((uint64_t)hi << 32) | lo;
-    if (l >= d) v += o;
-  }
-  return v;
-}
 
 __device__ __forceinline__ void atomic_add_ag(uint64_t *p, uint64_t v) {
   (void)__hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -144,7 +132,7 @@ __device__ __forceinline__ double block_excl_scan_f64(double v, double &tot, Dee
 // slice end), so f may use ballots. Ends with a barrier.
 template <int DT, bool AL, typename F>
 __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c, int row, int p0, int p1,
-                                             DeepShared &sh, F f) {
+                                             DeepShared &sh, float *zrow, F f) {
   using L = Lay<DT>;
   const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
   const int nfull = (p1 - p0) / CHK;
@@ -192,6 +180,21 @@ __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c,
     for (int v = 0; v < L::NV; ++v) asm volatile("" : "+v"(mw[v]));
     (void)chunk_phase1<DT>(a, c, row, cb, p0, p1, x, mw, ln, sh.h);
 #pragma unroll
+    for (int v = 0; v < L::NV; ++v) {  // z into the row's buffer (four elements per store)
+#pragma unroll
+      for (int q = 0; q < L::VEC; q += 4) {
+        const int t = cb + v * L::STRIDE + lane * L::VEC + q;
+        const int i = v * L::VEC + q;
+        if (t + 4 <= p1) {
+          *reinterpret_cast<float4 *>(zrow + t) = make_float4(x[i], x[i + 1], x[i + 2], x[i + 3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (t + e < p1) zrow[t + e] = x[i + e];
+        }
+      }
+    }
+#pragma unroll
     for (int v = 0; v < L::NV; ++v) {
 #pragma unroll
       for (int e = 0; e < L::VEC; ++e) {
@@ -220,8 +223,7 @@ __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c,
 }
 
 // Slices of the deep rows: as many per row as one round of the grid holds (the grid is resident at once), at most
-// DSMAX, each a multiple of CHK long and at most PTOK. Both launches see the same grid and row count, so they slice
-// alike. Item i of a launch is slice i % S of slot i / S.
+// DSMAX, each a multiple of CHK long and at most PTOK. Item i is slice i % S of slot i / S, in both phases.
 struct DGeom {
   int S, len;
 };
@@ -359,15 +361,16 @@ __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode
   n1 = wave_sum_u64(n1);
   n2 = wave_sum_u64(n2);
   const uint32_t status = (inw > 0 && inw <= (uint64_t)DCAP && S > 0.0 && fabsf(M) < INFINITY) ? DS_PLANNED : DS_FAIL;
-  if (l == 0) {
-    ds->w2lo = w2lo;
-    ds->w2hi = w2hi;
-    ds->w1lo = w1lo;
-    ds->w1hi = w1hi;
-    ds->status = status;
-    ds->acc[DA_C0] = n0;  // (the element counts of the regions the pick pass sums without listing)
-    ds->acc[DA_C1] = n1;
-    ds->acc[DA_C2] = n2;
+  if (l == 0) {  // the plan, then (once it is stored) its status, which the row's pick slices wait for
+    st_ag(&ds->w2lo, w2lo);
+    st_ag(&ds->w2hi, w2hi);
+    st_ag(&ds->w1lo, w1lo);
+    st_ag(&ds->w1hi, w1hi);
+    st_ag(&ds->acc[DA_C0], n0);  // (the element counts of the regions the pick pass sums without listing)
+    st_ag(&ds->acc[DA_C1], n1);
+    st_ag(&ds->acc[DA_C2], n2);
+    store_wait();
+    st_ag(&ds->status, status);
   }
 }
 
@@ -385,7 +388,8 @@ __device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slic
     sh.c.cnt[b] = 0;
     sh.c.mass[b] = 0;
   }
-  stream_slice<DT, AL>(a, c, row, p0, p1, sh, [&](float z, int, bool ok) __attribute__((always_inline)) {
+  stream_slice<DT, AL>(a, c, row, p0, p1, sh, a.dz + (size_t)slot * a.dz_ld,
+                       [&](float z, int, bool ok) __attribute__((always_inline)) {
     if (ok && z > -INFINITY) {
       const uint32_t b = dbin(z, M);
       atomicAdd(&sh.c.cnt[b], 1u);
@@ -406,19 +410,10 @@ __device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slic
   if (tid == 0) sh.ticket = ticket_add(&ds->cdone);
   __syncthreads();
   if (sh.ticket == (uint32_t)(g.S - 1) && tid < WAVE) {
+    __builtin_amdgcn_s_setprio(3);  // (the row's other slices wait for the plan)
     plan_row(gh, ds, a.mode);
     if (tid == 0) ds->cdone = 0u;
   }
-}
-
-// Four waves per SIMD: every workgroup of the grid resident at once.
-template <int DT, bool AL>
-__global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void deep_count_kernel(ScanArgs a) {
-  __shared__ DeepShared sh;
-  const int nd = (int)min(a.dctl[0], (uint32_t)DEEP_MAX);
-  if (nd == 0) return;
-  const DGeom g = deep_geom(a, nd);
-  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) count_item<DT, AL>(a, i / g.S, i % g.S, g, sh);
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -525,11 +520,11 @@ __device__ __noinline__ void finish_row(const FinArgs a, DeepSlot *ds, FinShared
   const int row = ds->row;
   const float Mf = ds->M;
   const double M = (double)Mf;
-  const uint32_t w2hi = ds->w2hi, w1lo = ds->w1lo;
+  const uint32_t w2hi = ld_ag(&ds->w2hi), w1lo = ld_ag(&ds->w1lo);
   const bool sep = w1lo > w2hi;  // an unlisted gap (region 1) between the draw window and the cut window
   const Fx X0{ld_ag(&ds->acc[DA_X0HI]), ld_ag(&ds->acc[DA_X0LO])}, X1{ld_ag(&ds->acc[DA_X1HI]), ld_ag(&ds->acc[DA_X1LO])};
   const Fx SF = fx_add(fx_add(X0, X1), Fx{ld_ag(&ds->acc[DA_RHI]), ld_ag(&ds->acc[DA_RLO])});
-  const uint64_t c0 = ds->acc[DA_C0], c1 = ds->acc[DA_C1], tail = ds->acc[DA_C2];
+  const uint64_t c0 = ld_ag(&ds->acc[DA_C0]), c1 = ld_ag(&ds->acc[DA_C1]), tail = ld_ag(&ds->acc[DA_C2]);
   const uint32_t nraw = ld_ag(&ds->lcnt);
   const double Sd = fx_val(SF);
   const uint64_t K = P.top_k > 0 ? (uint64_t)P.top_k : ~0ull;
@@ -547,11 +542,22 @@ __device__ __noinline__ void finish_row(const FinArgs a, DeepSlot *ds, FinShared
   sh.shi[tid] = 0;
   sh.slo[tid] = 0;
   __syncthreads();
-  for (int i = tid; i < n; i += MT) {
-    const uint32_t k = pk_key(ld_ag(&lst[i]));
-    const int g = (sep && dbin(fkey_inv(k), Mf) >= w1lo) ? 1 : 0;
-    atomicMax(&sh.kmax[g], k);
-    atomicMin(&sh.kmin[g], k);
+  {
+    uint32_t kx[2] = {0u, 0u}, kn[2] = {NONE, NONE};
+    for (int i = tid; i < n; i += MT) {
+      const uint32_t k = pk_key(ld_ag(&lst[i]));
+      const int g = (sep && dbin(fkey_inv(k), Mf) >= w1lo) ? 1 : 0;
+      kx[g] = max(kx[g], k);
+      kn[g] = min(kn[g], k);
+    }
+    for (int g = 0; g < 2; ++g) {  // (one LDS atomic per wave)
+      kx[g] = wave_max_u32(kx[g]);
+      kn[g] = wave_min_u32(kn[g]);
+      if (lane_id() == 0) {
+        atomicMax(&sh.kmax[g], kx[g]);
+        atomicMin(&sh.kmin[g], kn[g]);
+      }
+    }
   }
   __syncthreads();
   uint32_t shift[2];
@@ -754,30 +760,45 @@ union PickShared {
   FinShared f;
 };
 
-template <int DT, bool AL>
+// Wall-clock ticks (100 MHz) a pick slice waits for its row's plan. Every slice of the grid is resident at once, and
+// a plan takes microseconds; the limit only ends the wait when the device could not hold the whole grid.
+constexpr uint64_t PLAN_WAIT = 400000;  // 4 ms
+
 __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice, const DGeom &g, PickShared &ps,
                                           const double *etab) {
   DeepShared &sh = ps.d;
   const int tid = threadIdx.x;
   DeepSlot *ds = a.dslot + slot;
-  const int row = ds->row;
-  const gse_row P = ds->P;
   const float Mf = ds->M;
   const double M = (double)Mf;
-  const RowCtx c = make_ctx(a, row, P);
   const int p0 = slice * g.len, p1 = min(a.V, p0 + g.len);
-  // the plan (written by the count launch)
-  const uint32_t w2lo = ds->w2lo, w2hi = ds->w2hi, w1lo = ds->w1lo, w1hi = ds->w1hi;
-  const bool planned = ds->status == DS_PLANNED;
   __syncthreads();  // (LDS of the previous item)
-  if (tid == 0) sh.nwl = 0;
+  if (tid == 0) {
+    sh.nwl = 0;
+    uint32_t st = ld_ag(&ds->status);
+    if (st == DS_PENDING) {
+      const uint64_t t0 = wall_clock64();
+      while ((st = ld_ag(&ds->status)) == DS_PENDING) {
+        if (wall_clock64() - t0 > PLAN_WAIT) {
+          (void)__hip_atomic_fetch_or(&ds->spoil, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          st = DS_FAIL;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(16);  // (about 1000 clocks between polls)
+      }
+    }
+    sh.pstat = st;
+  }
+  __syncthreads();
+  const bool planned = sh.pstat == DS_PLANNED;
   if (planned) {
+    const uint32_t w2lo = ld_ag(&ds->w2lo), w2hi = ld_ag(&ds->w2hi), w1lo = ld_ag(&ds->w1lo), w1hi = ld_ag(&ds->w1hi);
     // per lane, exact fixed-point masses of three regions (before the draw window, between the windows, the rest):
     // whole multiples of 2^-40 and 2^-64, summed in fp64 (exact below 2^53)
     double h0 = 0.0, l0 = 0.0, h1 = 0.0, l1 = 0.0, h2 = 0.0, l2 = 0.0;
-    stream_slice<DT, AL>(a, c, row, p0, p1, sh, [&](float z, int t, bool ok) __attribute__((always_inline)) {
+    auto elem = [&](float z, int t) __attribute__((always_inline)) {
       bool inw = false;
-      if (ok && z > -INFINITY) {
+      if (z > -INFINITY) {
         const uint32_t b = dbin(z, Mf);
         const double s = exp_nonpos((double)z - M, etab) * 1099511627776.0;  // 2^40
         const double hi = floor(s), lo = floor((s - hi) * 16777216.0);  // (fx_of)
@@ -797,7 +818,29 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
         const uint32_t pos = atomicAdd(&sh.nwl, 1u);
         if (pos < (uint32_t)WLC) sh.wl[pos] = pack(fkey(z), (uint32_t)t);
       }
-    });
+    };
+    // the slice's z, as the count phase of this workgroup wrote it: four vectors per thread in flight, loaded
+    // unconditionally (a vector past the slice end reloads the slice's first one and is skipped; a vector that starts
+    // below p1 lies inside the row's buffer, whose length is a multiple of 64)
+    const float *zr = a.dz + (size_t)slot * a.dz_ld;
+    constexpr int PV = 4;
+#pragma unroll 1
+    for (int t0 = p0; t0 < p1; t0 += PV * MT * 4) {
+      float4 v[PV];
+#pragma unroll
+      for (int j = 0; j < PV; ++j) {
+        const int t = t0 + (j * MT + tid) * 4;
+        v[j] = *reinterpret_cast<const float4 *>(zr + (t < p1 ? t : p0));
+      }
+#pragma unroll
+      for (int j = 0; j < PV; ++j) {
+        const int t = t0 + (j * MT + tid) * 4;
+        const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (t + k < p1) elem(e[k], t + k);
+      }
+    }
     // the slice's sums into the row record (per wave; integer adds, any order), its window elements into the row list
     const uint64_t hv[6] = {(uint64_t)h0, (uint64_t)l0, (uint64_t)h1, (uint64_t)l1, (uint64_t)h2, (uint64_t)l2};
 #pragma unroll
@@ -805,6 +848,7 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
       const uint64_t v = wave_sum_u64(hv[k]);
       if (lane_id() == 0 && v) atomic_add_ag(&ds->acc[DA_X0HI + k], v);
     }
+    __syncthreads();  // (sh.nwl)
     const uint32_t nw = sh.nwl;
     if (tid == 0 && nw) {
       // a slice with more window elements than it can hold spoils the row's count (the row takes the exact path)
@@ -826,7 +870,9 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
   if (tid == 0) sh.ticket = ticket_add(&ds->pdone);
   __syncthreads();
   if (sh.ticket != (uint32_t)(g.S - 1)) return;
-  if (planned) finish_row(FinArgs{a.dlist + (size_t)slot * DCAP, a.info, a.tokens, a.mode}, ds, ps.f, etab);
+  __builtin_amdgcn_s_setprio(3);  // (the finish is the row's critical path)
+  if (planned && ld_ag(&ds->spoil) == 0u)
+    finish_row(FinArgs{a.dlist + (size_t)slot * DCAP, a.info, a.tokens, a.mode}, ds, ps.f, etab);
   __syncthreads();  // (every thread has read the row's sums)
   uint64_t *gh = a.dhist + (size_t)slot * 2 * DNB;
   for (int b = tid; b < 2 * DNB; b += MT) gh[b] = 0;
@@ -834,25 +880,27 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
   if (tid == 0) {
     ds->lcnt = 0;
     ds->pdone = 0;
+    ds->spoil = 0;
   }
 }
 
+// Four waves per SIMD: every workgroup of the grid resident at once. All count items of a workgroup come before its
+// pick items, so a pick item only waits for count work that never waits itself.
 template <int DT, bool AL>
-__global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void deep_pick_kernel(ScanArgs a) {
+__global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void deep_kernel(ScanArgs a) {
   __shared__ PickShared sh;
   __shared__ double etab[64];
   const int nd = (int)min(a.dctl[0], (uint32_t)DEEP_MAX);
   if (nd == 0) return;
   if (threadIdx.x < 64) etab[threadIdx.x] = EXP2_64[threadIdx.x];  // (published by the first barrier of an item)
   const DGeom g = deep_geom(a, nd);
-  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) pick_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab);
+  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) count_item<DT, AL>(a, i / g.S, i % g.S, g, sh.d);
+  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) pick_item(a, i / g.S, i % g.S, g, sh, etab);
 }
 
 template <int DT, bool AL>
 void launch_all(const ScanArgs &a, hipStream_t s) {
-  dim3 grid((unsigned)a.dgrid), block(MT);
-  hipLaunchKernelGGL((deep_count_kernel<DT, AL>), grid, block, 0, s, a);
-  hipLaunchKernelGGL((deep_pick_kernel<DT, AL>), grid, block, 0, s, a);
+  hipLaunchKernelGGL((deep_kernel<DT, AL>), dim3((unsigned)a.dgrid), dim3(MT), 0, s, a);
 }
 
 }  // namespace

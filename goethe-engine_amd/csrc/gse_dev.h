@@ -110,43 +110,70 @@ __device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  for (int m = 32; m; m >>= 1) {
-    uint64_t o = shfl_xor_u64(v, m);
-    v = o > v ? o : v;
+// Cross-lane moves through DPP (VALU, no LDS round trip): lane l receives v from the lane that CTRL names, or id where
+// there is none or its row (16 lanes) is not in ROWM.
+template <int CTRL, int ROWM>
+__device__ __forceinline__ uint32_t dpp32(uint32_t id, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)id, (int)v, CTRL, ROWM, 0xF, false);
+}
+template <int CTRL, int ROWM, typename T>
+__device__ __forceinline__ T dpp_mov(T id, T v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, dpp32<CTRL, ROWM>(__builtin_bit_cast(uint32_t, id), __builtin_bit_cast(uint32_t, v)));
+  } else {
+    const uint64_t i = __builtin_bit_cast(uint64_t, id), x = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = dpp32<CTRL, ROWM>((uint32_t)i, (uint32_t)x);
+    const uint32_t hi = dpp32<CTRL, ROWM>((uint32_t)(i >> 32), (uint32_t)(x >> 32));
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
   }
+}
+// Inclusive scan over the 64 lanes (all active) with op and its identity id, in a fixed association: inside each row
+// of 16 lanes by row shifts of 1, 2, 4 and 8, then across rows by the broadcasts of lanes 15 and 31.
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_scan(T v, T id, Op op) {
+  v = op(v, dpp_mov<0x111, 0xF>(id, v));  // row_shr:1
+  v = op(v, dpp_mov<0x112, 0xF>(id, v));  // row_shr:2
+  v = op(v, dpp_mov<0x114, 0xF>(id, v));  // row_shr:4
+  v = op(v, dpp_mov<0x118, 0xF>(id, v));  // row_shr:8
+  v = op(v, dpp_mov<0x142, 0xA>(id, v));  // row_bcast:15 into rows 1 and 3
+  v = op(v, dpp_mov<0x143, 0xC>(id, v));  // row_bcast:31 into rows 2 and 3
   return v;
 }
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  for (int m = 32; m; m >>= 1) v = max(v, shfl_xor_u32(v, m));
-  return v;
-}
-__device__ __forceinline__ double wave_sum_f64(double v) {
-  for (int m = 32; m; m >>= 1) {
-    int2 b = *reinterpret_cast<int2 *>(&v);
-    b.x = __shfl_xor(b.x, m, WAVE);
-    b.y = __shfl_xor(b.y, m, WAVE);
-    v += *reinterpret_cast<double *>(&b);
+// The value of lane 63 (wave-uniform).
+template <typename T>
+__device__ __forceinline__ T lane63(T v) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+  } else {
+    const uint64_t x = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), 63);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
   }
-  return v;
 }
-// Inclusive prefix sum over the 64 lanes (Hillis-Steele, fixed association).
-__device__ __forceinline__ double wave_incl_scan_f64(double v) {
-  int l = lane_id();
-  for (int d = 1; d < WAVE; d <<= 1) {
-    double o = shfl_up_f64(v, d);
-    if (l >= d) v += o;
-  }
-  return v;
-}
-__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
-  int l = lane_id();
-  for (int d = 1; d < WAVE; d <<= 1) {
-    uint32_t o = (uint32_t)__shfl_up((int)v, d, WAVE);
-    if (l >= d) v += o;
-  }
-  return v;
-}
+
+struct OpAdd {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
+};
+struct OpMax {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T a, T b) const { return a > b ? a : b; }
+};
+struct OpMin {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T a, T b) const { return a < b ? a : b; }
+};
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) { return lane63(wave_scan(v, (uint64_t)0, OpMax{})); }
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) { return lane63(wave_scan(v, 0u, OpMax{})); }
+__device__ __forceinline__ double wave_sum_f64(double v) { return lane63(wave_scan(v, 0.0, OpAdd{})); }
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) { return lane63(wave_scan(v, (uint64_t)0, OpAdd{})); }
+// Inclusive prefix sums over the 64 lanes (fixed association).
+__device__ __forceinline__ double wave_incl_scan_f64(double v) { return wave_scan(v, 0.0, OpAdd{}); }
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) { return wave_scan(v, 0u, OpAdd{}); }
+__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) { return wave_scan(v, (uint64_t)0, OpAdd{}); }
 
 // Bitonic sort of one u32 per lane across the wave, descending: lane i ends with the i-th largest value.
 __device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) {
@@ -189,17 +216,10 @@ __device__ __forceinline__ uint32_t wave_kth_largest_u16(uint32_t v, int k) {
 }
 
 __device__ __forceinline__ float wave_max_f32(float v) {
-  for (int m = 32; m; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, WAVE));
-  return v;
+  return lane63(wave_scan(v, -INFINITY, [](float x, float y) { return fmaxf(x, y); }));
 }
-__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-  for (int m = 32; m; m >>= 1) v += shfl_xor_u32(v, m);
-  return v;
-}
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-  for (int m = 32; m; m >>= 1) v = min(v, shfl_xor_u32(v, m));
-  return v;
-}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) { return lane63(wave_scan(v, 0u, OpAdd{})); }
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return lane63(wave_scan(v, 0xFFFFFFFFu, OpMin{})); }
 __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }

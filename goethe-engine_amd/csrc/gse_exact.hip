@@ -87,10 +87,6 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, ExactShared &sh) {
   return r;
 }
 
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-  for (int m = 32; m; m >>= 1) v += shfl_xor_u64(v, m);
-  return v;
-}
 
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, ExactShared &sh) {
   v = wave_sum_u64(v);
@@ -115,16 +111,6 @@ __device__ __forceinline__ double block_sum_f64(double v, ExactShared &sh) {
   return r;
 }
 
-__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) {
-  const int l = lane_id();
-  for (int d = 1; d < WAVE; d <<= 1) {
-    const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)v, d, WAVE);
-    const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)(v >> 32), d, WAVE);
-    const uint64_t o = ((uint64_t)hi << 32) | lo;
-    if (l >= d) v += o;
-  }
-  return v;
-}
 
 // Exclusive block scan of two u64 values per thread (in thread order).
 __device__ __forceinline__ void block_excl_scan2(uint64_t &a, uint64_t &b, ExactShared &sh) {

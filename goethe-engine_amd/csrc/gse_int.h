@@ -79,7 +79,9 @@ struct DeepSlot {    // 256 bytes, one per deep row of a call
   uint32_t lcnt;                    // listed window elements
   uint32_t cdone, pdone;            // slice tickets of the two passes (zero between calls)
   uint64_t acc[DA_N];               // pick-pass sums (atomic adds; zero between calls)
-  uint64_t pad[8];
+  uint32_t spoil;                   // a slice gave up waiting for the plan: the exact path takes the row (zero between calls)
+  uint32_t pad32;
+  uint64_t pad[7];
 };
 static_assert(sizeof(DeepSlot) == 256, "");
 
@@ -120,6 +122,8 @@ struct ScanArgs {
   DeepSlot *dslot;   // [DEEP_MAX]
   uint64_t *dhist;   // [DEEP_MAX][2][DNB]: per bin, element count and fixed-point mass (2^-40 units), atomic adds
   uint64_t *dlist;   // [DEEP_MAX][DCAP]: packed keys of the window elements
+  float *dz;         // [DEEP_MAX][dz_ld]: z of the deep rows, written by the count phase, read back by the pick phase
+  int64_t dz_ld;
   int dslices, dgrid;  // split-row finish enabled (slices per deep row, at most), workgroups per pass
 };
 
