@@ -174,7 +174,7 @@ def main():
         step(k, profile=True)
     torch.cuda.synchronize()
     calls, kms = h.profile()
-    kern = ["main_kernel", "deep (count + pick)", "exact_kernel"]
+    kern = ["main_kernel", "deep_kernel", "exact_kernel"]
     per = {kern[i]: kms[i] / calls * 1e3 for i in range(min(len(kern), len(kms)))}
     ms_per_step = wall * 1e3 / args.steps
     value = rows * args.steps / wall

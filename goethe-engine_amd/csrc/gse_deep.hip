@@ -429,9 +429,12 @@ __device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slic
 constexpr int NSB = 256;        // sub-bins (128 per window)
 constexpr int SUBC = 2048;      // entries of one sub-bin that can be collected
 constexpr int SW = SUBC / MT;   // sorted entries per thread in the walks
+constexpr int LC = 2048;        // window entries the finish copies into LDS (the rest it reads from the list)
+static_assert(LC <= DCAP && LC % MT == 0, "");
 constexpr uint32_t NONE = 0xFFFFFFFFu;
 
 struct FinShared {
+  uint64_t lc[LC];              // the first LC window entries
   uint64_t sub[SUBC];           // the collected entries of one sub-bin, sorted
   uint32_t scnt[NSB];           // sub-bin counts, then their exclusive prefix
   uint32_t stop[NSB];           // sub-bin head keys (largest key)
@@ -505,7 +508,7 @@ __device__ __forceinline__ Fx mass_of(uint32_t key, double M, const double *etab
   return fx_of(exp_nonpos((double)fkey_inv(key) - M, etab));
 }
 
-// What the finish uses of the launch arguments (by value: the pick kernel keeps its arguments in registers).
+// What the finish uses of the launch arguments (by value: the kernel keeps its arguments in registers).
 struct FinArgs {
   const uint64_t *lst;  // the row's window list
   RowInfo *info;
@@ -532,6 +535,16 @@ __device__ __noinline__ void finish_row(const FinArgs a, DeepSlot *ds, FinShared
   const bool ok0 = nraw > 0 && nraw <= (uint32_t)DCAP && Sd > 0.0;
   const int n = ok0 ? (int)nraw : 0;
   const uint64_t *lst = a.lst;
+  // the list's first LC entries into LDS, every load issued before the first is used (entries past n are stale and
+  // never read)
+  {
+    uint64_t v[LC / MT];
+#pragma unroll
+    for (int j = 0; j < LC / MT; ++j) v[j] = ld_ag(&lst[j * MT + tid]);
+#pragma unroll
+    for (int j = 0; j < LC / MT; ++j) sh.lc[j * MT + tid] = v[j];
+  }
+  auto entry = [&](int i) -> uint64_t { return i < LC ? sh.lc[i] : ld_ag(&lst[i]); };
   // key ranges of the two windows
   if (tid < 2) {
     sh.kmax[tid] = 0;
@@ -545,7 +558,7 @@ __device__ __noinline__ void finish_row(const FinArgs a, DeepSlot *ds, FinShared
   {
     uint32_t kx[2] = {0u, 0u}, kn[2] = {NONE, NONE};
     for (int i = tid; i < n; i += MT) {
-      const uint32_t k = pk_key(ld_ag(&lst[i]));
+      const uint32_t k = pk_key(entry(i));
       const int g = (sep && dbin(fkey_inv(k), Mf) >= w1lo) ? 1 : 0;
       kx[g] = max(kx[g], k);
       kn[g] = min(kn[g], k);
@@ -569,7 +582,7 @@ __device__ __noinline__ void finish_row(const FinArgs a, DeepSlot *ds, FinShared
   }
   // exact sub-bin counts, masses and head keys
   for (int i = tid; i < n; i += MT) {
-    const uint32_t k = pk_key(ld_ag(&lst[i]));
+    const uint32_t k = pk_key(entry(i));
     const int b = sub_of(k, shift, sep, w1lo, Mf, sh);
     const Fx f = mass_of(k, M, etab);
     atomicAdd(&sh.scnt[b], 1u);
@@ -660,7 +673,7 @@ __device__ __noinline__ void finish_row(const FinArgs a, DeepSlot *ds, FinShared
     if (tid == 0) sh.ns = 0;
     __syncthreads();
     for (int i = tid; i < n; i += MT) {
-      const uint64_t pk = ld_ag(&lst[i]);
+      const uint64_t pk = entry(i);
       if (sub_of(pk_key(pk), shift, sep, w1lo, Mf, sh) == sb) {
         const uint32_t pos = atomicAdd(&sh.ns, 1u);
         if (pos < (uint32_t)SUBC) sh.sub[pos] = pk;

@@ -114,7 +114,7 @@ struct ScanArgs {
   float *lps;
   int64_t lp_ld;
   SliceRec *rec;    // [rows][nparts]: one record per part
-  uint64_t *cand;   // [rows][nparts][PWAVES][CAPW]
+  uint64_t *cand;   // [rows][nparts][PWAVES][CAPW]: listed elements, (bits of z) << 32 | token
   RowInfo *info;
   uint32_t *done;   // [rows] slice tickets, zero between calls
   // split-row finish

@@ -73,6 +73,14 @@ struct Shared {
   double etab[64];             // 2^(j / 64) for exp_nonpos
 };
 
+// A listed element as the stream writes it: the bits of z over the token (the resolve packs it into a sort key).
+__device__ __forceinline__ uint64_t raw_entry(float z, uint32_t tok) {
+  return ((uint64_t)__float_as_uint(z) << 32) | tok;
+}
+__device__ __forceinline__ uint64_t key_of_raw(uint64_t r) {
+  return pack(fkey(__uint_as_float((uint32_t)(r >> 32))), (uint32_t)r);
+}
+
 __device__ __forceinline__ void lp_invalid(const ScanArgs &a, int row, int nlp) {
   for (int i = threadIdx.x; i < nlp; i += MT) {
     a.lp_ids[(int64_t)row * a.lp_ld + i] = -1;
@@ -421,7 +429,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
           if (sh.loff[mid] <= f) lo = mid;
           else hi = mid - 1;
         }
-        pk[g] = ld_ag(&cl0[(size_t)lo * CAPW + (f - sh.loff[lo])]);
+        pk[g] = key_of_raw(ld_ag(&cl0[(size_t)lo * CAPW + (f - sh.loff[lo])]));
       }
     }
     // (through LDS, so that the processing loop stays rolled: this code runs once per row, with a cold instruction
@@ -614,6 +622,8 @@ __device__ __forceinline__ float chunk_z(const RowCtx &c, int cb, int p0, int pv
   }
   float cmax = -INFINITY;
 #pragma unroll
+  for (int i = 0; i < EPL; i += 2) rn.nanm |= ballot64(__builtin_isunordered(xr[i], xr[i + 1]));  // (a NaN in either)
+#pragma unroll
   for (int v = 0; v < L::NV; ++v) {
     const int t0 = cb + v * L::STRIDE + l * L::VEC;
     const uint32_t keep = (MASKED ? (mw[v] >> ((l * L::VEC) & 31)) : VMASK) & inr[v];
@@ -621,7 +631,6 @@ __device__ __forceinline__ float chunk_z(const RowCtx &c, int cb, int p0, int pv
     for (int k = 0; k < L::VEC; ++k) {
       const int i = v * L::VEC + k;
       const float x = xr[i];
-      rn.nanm |= ballot64(x != x);
       const float xm = keep_or_ninf(x, keep, k);
       if constexpr (GREEDY) {  // masked tokens take part in the argmax as -FLT_MAX
         const float g = fminf(fmaxf(xm, -FLTMAX), FLTMAX);
@@ -691,7 +700,7 @@ __device__ __forceinline__ void chunk_sum(const ScanArgs &a, int row, int wl, fl
       if (bl) {
         if (p) {
           const uint32_t pos = woff + lanes_below(bl);
-          if (pos < (uint32_t)CAPW) st_ag(&cl[pos], pack(fkey(zr[i]), tok(i)));
+          if (pos < (uint32_t)CAPW) st_ag(&cl[pos], raw_entry(zr[i], tok(i)));
           e[i] = 0.0f;
         }
         woff += (uint32_t)__popcll(bl);
