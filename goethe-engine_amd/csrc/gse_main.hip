@@ -789,30 +789,41 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
       hid[k] = j < c.he ? a.hist[j] : -1;
     }
   }
-  // allowed tokens of the part's stream range (masked rows: popcounts of its mask words; they load with the history)
-  uint32_t apc = 0;
-  if constexpr (MASKED) {
-    const int nw = (pv - p0 + 31) >> 5;
-    for (int i = tid; i < nw; i += MT) {
-      uint32_t word = c.mw[(p0 >> 5) + i];
-      const int below = pv - (p0 + 32 * i);  // tokens of this word below pv (>= 1)
-      if (below < 32) word &= (1u << below) - 1u;
-      apc += (uint32_t)__popc(word);
-    }
-  } else {
-    apc = tid == 0 ? (uint32_t)(pv - p0) : 0u;
-  }
   float xa[EPL], xb[EPL], xc[EPL];
   uint32_t ma[L::NV], mb[L::NV], mcw[L::NV];
   int c0 = w, c1 = w + NWV;  // chunks 0..7 go to waves 0..3 two by two; later ones from the LDS counter
   load_u<DT, AL, MASKED>(c, p0 + c0 * CHK, pv, p1, xa, ma);
   load_u<DT, AL, MASKED>(c, p0 + c1 * CHK, pv, p1, xb, mb);
+  // allowed tokens of the part's stream range (masked rows: popcounts of its mask words, every load issued before the
+  // first is used; the sum comes after the history build)
+  constexpr int APW = (PTOK / 32 + MT - 1) / MT;  // mask words per thread
+  const int nmw = (pv - p0 + 31) >> 5;
+  uint32_t mwd[APW];
+  if constexpr (MASKED) {
+#pragma unroll
+    for (int k = 0; k < APW; ++k) mwd[k] = c.mw[(p0 >> 5) + max(min(tid + k * MT, nmw - 1), 0)];
+  }
   if (tid == 0) {
     sh.next = 2 * NWV;
     sh.hover = 0;
   }
   if (c.pen) build_history(c, a.hist, hid, p0, p1, sh.h, sh.wcnt, sh.hover);
   else __syncthreads();
+  uint32_t apc = 0;
+  if constexpr (MASKED) {
+#pragma unroll
+    for (int k = 0; k < APW; ++k) {
+      const int i = tid + k * MT;
+      if (i < nmw) {
+        uint32_t word = mwd[k];
+        const int below = pv - (p0 + 32 * i);  // tokens of this word below pv (>= 1)
+        if (below < 32) word &= (1u << below) - 1u;
+        apc += (uint32_t)__popc(word);
+      }
+    }
+  } else {
+    apc = tid == 0 ? (uint32_t)(pv - p0) : 0u;
+  }
 
   Run rn;
   rn.m = -INFINITY;
