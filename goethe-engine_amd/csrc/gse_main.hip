@@ -421,21 +421,18 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
 #pragma unroll
     for (int g = 0; g < GPT; ++g) {
       const uint32_t f = f0 + g * MT + tid;
-      pk[g] = 0;
-      if (f < ltot) {
-        int lo = 0, hi = nsl - 1;  // the wave list whose range [loff, loff + count) holds f
-        while (lo < hi) {
-          const int mid = (lo + hi + 1) >> 1;
-          if (sh.loff[mid] <= f) lo = mid;
-          else hi = mid - 1;
-        }
-        pk[g] = key_of_raw(ld_ag(&cl0[(size_t)lo * CAPW + (f - sh.loff[lo])]));
+      int lo = 0;  // the wave list whose range [loff, loff + count) holds f: the last with loff <= f (fixed steps)
+#pragma unroll
+      for (int st = NSL / 2; st > 0; st >>= 1) {
+        const int m = lo + st;
+        if (m < nsl && sh.loff[m] <= f) lo = m;
       }
+      pk[g] = f < ltot ? ld_ag(&cl0[(size_t)lo * CAPW + min(f - sh.loff[lo], (uint32_t)CAPW - 1u)]) : 0ull;
     }
     // (through LDS, so that the processing loop stays rolled: this code runs once per row, with a cold instruction
     // cache, and its length is its cost)
 #pragma unroll
-    for (int g = 0; g < GPT; ++g) sh.r.tmp[g * MT + tid] = pk[g];
+    for (int g = 0; g < GPT; ++g) sh.r.tmp[g * MT + tid] = f0 + g * MT + tid < ltot ? key_of_raw(pk[g]) : 0ull;
 #pragma unroll 1
     for (int g = 0; g < GPT; ++g) {
       const uint64_t v = sh.r.tmp[g * MT + tid];
