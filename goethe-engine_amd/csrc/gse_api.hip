@@ -201,8 +201,8 @@ GSE_API int gse_open(const gse_open_params *p, gse_handle **out) {
       (e = hipMalloc(&h->dctl, 64)) != hipSuccess || (e = hipMemset(h->dctl, 0, 64)) != hipSuccess ||
       (e = hipMalloc(&h->dslot, gse::DEEP_MAX * sizeof(gse::DeepSlot))) != hipSuccess ||
       (e = hipMemset(h->dslot, 0, gse::DEEP_MAX * sizeof(gse::DeepSlot))) != hipSuccess ||
-      (e = hipMalloc(&h->dhist, (size_t)gse::DEEP_MAX * 2 * gse::DNB * sizeof(uint64_t))) != hipSuccess ||
-      (e = hipMemset(h->dhist, 0, (size_t)gse::DEEP_MAX * 2 * gse::DNB * sizeof(uint64_t))) != hipSuccess ||
+      (e = hipMalloc(&h->dhist, (size_t)gse::DEEP_MAX * 3 * gse::DNB * sizeof(uint64_t))) != hipSuccess ||
+      (e = hipMemset(h->dhist, 0, (size_t)gse::DEEP_MAX * 3 * gse::DNB * sizeof(uint64_t))) != hipSuccess ||
       (e = hipMalloc(&h->dlist, (size_t)gse::DEEP_MAX * gse::DCAP * sizeof(uint64_t))) != hipSuccess ||
       (e = hipMalloc(&h->dz, dzn * sizeof(float))) != hipSuccess ||
       (e = hipDeviceSynchronize()) != hipSuccess) {

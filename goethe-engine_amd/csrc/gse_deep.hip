@@ -6,14 +6,13 @@
 // carries on with the row. Every workgroup runs all its count items before any pick item.
 //
 //   count:  each slice recomputes z exactly as the main pass does, keeps it (dz), and adds a 512-bin histogram of
-//           d = z_max - z (counts, and masses exp2 in fp32 summed as 2^-40 fixed point; bins 1/32 wide, the last one
-//           open-ended). d is monotone in z, so the bins follow the stable order and ties share a bin. The row's last
-//           slice plans: the bins that may hold the last kept element (top-p, top-k and min-p cuts, with a margin for
-//           the fp32 masses), the bins that may hold the draw, and whether they hold at most DCAP elements; then it
-//           publishes the plan's status.
+//           d = z_max - z: counts and exact fixed-point masses (fp64 exp, whole multiples of 2^-40 and 2^-64; bins
+//           1/32 wide, the last one open-ended). d is monotone in z, so the bins follow the stable order and ties share
+//           a bin. The row's last slice plans: the bins that hold the last kept element (top-p, top-k and min-p cuts)
+//           and the bins that may hold the draw, whether they hold at most DCAP elements, and the exact masses of the
+//           regions before and between them; then it publishes the plan's status.
 //   pick:   each slice waits for its row's plan (a bounded wait: past the limit the slice spoils the row, which then
-//           takes the exact path), reads its z back, adds the exact fixed-point mass of every element (fp64 exp, 2^-64
-//           resolution) to S and to the regions before and between the two windows, and lists the window elements.
+//           takes the exact path), reads its z back and lists the window elements.
 //           The row's last slice finishes: exact sub-bin counts and masses over the list locate the cut and the draw,
 //           only the sub-bins holding them are sorted, and their exact prefixes (one scan) give the last kept element,
 //           c_last and the token. A failed check leaves the row to the exact path (gse_exact.hip). It then clears the
@@ -38,8 +37,8 @@ struct DeepShared {
   HistTab h;                    // the slice's history tables while streaming
   union {
     struct {
-      uint32_t cnt[DNB];        // count pass: the slice's histogram
-      uint64_t mass[DNB];
+      uint64_t hi[DNB];         // count pass: the slice's histogram, mass in 2^-40 units
+      uint64_t lo[DNB];         // mass in 2^-64 units (below 2^40), element count << 48
     } c;
     uint64_t wl[WLC];           // pick pass: the slice's window elements
   };
@@ -58,70 +57,8 @@ __device__ __forceinline__ uint32_t dbin(float z, float M) {
   return (uint32_t)fminf((M - z) * BSC, (float)(DNB - 1));
 }
 
-// floor(e * 2^40) for an fp32 e in [0, 1], exact integer arithmetic on its bits.
-__device__ __forceinline__ uint64_t q40(float e) {
-  const uint32_t b = __float_as_uint(e);
-  const int ex = (int)(b >> 23);
-  if (ex == 0) return 0;  // zero (subnormals are flushed)
-  const uint64_t m = (uint64_t)((b & 0x7FFFFFu) | 0x800000u);
-  const int sh = ex - 127 - 23 + 40;
-  return sh >= 0 ? m << sh : (sh > -64 ? m >> -sh : 0ull);
-}
-
-
 __device__ __forceinline__ void atomic_add_ag(uint64_t *p, uint64_t v) {
   (void)__hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, DeepShared &sh) {
-  v = wave_sum_u64(v);
-  __syncthreads();
-  if (lane_id() == 0) sh.wred[threadIdx.x >> 6] = v;
-  __syncthreads();
-  uint64_t r = 0;
-#pragma unroll
-  for (int w = 0; w < NWV; ++w) r += sh.wred[w];
-  __syncthreads();
-  return r;
-}
-
-// Exclusive prefix of two u64 values per thread, in thread order.
-__device__ __forceinline__ void block_excl_scan2(uint64_t &a, uint64_t &b, DeepShared &sh) {
-  const uint64_t ia = wave_incl_scan_u64(a), ib = wave_incl_scan_u64(b);
-  __syncthreads();
-  if (lane_id() == WAVE - 1) {
-    sh.wred[threadIdx.x >> 6] = ia;
-    sh.wred2[threadIdx.x >> 6] = ib;
-  }
-  __syncthreads();
-  uint64_t pa = 0, pb = 0;
-  const int w = threadIdx.x >> 6;
-#pragma unroll
-  for (int k = 0; k < NWV; ++k) {
-    pa += k < w ? sh.wred[k] : 0ull;
-    pb += k < w ? sh.wred2[k] : 0ull;
-  }
-  a = pa + ia - a;
-  b = pb + ib - b;
-  __syncthreads();
-}
-
-// Exclusive prefix of an fp64 value per thread in thread order (fixed association); tot receives the total.
-__device__ __forceinline__ double block_excl_scan_f64(double v, double &tot, DeepShared &sh) {
-  const double inc = wave_incl_scan_f64(v);
-  __syncthreads();
-  if (lane_id() == WAVE - 1) sh.dred[threadIdx.x >> 6] = inc;
-  __syncthreads();
-  double pre = 0.0, t = 0.0;
-  const int w = threadIdx.x >> 6;
-#pragma unroll
-  for (int k = 0; k < NWV; ++k) {
-    if (k < w) pre += sh.dred[k];
-    t += sh.dred[k];
-  }
-  __syncthreads();
-  tot = t;
-  return pre + inc - v;
 }
 
 // Streams the slice [p0, p1) of the row through the main pass's element pipeline. The full chunks go through a
@@ -245,19 +182,21 @@ __device__ __forceinline__ DGeom deep_geom(const ScanArgs &a, int nd) {
 constexpr int PBL = DNB / WAVE;  // bins per lane
 static_assert(PBL * WAVE == DNB, "");
 
-__device__ __forceinline__ uint32_t first_bin(bool hit, uint32_t b) { return wave_min_u32(hit ? b : (uint32_t)DNB - 1u); }
-
 __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode) {
   const int l = lane_id();
   const gse_row &P = ds->P;
   const float M = ds->M;
-  uint64_t c[PBL];
+  uint64_t c[PBL], mh[PBL], mo[PBL];
   double m[PBL];
   uint64_t cl = 0;
   double ml = 0.0;
   for (int j = 0; j < PBL; ++j) {
     c[j] = ld_ag(&gh[l * PBL + j]);
-    m[j] = (double)ld_ag(&gh[DNB + l * PBL + j]) * 9.094947017729282e-13;  // 2^-40
+    mh[j] = ld_ag(&gh[DNB + l * PBL + j]);
+    mo[j] = ld_ag(&gh[2 * DNB + l * PBL + j]);
+  }
+  for (int j = 0; j < PBL; ++j) {
+    m[j] = fx_val(Fx{mh[j], mo[j]});
     cl += c[j];
     ml += m[j];
   }
@@ -265,8 +204,8 @@ __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode
   const double S = shfl_f64(mi, WAVE - 1);
   const uint64_t ci = wave_incl_scan_u64(cl);
   const uint64_t ctot = shfl_u64(ci, WAVE - 1);
-  // the fp32 exp2 terms (2 ulp) and the 2^-40 floors stay far inside this margin
-  const double delta = 1e-4 * S;
+  // the masses are exact; the margin covers the fp64 roundings of their prefix sums here (the finish decides exactly)
+  const double delta = 1e-12 * S;
   const uint64_t K = P.top_k > 0 ? (uint64_t)P.top_k : ~0ull;
   const double tS = P.top_p * S;
   // min-p keeps exp(z - M) >= min_p, i.e. d <= -ln(min_p): bins below bm - 1 are all kept, bins above bm + 1 all cut
@@ -349,17 +288,22 @@ __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode
     w1hi = w2hi;
   }
   uint64_t inw = 0, n0 = 0, n1 = 0, n2 = 0;
+  uint64_t xm[6] = {0, 0, 0, 0, 0, 0};  // exact masses (2^-40, 2^-64 parts): before the draw window, between, the rest
   for (int j = 0; j < PBL; ++j) {
     const uint32_t b = l * PBL + j;
     if ((b >= w2lo && b <= w2hi) || (b >= w1lo && b <= w1hi)) inw += c[j];
     else if (b < w2lo) n0 += c[j];
     else if (b < w1lo) n1 += c[j];
     else n2 += c[j];
+    const int r = b < w2lo ? 0 : (b > w2hi && b < w1lo) ? 1 : 2;
+    xm[2 * r] += mh[j];
+    xm[2 * r + 1] += mo[j];
   }
   inw = wave_sum_u64(inw);
   n0 = wave_sum_u64(n0);
   n1 = wave_sum_u64(n1);
   n2 = wave_sum_u64(n2);
+  for (int k = 0; k < 6; ++k) xm[k] = wave_sum_u64(xm[k]);
   const uint32_t status = (inw > 0 && inw <= (uint64_t)DCAP && S > 0.0 && fabsf(M) < INFINITY) ? DS_PLANNED : DS_FAIL;
   if (l == 0) {  // the plan, then (once it is stored) its status, which the row's pick slices wait for
     st_ag(&ds->w2lo, w2lo);
@@ -369,39 +313,44 @@ __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode
     st_ag(&ds->acc[DA_C0], n0);  // (the element counts of the regions the pick pass sums without listing)
     st_ag(&ds->acc[DA_C1], n1);
     st_ag(&ds->acc[DA_C2], n2);
+    for (int k = 0; k < 6; ++k) st_ag(&ds->acc[DA_X0HI + k], xm[k]);
     store_wait();
     st_ag(&ds->status, status);
   }
 }
 
 template <int DT, bool AL>
-__device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slice, const DGeom &g, DeepShared &sh) {
+__device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slice, const DGeom &g, DeepShared &sh,
+                                           const double *etab) {
   const int tid = threadIdx.x;
   DeepSlot *ds = a.dslot + slot;
   const int row = ds->row;
   const gse_row P = ds->P;
   const float M = ds->M;
+  const double Md = (double)M;
   const RowCtx c = make_ctx(a, row, P);
   const int p0 = slice * g.len, p1 = min(a.V, p0 + g.len);
   __syncthreads();  // (LDS of the previous item)
   for (int b = tid; b < DNB; b += MT) {
-    sh.c.cnt[b] = 0;
-    sh.c.mass[b] = 0;
+    sh.c.hi[b] = 0;
+    sh.c.lo[b] = 0;
   }
   stream_slice<DT, AL>(a, c, row, p0, p1, sh, a.dz + (size_t)slot * a.dz_ld,
                        [&](float z, int, bool ok) __attribute__((always_inline)) {
     if (ok && z > -INFINITY) {
       const uint32_t b = dbin(z, M);
-      atomicAdd(&sh.c.cnt[b], 1u);
-      atomicAdd((unsigned long long *)&sh.c.mass[b], (unsigned long long)q40(__builtin_amdgcn_exp2f((z - M) * LOG2E)));
+      const Fx f = fx_of(exp_nonpos((double)z - Md, etab));
+      atomicAdd((unsigned long long *)&sh.c.hi[b], (unsigned long long)f.hi);
+      atomicAdd((unsigned long long *)&sh.c.lo[b], (unsigned long long)(f.lo | (1ull << 48)));
     }
   });
-  uint64_t *gh = a.dhist + (size_t)slot * 2 * DNB;
+  uint64_t *gh = a.dhist + (size_t)slot * 3 * DNB;
   for (int b = tid; b < DNB; b += MT) {
-    const uint32_t n = sh.c.cnt[b];
-    if (n) {
-      atomic_add_ag(&gh[b], (uint64_t)n);
-      atomic_add_ag(&gh[DNB + b], sh.c.mass[b]);
+    const uint64_t lo = sh.c.lo[b];
+    if (lo) {
+      atomic_add_ag(&gh[b], lo >> 48);
+      atomic_add_ag(&gh[DNB + b], sh.c.hi[b]);
+      atomic_add_ag(&gh[2 * DNB + b], lo & ((1ull << 48) - 1ull));
     }
   }
   // Ticket: the row's last slice plans it.
@@ -783,7 +732,6 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
   const int tid = threadIdx.x;
   DeepSlot *ds = a.dslot + slot;
   const float Mf = ds->M;
-  const double M = (double)Mf;
   const int p0 = slice * g.len, p1 = min(a.V, p0 + g.len);
   __syncthreads();  // (LDS of the previous item)
   if (tid == 0) {
@@ -806,30 +754,13 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
   const bool planned = sh.pstat == DS_PLANNED;
   if (planned) {
     const uint32_t w2lo = ld_ag(&ds->w2lo), w2hi = ld_ag(&ds->w2hi), w1lo = ld_ag(&ds->w1lo), w1hi = ld_ag(&ds->w1hi);
-    // per lane, exact fixed-point masses of three regions (before the draw window, between the windows, the rest):
-    // whole multiples of 2^-40 and 2^-64, summed in fp64 (exact below 2^53)
-    double h0 = 0.0, l0 = 0.0, h1 = 0.0, l1 = 0.0, h2 = 0.0, l2 = 0.0;
     auto elem = [&](float z, int t) __attribute__((always_inline)) {
-      bool inw = false;
       if (z > -INFINITY) {
         const uint32_t b = dbin(z, Mf);
-        const double s = exp_nonpos((double)z - M, etab) * 1099511627776.0;  // 2^40
-        const double hi = floor(s), lo = floor((s - hi) * 16777216.0);  // (fx_of)
-        if (b < w2lo) {
-          h0 += hi;
-          l0 += lo;
-        } else if (b > w2hi && b < w1lo) {
-          h1 += hi;
-          l1 += lo;
-        } else {
-          h2 += hi;
-          l2 += lo;
-          inw = b <= w1hi;
+        if ((b >= w2lo && b <= w2hi) || (b >= w1lo && b <= w1hi)) {
+          const uint32_t pos = atomicAdd(&sh.nwl, 1u);
+          if (pos < (uint32_t)WLC) sh.wl[pos] = pack(fkey(z), (uint32_t)t);
         }
-      }
-      if (inw) {
-        const uint32_t pos = atomicAdd(&sh.nwl, 1u);
-        if (pos < (uint32_t)WLC) sh.wl[pos] = pack(fkey(z), (uint32_t)t);
       }
     };
     // the slice's z, as the count phase of this workgroup wrote it: four vectors per thread in flight, loaded
@@ -854,13 +785,7 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
           if (t + k < p1) elem(e[k], t + k);
       }
     }
-    // the slice's sums into the row record (per wave; integer adds, any order), its window elements into the row list
-    const uint64_t hv[6] = {(uint64_t)h0, (uint64_t)l0, (uint64_t)h1, (uint64_t)l1, (uint64_t)h2, (uint64_t)l2};
-#pragma unroll
-    for (int k = 0; k < 6; ++k) {
-      const uint64_t v = wave_sum_u64(hv[k]);
-      if (lane_id() == 0 && v) atomic_add_ag(&ds->acc[DA_X0HI + k], v);
-    }
+    // the slice's window elements into the row list
     __syncthreads();  // (sh.nwl)
     const uint32_t nw = sh.nwl;
     if (tid == 0 && nw) {
@@ -887,8 +812,8 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
   if (planned && ld_ag(&ds->spoil) == 0u)
     finish_row(FinArgs{a.dlist + (size_t)slot * DCAP, a.info, a.tokens, a.mode}, ds, ps.f, etab);
   __syncthreads();  // (every thread has read the row's sums)
-  uint64_t *gh = a.dhist + (size_t)slot * 2 * DNB;
-  for (int b = tid; b < 2 * DNB; b += MT) gh[b] = 0;
+  uint64_t *gh = a.dhist + (size_t)slot * 3 * DNB;
+  for (int b = tid; b < 3 * DNB; b += MT) gh[b] = 0;
   if (tid < DA_N) ds->acc[tid] = 0;
   if (tid == 0) {
     ds->lcnt = 0;
@@ -907,7 +832,7 @@ __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
   if (nd == 0) return;
   if (threadIdx.x < 64) etab[threadIdx.x] = EXP2_64[threadIdx.x];  // (published by the first barrier of an item)
   const DGeom g = deep_geom(a, nd);
-  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) count_item<DT, AL>(a, i / g.S, i % g.S, g, sh.d);
+  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) count_item<DT, AL>(a, i / g.S, i % g.S, g, sh.d, etab);
   for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) pick_item(a, i / g.S, i % g.S, g, sh, etab);
 }
 

@@ -60,7 +60,7 @@ constexpr int DCAP = 8192;     // window elements listed per deep row
 
 enum : uint32_t { DS_PENDING = 0u, DS_PLANNED = 1u, DS_FAIL = 2u };
 
-enum {  // DeepSlot.acc: exact fixed-point sums of the pick pass (hi: 2^-40 units, lo: 2^-64 units) and counts
+enum {  // DeepSlot.acc: exact fixed-point masses of the plan's regions (hi: 2^-40 units, lo: 2^-64 units) and counts
   DA_X0HI, DA_X0LO,  // bins before the draw window
   DA_X1HI, DA_X1LO,  // bins strictly between the two windows
   DA_RHI, DA_RLO,    // the other bins (the windows and after)
@@ -78,7 +78,7 @@ struct DeepSlot {    // 256 bytes, one per deep row of a call
   uint32_t w2lo, w2hi, w1lo, w1hi;  // bin windows holding the draw and the last kept element (inclusive)
   uint32_t lcnt;                    // listed window elements
   uint32_t cdone, pdone;            // slice tickets of the two passes (zero between calls)
-  uint64_t acc[DA_N];               // pick-pass sums (atomic adds; zero between calls)
+  uint64_t acc[DA_N];               // the plan's region sums and counts
   uint32_t spoil;                   // a slice gave up waiting for the plan: the exact path takes the row (zero between calls)
   uint32_t pad32;
   uint64_t pad[7];
@@ -120,7 +120,7 @@ struct ScanArgs {
   // split-row finish
   uint32_t *dctl;    // [0]: deep rows taken by this call (reset by the exact pass)
   DeepSlot *dslot;   // [DEEP_MAX]
-  uint64_t *dhist;   // [DEEP_MAX][2][DNB]: per bin, element count and fixed-point mass (2^-40 units), atomic adds
+  uint64_t *dhist;   // [DEEP_MAX][3][DNB]: per bin, element count and exact mass (2^-40 and 2^-64 parts), atomic adds
   uint64_t *dlist;   // [DEEP_MAX][DCAP]: packed keys of the window elements
   float *dz;         // [DEEP_MAX][dz_ld]: z of the deep rows, written by the count phase, read back by the pick phase
   int64_t dz_ld;
