@@ -14,16 +14,15 @@
 // RN32(x * RN64(1 / T)) (exact, see div_exact), each lane's running maximum, and the softmax sum of the elements the
 // wave does not list, from v_exp_f32 with a rigorous error bound (rescaled in fp64 when a lane's maximum rises). The
 // row history's tokens of the part (penalties: counts from an LDS table indexed by rank) take a side pass with the same
-// arithmetic. The part's listing threshold is the 12th largest of the 256 lane maxima of its waves' first chunks (to 16
-// key bits; the rank scaled down by the share of lanes that saw a z > -inf); a wave whose list passes half its capacity
-// raises its own to the 8th largest of its running lane maxima. Every element at or above the threshold in force when
-// it is processed is listed (exact key, id); thresholds only rise, so a wave's list certifies its top elements down to
-// its final threshold.
+// arithmetic. The part's listing threshold is the kp-th largest of the 256 lane maxima of its waves' first chunks (to
+// 16 key bits; kp aims at KT tokens of the part above it, scaled by the exact counts of allowed tokens in the sample and
+// in the part); a wave whose list passes a quarter of its capacity raises its own to the KV-th largest of its running
+// lane maxima. Every element at or above the threshold in force when it is processed is listed (z bits, id);
+// thresholds only rise, so a wave's list certifies its top elements down to its final threshold.
 //
 // Row resolve: the union of the waves' lists cut at the largest certified key is the row's certified head: exactly its
-// top elements, stable order included. The resolve sorts the top ~256 of the head (the whole head when the keep prefix
-// runs past them), takes exact fp64 masses of it (and of every listed element for S), and decides the keep prefix and
-// the draw. Top-k, min-p and the draw do not depend on S (they compare masses with masses); top-p uses the S bounds.
+// top elements, stable order included. The resolve sorts the whole head, takes exact fp64 masses of it (and of every
+// listed element for S), and decides the keep prefix and the draw. Top-k, min-p and the draw do not depend on S (they compare masses with masses); top-p uses the S bounds.
 // A decision inside the bound, a keep prefix that runs past the head, or an overflowing list marks the row hard: the
 // split-row finish (gse_deep.hip) or, failing that, the exact path (gse_exact.hip) finishes it.
 #include <utility>
