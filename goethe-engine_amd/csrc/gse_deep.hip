@@ -182,29 +182,62 @@ __device__ __forceinline__ DGeom deep_geom(const ScanArgs &a, int nd) {
 constexpr int PBL = DNB / WAVE;  // bins per lane
 static_assert(PBL * WAVE == DNB, "");
 
+// p[j] of lane b / PBL for j = b % PBL (b wave-uniform; zero for b < 0).
+template <typename T>
+__device__ __forceinline__ T bin_at(const T (&p)[PBL], int b) {
+  if (b < 0) return T(0);
+  const int jj = b % PBL;
+  T v = p[0];
+#pragma unroll
+  for (int j = 1; j < PBL; ++j) v = j == jj ? p[j] : v;
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), b / PBL));
+  } else {
+    const uint64_t x = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, b / PBL);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), b / PBL);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  }
+}
+
 __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode) {
   const int l = lane_id();
   const gse_row &P = ds->P;
   const float M = ds->M;
   uint64_t c[PBL], mh[PBL], mo[PBL];
-  double m[PBL];
-  uint64_t cl = 0;
-  double ml = 0.0;
+#pragma unroll
   for (int j = 0; j < PBL; ++j) {
     c[j] = ld_ag(&gh[l * PBL + j]);
     mh[j] = ld_ag(&gh[DNB + l * PBL + j]);
     mo[j] = ld_ag(&gh[2 * DNB + l * PBL + j]);
   }
+  // inclusive prefixes through each bin: counts, exact masses (2^-40 and 2^-64 parts) and their fp64 values
+  uint64_t cl = 0, hl = 0, ol = 0;
+#pragma unroll
   for (int j = 0; j < PBL; ++j) {
-    m[j] = fx_val(Fx{mh[j], mo[j]});
     cl += c[j];
-    ml += m[j];
+    hl += mh[j];
+    ol += mo[j];
   }
-  const double mi = wave_incl_scan_f64(ml);
-  const double S = shfl_f64(mi, WAVE - 1);
-  const uint64_t ci = wave_incl_scan_u64(cl);
-  const uint64_t ctot = shfl_u64(ci, WAVE - 1);
-  // the masses are exact; the margin covers the fp64 roundings of their prefix sums here (the finish decides exactly)
+  const uint64_t ci = wave_incl_scan_u64(cl), hi = wave_incl_scan_u64(hl), oi = wave_incl_scan_u64(ol);
+  const uint64_t ctot = lane63(ci), htot = lane63(hi), otot = lane63(oi);
+  uint64_t pc[PBL], ph[PBL], po[PBL];
+  double pm[PBL];
+  {
+    uint64_t rc = ci - cl, rh = hi - hl, ro = oi - ol;
+#pragma unroll
+    for (int j = 0; j < PBL; ++j) {
+      rc += c[j];
+      rh += mh[j];
+      ro += mo[j];
+      pc[j] = rc;
+      ph[j] = rh;
+      po[j] = ro;
+      pm[j] = fx_val(Fx{rh, ro});
+    }
+  }
+  const double S = fx_val(Fx{htot, otot});
+  // the masses are exact; the margin covers the fp64 roundings of their values here (the finish decides exactly)
   const double delta = 1e-12 * S;
   const uint64_t K = P.top_k > 0 ? (uint64_t)P.top_k : ~0ull;
   const double tS = P.top_p * S;
@@ -221,18 +254,19 @@ __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode
   //   b5 - 1: last non-empty bin below bm - 1 (min-p: holds a kept element, so the last kept one is at or after it)
   //   b6:     first non-empty bin above bm + 1 (min-p: holds a cut element)
   uint32_t b0 = DNB - 1, b1 = DNB - 1, b2 = DNB - 1, b5 = 0, b6 = DNB - 1;
-  {
-    double pin = mi - ml;
-    uint64_t cin = ci - cl;
+#pragma unroll
+  for (int j = PBL - 1; j >= 0; --j) {
+    const uint32_t b = l * PBL + j;
+    if (pm[j] >= tS - delta) b0 = b;
+    if (pm[j] >= tS + delta) b1 = b;
+    if (pc[j] >= K) b2 = b;
+    if (mp && c[j] && b > bm + 1) b6 = b;
+  }
+  if (mp) {
+#pragma unroll
     for (int j = 0; j < PBL; ++j) {
       const uint32_t b = l * PBL + j;
-      pin += m[j];
-      cin += c[j];
-      if (pin >= tS - delta) b0 = min(b0, b);
-      if (pin >= tS + delta) b1 = min(b1, b);
-      if (cin >= K) b2 = min(b2, b);
-      if (mp && c[j] && b + 1 < bm) b5 = max(b5, b + 1);
-      if (mp && c[j] && b > bm + 1) b6 = min(b6, b);
+      if (c[j] && b + 1 < bm) b5 = b + 1;
     }
   }
   b0 = wave_min_u32(b0);
@@ -251,30 +285,17 @@ __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode
     // when min-p may bind, the window reaches its first cut element (the finish cannot test min-p unlisted)
     w1hi = lo <= w1hi ? max(w1hi, min(hi, (uint32_t)(DNB - 1))) : min(w1hi, hi);
   }
-  // masses before w1lo and through w1hi (approximate), then the windows of the draw
-  double qd0 = 0.0, qd1 = 0.0;
-  {
-    double pin = mi - ml;
-    for (int j = 0; j < PBL; ++j) {
-      const uint32_t b = l * PBL + j;
-      if (b == w1lo) qd0 = pin;
-      pin += m[j];
-      if (b == w1hi) qd1 = pin;
-    }
-  }
-  qd0 = wave_sum_f64(qd0);  // (one lane holds each)
-  qd1 = wave_sum_f64(qd1);
+  // masses before w1lo and through w1hi, then the windows of the draw
   uint32_t w2lo = w1lo, w2hi = w1hi;
   if (mode == MODE_SAMPLE) {
+    const double qd0 = bin_at(pm, (int)w1lo - 1), qd1 = bin_at(pm, (int)w1hi);
     const double u = ds->u;
     const double tlo = u * (qd0 - delta) - delta, thi = u * (qd1 + delta) + delta;
     uint32_t b3 = DNB - 1, b4 = DNB - 1;
-    double pin = mi - ml;
-    for (int j = 0; j < PBL; ++j) {
-      const uint32_t b = l * PBL + j;
-      pin += m[j];
-      if (pin >= tlo) b3 = min(b3, b);
-      if (pin >= thi) b4 = min(b4, b);
+#pragma unroll
+    for (int j = PBL - 1; j >= 0; --j) {
+      if (pm[j] >= tlo) b3 = l * PBL + j;
+      if (pm[j] >= thi) b4 = l * PBL + j;
     }
     b3 = wave_min_u32(b3);
     b4 = wave_min_u32(b4);
@@ -287,23 +308,17 @@ __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode
     w1lo = w2lo;
     w1hi = w2hi;
   }
-  uint64_t inw = 0, n0 = 0, n1 = 0, n2 = 0;
-  uint64_t xm[6] = {0, 0, 0, 0, 0, 0};  // exact masses (2^-40, 2^-64 parts): before the draw window, between, the rest
-  for (int j = 0; j < PBL; ++j) {
-    const uint32_t b = l * PBL + j;
-    if ((b >= w2lo && b <= w2hi) || (b >= w1lo && b <= w1hi)) inw += c[j];
-    else if (b < w2lo) n0 += c[j];
-    else if (b < w1lo) n1 += c[j];
-    else n2 += c[j];
-    const int r = b < w2lo ? 0 : (b > w2hi && b < w1lo) ? 1 : 2;
-    xm[2 * r] += mh[j];
-    xm[2 * r + 1] += mo[j];
-  }
-  inw = wave_sum_u64(inw);
-  n0 = wave_sum_u64(n0);
-  n1 = wave_sum_u64(n1);
-  n2 = wave_sum_u64(n2);
-  for (int k = 0; k < 6; ++k) xm[k] = wave_sum_u64(xm[k]);
+  // the regions outside the windows from the prefixes at their edges: before the draw window (0), between the
+  // windows (1), after the cut window (counts), and the rest of the mass (2)
+  const bool sep = w1lo > w2hi + 1;
+  const uint64_t n0 = bin_at(pc, (int)w2lo - 1);
+  const uint64_t n1 = sep ? bin_at(pc, (int)w1lo - 1) - bin_at(pc, (int)w2hi) : 0ull;
+  const uint64_t n2 = ctot - bin_at(pc, (int)w1hi);
+  const uint64_t inw = ctot - n0 - n1 - n2;
+  const uint64_t x0h = bin_at(ph, (int)w2lo - 1), x0o = bin_at(po, (int)w2lo - 1);
+  const uint64_t x1h = sep ? bin_at(ph, (int)w1lo - 1) - bin_at(ph, (int)w2hi) : 0ull;
+  const uint64_t x1o = sep ? bin_at(po, (int)w1lo - 1) - bin_at(po, (int)w2hi) : 0ull;
+  const uint64_t xm[6] = {x0h, x0o, x1h, x1o, htot - x0h - x1h, otot - x0o - x1o};
   const uint32_t status = (inw > 0 && inw <= (uint64_t)DCAP && S > 0.0 && fabsf(M) < INFINITY) ? DS_PLANNED : DS_FAIL;
   if (l == 0) {  // the plan, then (once it is stored) its status, which the row's pick slices wait for
     st_ag(&ds->w2lo, w2lo);
@@ -484,6 +499,7 @@ __device__ __noinline__ void finish_row(const FinArgs a, DeepSlot *ds, FinShared
   const bool ok0 = nraw > 0 && nraw <= (uint32_t)DCAP && Sd > 0.0;
   const int n = ok0 ? (int)nraw : 0;
   const uint64_t *lst = a.lst;
+  const uint64_t cmax = a.info[row].cmax;  // (written by the main pass; loaded now, used at the end)
   // the list's first LC entries into LDS, every load issued before the first is used (entries past n are stale and
   // never read)
   {
@@ -706,7 +722,7 @@ __device__ __noinline__ void finish_row(const FinArgs a, DeepSlot *ds, FinShared
   if (tid == 0 && ok) {
     RowInfo *ri = a.info + row;
     RowInfo r = {};
-    r.cmax = ri->cmax;
+    r.cmax = cmax;
     r.kkeep = kkeep;
     r.S = Sd;
     r.Z = clast;
