@@ -18,6 +18,7 @@ F32, BF16 = 0, 1
 ROW_TEMP_UNDERFLOW = 1
 BATCH_EXACT = 1
 BATCH_PROFILE = 2
+BATCH_NO_PLAN_WAIT = 4
 MAX_LOGPROBS = 64
 P_ = C.POINTER
 

@@ -738,10 +738,6 @@ union PickShared {
   FinShared f;
 };
 
-// Wall-clock ticks (100 MHz) a pick slice waits for its row's plan. Every slice of the grid is resident at once, and
-// a plan takes microseconds; the limit only ends the wait when the device could not hold the whole grid.
-constexpr uint64_t PLAN_WAIT = 400000;  // 4 ms
-
 __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice, const DGeom &g, PickShared &ps,
                                           const double *etab) {
   DeepShared &sh = ps.d;
@@ -756,7 +752,9 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
     if (st == DS_PENDING) {
       const uint64_t t0 = wall_clock64();
       while ((st = ld_ag(&ds->status)) == DS_PENDING) {
-        if (wall_clock64() - t0 > PLAN_WAIT) {
+        // (every slice of the grid is resident at once and a plan takes microseconds: the limit, a.plan_wait, only
+        // ends the wait when the device could not hold the whole grid)
+        if (wall_clock64() - t0 >= a.plan_wait) {
           (void)__hip_atomic_fetch_or(&ds->spoil, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           st = DS_FAIL;
           break;

@@ -125,6 +125,7 @@ struct ScanArgs {
   float *dz;         // [DEEP_MAX][dz_ld]: z of the deep rows, written by the count phase, read back by the pick phase
   int64_t dz_ld;
   int dslices, dgrid;  // split-row finish enabled (slices per deep row, at most), workgroups per pass
+  uint64_t plan_wait;  // wall-clock ticks (100 MHz) a split-row pick slice waits for its row's plan
 };
 
 hipError_t launch_main(const ScanArgs &a, hipStream_t s);

@@ -246,8 +246,10 @@ def _prepare(logits, params, seeds, idxs, masks, history, uniforms):
     return h, x, code, dev, _batch(x, code, rows_dev, mask_dev, mask_ld, hist_dev, uni_dev, dev), keep
 
 
-def sample_ex(logits, params, seeds, idxs, masks, history=None, uniforms=None, exact=False, processed=False):
-    """gse_sample on the current stream, asynchronously: a Selection of device tensors."""
+def sample_ex(logits, params, seeds, idxs, masks, history=None, uniforms=None, exact=False, processed=False,
+              flags=0):
+    """gse_sample on the current stream, asynchronously: a Selection of device tensors. flags adds GSE_BATCH_* bits
+    (testing: BATCH_NO_PLAN_WAIT)."""
     x, _ = _logits(logits)
     n, v = x.shape
     dev = x.device if n else None
@@ -256,6 +258,7 @@ def sample_ex(logits, params, seeds, idxs, masks, history=None, uniforms=None, e
     h, x, code, dev, b, keep = _prepare(x, params, seeds, idxs, masks, history, uniforms)
     if exact:
         b.flags |= _lib.BATCH_EXACT
+    b.flags |= int(flags)
     nlp = max([int(_get(p, "logprobs", 0)) for p in params] + [0])
     toks = torch.empty(n, dtype=torch.int32, device=dev)
     o = _lib.Out()

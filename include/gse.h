@@ -98,8 +98,10 @@ typedef struct gse_batch {
 
 /* gse_batch.flags */
 enum {
-  GSE_BATCH_EXACT = 1u,  /* finish every sampled row on the exact radix-select path (same results, slower) */
-  GSE_BATCH_PROFILE = 2u /* record HIP events around each kernel of this call on its stream (read with gse_profile) */
+  GSE_BATCH_EXACT = 1u,   /* finish every sampled row on the exact radix-select path (same results, slower) */
+  GSE_BATCH_PROFILE = 2u, /* record HIP events around each kernel of this call on its stream (read with gse_profile) */
+  GSE_BATCH_NO_PLAN_WAIT = 4u /* testing: a split-row finish slice whose row's plan is not out when it first looks
+                               * does not wait; the row takes the exact path (same results, slower) */
 };
 
 typedef struct gse_out {

@@ -209,3 +209,20 @@ def test_deep_rows_sample_and_dist(ge, gpu):
     d = ge.sampling.dist_batch(xt, params).cpu().numpy()
     for r in range(0, n, 5):
         np.testing.assert_allclose(d[r], ora.dist(x[r], params[r]), rtol=DIST_RTOL, atol=1e-300)
+
+
+@pytest.mark.gpu
+def test_deep_rows_plan_wait_off(ge, gpu):
+    """The split-row finish's bounded wait: with GSE_BATCH_NO_PLAN_WAIT a pick slice that finds its row's plan not yet
+    out gives the row up (the forced form of a wait that ran out), and the exact path finishes it: same tokens."""
+    n, v = 24, 151936
+    x, params = _flat_rows(ge, n, v, 7)
+    u = np.array([ora.uniform(1000 + r, 3) for r in range(n)], np.float64)
+    xt = torch.from_numpy(x).to(gpu)
+    got = ge.sampling.sample_ex(xt, params, None, None, None, uniforms=u,
+                                flags=ge._lib.BATCH_NO_PLAN_WAIT).tolist()
+    paths = ge._lib.handle(gpu.index, n, v).row_paths(n)
+    assert got == ora.sample(x, params, None, None, None, uniforms=u)
+    assert (paths == ge._lib.PATH_EXACT).sum() >= 1, paths
+    again = ge.sampling.sample_ex(xt, params, None, None, None, uniforms=u).tolist()  # the slots were cleared
+    assert again == got
