@@ -549,32 +549,44 @@ __device__ __forceinline__ float keep_or_ninf(float x, uint32_t keep, int k) {
   return __uint_as_float((__float_as_uint(x) & sel) | (0xFF800000u & ~sel));
 }
 
-// One chunk's logits and mask words, with the same loads for every chunk: a vector that does not lie below pv loads
-// the row's first vector instead (aligned rows); unaligned rows load element by element, clamped to the part.
+// Buffer resources of the row's logits and mask words: 32-bit offsets from a scalar base (no per-lane 64-bit address
+// arithmetic), and a load at or past the end of the row returns zeros instead of reading past it.
+struct RowBufs {
+  __amdgpu_buffer_rsrc_t x, m;
+};
+__device__ __forceinline__ RowBufs row_bufs(const RowCtx &c) {
+  constexpr int FMT = 0x00020000;  // raw 32-bit buffer (GFX9 resource word 3)
+  RowBufs r;
+  r.x = __builtin_amdgcn_make_buffer_rsrc((void *)c.base, (short)0, c.V * (c.dtype == GSE_BF16 ? 2 : 4), FMT);
+  r.m = __builtin_amdgcn_make_buffer_rsrc((void *)c.mw, (short)0, c.mw ? (c.V + 31) / 32 * 4 : 0, FMT);
+  return r;
+}
+
+// One chunk's logits and mask words, the same loads for every chunk. Aligned rows: one 16-byte buffer load per vector
+// (a vector past the stream end pv loads the row's next tokens, or zeros past the row, and is ignored: its tokens are
+// not in the chunk's in-range bits); unaligned rows load element by element, clamped to the part.
 template <int DT, bool AL, bool MASKED>
-__device__ __forceinline__ void load_u(const RowCtx &c, int cb, int pv, int p1, float (&x)[EPL],
+__device__ __forceinline__ void load_u(const RowCtx &c, const RowBufs &rb, int cb, int pv, int p1, float (&x)[EPL],
                                        uint32_t (&mw)[Lay<DT>::NV]) {
   using L = Lay<DT>;
   const int l = lane_id();
 #pragma unroll
   for (int v = 0; v < L::NV; ++v) {
     const int t0 = cb + v * L::STRIDE + l * L::VEC;
-    if constexpr (MASKED) mw[v] = c.mw[min(t0, p1 - 1) >> 5];
+    if constexpr (MASKED) {
+      if constexpr (AL) mw[v] = __builtin_amdgcn_raw_buffer_load_b32(rb.m, (t0 >> 5) * 4, 0, 0);
+      else mw[v] = c.mw[min(t0, p1 - 1) >> 5];
+    }
     if constexpr (AL) {
-      const int ts = t0 + L::VEC <= pv ? t0 : 0;
+      const auto u = __builtin_amdgcn_raw_buffer_load_b128(rb.x, t0 * (DT == GSE_F32 ? 4 : 2), 0, 0);
       if constexpr (DT == GSE_F32) {
-        const float4 f = *reinterpret_cast<const float4 *>((const float *)c.base + ts);
-        x[4 * v] = f.x;
-        x[4 * v + 1] = f.y;
-        x[4 * v + 2] = f.z;
-        x[4 * v + 3] = f.w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[4 * v + i] = __uint_as_float(u[i]);
       } else {
-        const uint4 u = *reinterpret_cast<const uint4 *>((const uint16_t *)c.base + ts);
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          x[8 * v + 2 * i] = __uint_as_float(w[i] << 16);
-          x[8 * v + 2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+          x[8 * v + 2 * i] = __uint_as_float(u[i] << 16);
+          x[8 * v + 2 * i + 1] = __uint_as_float(u[i] & 0xFFFF0000u);
         }
       }
     } else {
@@ -582,6 +594,7 @@ __device__ __forceinline__ void load_u(const RowCtx &c, int cb, int pv, int p1, 
       for (int k = 0; k < L::VEC; ++k) x[v * L::VEC + k] = load_one(c, min(t0 + k, p1 - 1));
     }
   }
+  (void)pv;
 }
 
 // z of one chunk in place: the mask and the history exclusion (one select; -inf for tokens the stream does not carry),
@@ -785,11 +798,12 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
       hid[k] = j < c.he ? a.hist[j] : -1;
     }
   }
+  const RowBufs rbuf = row_bufs(c);
   float xa[EPL], xb[EPL], xc[EPL];
   uint32_t ma[L::NV], mb[L::NV], mcw[L::NV];
   int c0 = w, c1 = w + NWV;  // chunks 0..7 go to waves 0..3 two by two; later ones from the LDS counter
-  load_u<DT, AL, MASKED>(c, p0 + c0 * CHK, pv, p1, xa, ma);
-  load_u<DT, AL, MASKED>(c, p0 + c1 * CHK, pv, p1, xb, mb);
+  load_u<DT, AL, MASKED>(c, rbuf, p0 + c0 * CHK, pv, p1, xa, ma);
+  load_u<DT, AL, MASKED>(c, rbuf, p0 + c1 * CHK, pv, p1, xb, mb);
   // allowed tokens of the part's stream range (masked rows: popcounts of its mask words, every load issued before the
   // first is used; the sum comes after the history build)
   constexpr int APW = (PTOK / 32 + MT - 1) / MT;  // mask words per thread
@@ -881,7 +895,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     rn.kap = max(r << 16, KEY_NEGINF + 1u);
   }
   int c2 = grab();
-  load_u<DT, AL, MASKED>(c, p0 + c2 * CHK, pv, p1, xc, mcw);
+  load_u<DT, AL, MASKED>(c, rbuf, p0 + c2 * CHK, pv, p1, xc, mcw);
   if (c0 < nck) {
     if (listing) chunk_sum<EPL>(a, row, wl, cmax, xa, rn, tok_of(p0 + c0 * CHK));
     else rn.m = fmaxf(rn.m, cmax);
@@ -895,15 +909,15 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   };
   while (true) {
     c0 = grab();
-    load_u<DT, AL, MASKED>(c, p0 + c0 * CHK, pv, p1, xa, ma);
+    load_u<DT, AL, MASKED>(c, rbuf, p0 + c0 * CHK, pv, p1, xa, ma);
     if (c1 >= nck) break;
     step(c1, xb, mb);
     c1 = grab();
-    load_u<DT, AL, MASKED>(c, p0 + c1 * CHK, pv, p1, xb, mb);
+    load_u<DT, AL, MASKED>(c, rbuf, p0 + c1 * CHK, pv, p1, xb, mb);
     if (c2 >= nck) break;
     step(c2, xc, mcw);
     c2 = grab();
-    load_u<DT, AL, MASKED>(c, p0 + c2 * CHK, pv, p1, xc, mcw);
+    load_u<DT, AL, MASKED>(c, rbuf, p0 + c2 * CHK, pv, p1, xc, mcw);
     if (c0 >= nck) break;
     step(c0, xa, ma);
   }
