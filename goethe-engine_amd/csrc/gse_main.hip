@@ -108,7 +108,8 @@ struct RowEval {
   const ScanArgs *a;
   int row, nlp, n;
   bool greedy, complete;
-  double M, S, B;
+  double M;
+  double S, B;    // the masses outside the head (unlisted, and listed below the certified key) and their error bound
   uint64_t gtop;  // greedy rows: packed argmax
   const gse_row *P;
 };
@@ -208,7 +209,7 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
   // [512 w, 512 w + 512), 64 consecutive ranks per step: conflict-free LDS accesses and wave scans (the additions are
   // the same, in the same order, every time). A_r = I_{r-1} is the exclusive prefix.
   double *ee = reinterpret_cast<double *>(sh.r.tmp);
-  const double M = ev.M, Sm = ev.S;
+  const double M = ev.M;
   const int lane = lane_id(), w = tid >> 6;
 #pragma unroll 1
   for (int i = tid; i < n; i += MT) ee[i] = exp_nonpos((double)fkey_inv(pk_key(arr[i])) - M, sh.etab);
@@ -225,8 +226,12 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
   }
   if (lane == 0) sh.wred[w] = carry;
   __syncthreads();
-  double base = 0.0;
-  for (int q = 0; q < w; ++q) base += sh.wred[q];
+  double base = 0.0, htot = 0.0;
+  for (int q = 0; q < NWV; ++q) {
+    if (q < w) base += sh.wred[q];
+    htot += sh.wred[q];
+  }
+  const double Sm = ev.S + htot;  // S: the unlisted and listed masses outside the head, then the head's
   if (w > 0) {
 #pragma unroll 1
     for (int s = 0; s < RPW / WAVE; ++s) {
@@ -255,7 +260,8 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
   // quotients as the definition does, where e lies within 1e-12 of min_p (elsewhere e >= min_p decides it).
   const int64_t K = P.top_k > 0 ? (int64_t)P.top_k : (int64_t)0x7FFFFFFFFFFFll;
   const double topp = P.top_p, minp = P.min_p;
-  const double q0 = 1.0 / Sm, tlo = topp * (Sm - ev.B), thi = topp * (Sm + ev.B);
+  const double B = ev.B + 2e-15 * Sm;
+  const double q0 = 1.0 / Sm, tlo = topp * (Sm - B), thi = topp * (Sm + B);
   uint32_t fsure = 0xFFFFFFFFu, fmaybe = 0xFFFFFFFFu;
 #pragma unroll 1
   for (int s = 0; s < RPW / WAVE; ++s) {
@@ -437,7 +443,8 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
       const uint64_t v = sh.r.tmp[g * MT + tid];
       const uint32_t k = pk_key(v);
       bestL = v > bestL ? v : bestL;
-      if (v && finite_max && k > KEY_NEGINF) scand += exp_nonpos((double)fkey_inv(k) - M, sh.etab);
+      // (the head's masses are summed by the evaluation, which takes them anyway)
+      if (v && finite_max && k > KEY_NEGINF && k < kappa) scand += exp_nonpos((double)fkey_inv(k) - M, sh.etab);
       // head appends: one LDS atomic per wave
       const bool h = v && k >= kappa;
       const uint64_t bl = ballot64(h);
@@ -478,8 +485,8 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   ev.greedy = greedy;
   ev.complete = complete;
   ev.M = M;
-  ev.S = srest + scand;
-  ev.B = brest + 2e-15 * ev.S;
+  ev.S = srest + scand;  // without the head's masses: the evaluation adds them
+  ev.B = brest;
   ev.gtop = gtop;
   ev.P = &P;
   const uint32_t nh_all = sh.nh;
