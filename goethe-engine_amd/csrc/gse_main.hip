@@ -530,10 +530,11 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
 // The stream carries every token of the part below pv (the part end, rounded down to a whole vector for aligned rows)
 // except the tokens of the row's history: those (at most a few hundred per part) and the ragged tokens [pv, p1) are
 // penalized and masked by a side pass with exactly the same arithmetic, and enter the same running state out of order.
-// Every chunk issues the same loads (a vector past pv loads the row's first vector and is ignored), so the compiler
-// can count the loads in flight: each wave keeps two chunks loading while it works on a third. The stream needs no
-// per-element branch: the mask and the history exclusion are one bit select per element, the listing is skipped for a
-// whole chunk when the lane maxima lie below the threshold, and the unlisted terms are summed in fp32 per chunk.
+// Every chunk issues the same loads (a vector past pv loads the row's next tokens, or zeros past the row's end, and is
+// ignored), so the compiler can count the loads in flight: each wave keeps two chunks loading while it works on a
+// third. The stream needs no per-element branch: the mask and the history exclusion are one bit select per element,
+// the listing is skipped for a whole chunk when the lane maxima lie below the threshold, and the unlisted terms are
+// summed in fp32 per chunk.
 
 // Per-lane running state of a wave.
 struct Run {
