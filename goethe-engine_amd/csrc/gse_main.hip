@@ -543,6 +543,7 @@ struct Run {
   double b;        // its error bound
   uint32_t kap;    // the wave's listing threshold key (uniform in the wave; only rises)
   uint32_t woff;   // elements the wave has listed (uniform)
+  uint32_t vnext;  // list length at which the valve next recomputes the threshold (uniform)
   float g;         // greedy rows: largest nan_to_num(x) so far, at the lowest token gid holding it
   uint32_t gid;
   uint32_t fid;    // lowest token of this lane with z not NaN (found in the lane's first chunk)
@@ -692,7 +693,10 @@ __device__ __forceinline__ void chunk_sum(const ScanArgs &a, int row, int wl, fl
                                           Run &rn, Tok tok) {
   static_assert((N & (N - 1)) == 0 && N <= 256, "");
   const float mnew = fmaxf(rn.m, cmax);
-  if (rn.woff > (uint32_t)(CAPW / 4)) rn.kap = max(rn.kap, wave_kth_largest_u16(fkey(mnew) >> 16, KV) << 16);
+  if (rn.woff >= rn.vnext) {  // (again after every KV / 2 more listed elements)
+    rn.kap = max(rn.kap, wave_kth_largest_u16(fkey(mnew) >> 16, KV) << 16);
+    rn.vnext = rn.woff + KV / 2;
+  }
   const float tauf = fkey_inv(rn.kap);
   if (mnew > rn.m && rn.m > -INFINITY) {  // rescale the lane's sum to its new maximum (fp64)
     const double f = exp((double)rn.m - (double)mnew);
@@ -849,6 +853,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   rn.b = 0.0;
   rn.kap = 0;
   rn.woff = 0;
+  rn.vnext = CAPW / 4 + 1;
   rn.g = -INFINITY;
   rn.gid = 0xFFFFFFFFu;
   rn.fid = 0xFFFFFFFFu;
