@@ -1,7 +1,7 @@
 // The fused selection pass. One 256-thread workgroup per (row, part), a part being a contiguous run of at most 40960
 // tokens of the row. Its four waves stream the part in 512-token chunks (64 lanes x 8 tokens), each wave on its own:
-// chunks are taken from an LDS counter, the next chunk's loads are in flight while the current one is processed, and
-// no barrier separates two chunks. One HBM read of the logits, the packed mask words and the row's history ids; the
+// wave w takes chunks w, w + 4, w + 8, ..., the next chunks' loads are in flight while the current one is processed,
+// and no barrier separates two chunks. One HBM read of the logits, the packed mask words and the row's history ids; the
 // last workgroup of each row to finish (atomic ticket, nothing waits) resolves the row.
 //
 // Reference semantics (goethe_engine/sampling.py:59-85):
@@ -813,7 +813,8 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   const RowBufs rbuf = row_bufs(c);
   float xa[EPL], xb[EPL], xc[EPL];
   uint32_t ma[L::NV], mb[L::NV], mcw[L::NV];
-  int c0 = w, c1 = w + NWV;  // chunks 0..7 go to waves 0..3 two by two; later ones from the LDS counter
+  const int wu = __builtin_amdgcn_readfirstlane(w);  // (the wave index as a scalar: the chunk loop stays uniform)
+  int c0 = wu, c1 = wu + NWV;  // wave w takes chunks w, w + 4, w + 8, ...
   load_u<DT, AL, MASKED>(c, rbuf, p0 + c0 * CHK, pv, p1, xa, ma);
   load_u<DT, AL, MASKED>(c, rbuf, p0 + c1 * CHK, pv, p1, xb, mb);
   // allowed tokens of the part's stream range (masked rows: popcounts of its mask words, every load issued before the
@@ -825,10 +826,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
 #pragma unroll
     for (int k = 0; k < APW; ++k) mwd[k] = c.mw[(p0 >> 5) + max(min(tid + k * MT, nmw - 1), 0)];
   }
-  if (tid == 0) {
-    sh.next = 2 * NWV;
-    sh.hover = 0;
-  }
+  if (tid == 0) sh.hover = 0;
   if (c.pen) build_history(c, a.hist, hid, p0, p1, sh.h, sh.wcnt, sh.hover);
   else __syncthreads();
   uint32_t apc = 0;
@@ -858,10 +856,12 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   rn.gid = 0xFFFFFFFFu;
   rn.fid = 0xFFFFFFFFu;
   rn.nanm = 0;
+  // the next chunks (scalar arithmetic: no LDS round trip and no vector temporary between a chunk's loads and its use)
+  int nxt = wu + 2 * NWV;
   auto grab = [&]() -> int {
-    uint32_t n = 0;
-    if (lane == 0) n = atomicAdd(&sh.next, 1u);
-    return __builtin_amdgcn_readfirstlane((int)n);
+    const int n = nxt;
+    nxt += NWV;
+    return n;
   };
   auto tok_of = [&](int cb) {
     return [=](int i) { return (uint32_t)(cb + (i / L::VEC) * L::STRIDE + lane * L::VEC + (i % L::VEC)); };
