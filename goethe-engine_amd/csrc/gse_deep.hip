@@ -42,7 +42,7 @@ struct DeepShared {
     } c;
     uint64_t wl[WLC];           // pick pass: the slice's window elements
   };
-  uint32_t next, hover, ticket, nwl, wbase, pstat;
+  uint32_t hover, ticket, nwl, wbase, pstat;
   uint32_t wsum[NWV];
   uint64_t wred[NWV], wred2[NWV];
   double dred[NWV];
@@ -83,12 +83,10 @@ __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c,
   }
   float xa[EPL], xb[EPL];
   uint32_t ma[L::NV], mb[L::NV];
-  int ck = w;
+  const int wu = __builtin_amdgcn_readfirstlane(w);  // (the wave index as a scalar: the chunk loop stays uniform)
+  int ck = wu;
   if (nfull > 0) load_full<DT, AL>(c, p0 + ck * CHK, ck < nfull, xa, ma);
-  if (tid == 0) {
-    sh.next = NWV;
-    sh.hover = 0;
-  }
+  if (tid == 0) sh.hover = 0;
   if (c.pen) build_history(c, a.hist, hid, p0, p1, sh.h, sh.wsum, sh.hover);
   else __syncthreads();
   Lane ln;
@@ -102,10 +100,11 @@ __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c,
   ln.fid = 0xFFFFFFFFu;
   ln.fnan = false;
   ln.ffin = false;
+  int nxt = wu + NWV;  // wave w takes chunks w, w + 4, w + 8, ... (scalar arithmetic)
   auto grab = [&]() -> int {
-    uint32_t n = 0;
-    if (lane == 0) n = atomicAdd(&sh.next, 1u);
-    return __builtin_amdgcn_readfirstlane((int)n);
+    const int n = nxt;
+    nxt += NWV;
+    return n;
   };
   auto body = [&](int k, float(&x)[EPL], uint32_t(&mw)[L::NV]) __attribute__((always_inline)) {
     const int cb = p0 + k * CHK;

@@ -56,7 +56,6 @@ struct Shared {
       uint32_t bofs[NBK];      // bucket starts
     } r;
   };
-  uint32_t next;               // next chunk of the part
   uint32_t hover;              // more distinct history ids than HMAX
   uint32_t ticket;
   float wmax[NWV];
