@@ -814,8 +814,12 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   uint32_t ma[L::NV], mb[L::NV], mcw[L::NV];
   const int wu = __builtin_amdgcn_readfirstlane(w);  // (the wave index as a scalar: the chunk loop stays uniform)
   int c0 = wu, c1 = wu + NWV;  // wave w takes chunks w, w + 4, w + 8, ...
-  load_u<DT, AL, MASKED>(c, rbuf, p0 + c0 * CHK, pv, p1, xa, ma);
-  load_u<DT, AL, MASKED>(c, rbuf, p0 + c1 * CHK, pv, p1, xb, mb);
+  // First token of chunk ck for its loads. A chunk past the stream gets a start far past the row (vocabularies are at
+  // most 2^21 tokens): its buffer loads fail the range check and return zeros without a memory access (unaligned rows
+  // clamp to the part instead), so the loads a wave issues ahead of its last chunk fetch nothing.
+  const auto cst = [&](int ck) -> int { return ck < nck ? p0 + ck * CHK : (1 << 28); };
+  load_u<DT, AL, MASKED>(c, rbuf, cst(c0), pv, p1, xa, ma);
+  load_u<DT, AL, MASKED>(c, rbuf, cst(c1), pv, p1, xb, mb);
   // allowed tokens of the part's stream range (masked rows: popcounts of its mask words, every load issued before the
   // first is used; the sum comes after the history build)
   constexpr int APW = (PTOK / 32 + MT - 1) / MT;  // mask words per thread
@@ -907,7 +911,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     rn.kap = max(r << 16, KEY_NEGINF + 1u);
   }
   int c2 = grab();
-  load_u<DT, AL, MASKED>(c, rbuf, p0 + c2 * CHK, pv, p1, xc, mcw);
+  load_u<DT, AL, MASKED>(c, rbuf, cst(c2), pv, p1, xc, mcw);
   if (c0 < nck) {
     if (listing) chunk_sum<EPL>(a, row, wl, cmax, xa, rn, tok_of(p0 + c0 * CHK));
     else rn.m = fmaxf(rn.m, cmax);
@@ -921,15 +925,15 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   };
   while (true) {
     c0 = grab();
-    load_u<DT, AL, MASKED>(c, rbuf, p0 + c0 * CHK, pv, p1, xa, ma);
+    load_u<DT, AL, MASKED>(c, rbuf, cst(c0), pv, p1, xa, ma);
     if (c1 >= nck) break;
     step(c1, xb, mb);
     c1 = grab();
-    load_u<DT, AL, MASKED>(c, rbuf, p0 + c1 * CHK, pv, p1, xb, mb);
+    load_u<DT, AL, MASKED>(c, rbuf, cst(c1), pv, p1, xb, mb);
     if (c2 >= nck) break;
     step(c2, xc, mcw);
     c2 = grab();
-    load_u<DT, AL, MASKED>(c, rbuf, p0 + c2 * CHK, pv, p1, xc, mcw);
+    load_u<DT, AL, MASKED>(c, rbuf, cst(c2), pv, p1, xc, mcw);
     if (c0 >= nck) break;
     step(c0, xa, ma);
   }
