@@ -181,22 +181,29 @@ __device__ __forceinline__ DGeom deep_geom(const ScanArgs &a, int nd) {
 constexpr int PBL = DNB / WAVE;  // bins per lane
 static_assert(PBL * WAVE == DNB, "");
 
-// p[j] of lane b / PBL for j = b % PBL (b wave-uniform; zero for b < 0).
+// p[j] of lane b / PBL for j = b % PBL (b wave-uniform; zero for b < 0). Every p[j] is read off that lane first and
+// the pick is a chain of scalar selects: a select over the registers by a run-time index becomes a private array in
+// scratch memory, with a memory round trip per lookup.
 template <typename T>
 __device__ __forceinline__ T bin_at(const T (&p)[PBL], int b) {
   if (b < 0) return T(0);
-  const int jj = b % PBL;
-  T v = p[0];
+  const int jj = b % PBL, ln = b / PBL;
+  uint64_t v = 0;
 #pragma unroll
-  for (int j = 1; j < PBL; ++j) v = j == jj ? p[j] : v;
-  if constexpr (sizeof(T) == 4) {
-    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), b / PBL));
-  } else {
-    const uint64_t x = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, b / PBL);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), b / PBL);
-    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  for (int j = 0; j < PBL; ++j) {
+    uint64_t x;
+    if constexpr (sizeof(T) == 4) {
+      x = (uint32_t)__builtin_amdgcn_readlane(__builtin_bit_cast(int, p[j]), ln);
+    } else {
+      const uint64_t y = __builtin_bit_cast(uint64_t, p[j]);
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)y, ln);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(y >> 32), ln);
+      x = ((uint64_t)hi << 32) | lo;
+    }
+    v = j == jj ? x : v;
   }
+  if constexpr (sizeof(T) == 4) return __builtin_bit_cast(T, (uint32_t)v);
+  else return __builtin_bit_cast(T, v);
 }
 
 __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode) {
