@@ -284,12 +284,14 @@ __device__ __forceinline__ double exp_nonpos(double d, const double *tab) {
 struct Fx {  // value = hi * 2^-40 + lo * 2^-64
   uint64_t hi, lo;
 };
+// The conversions are exact and short: h = floor(s) < 2^52 is an integer, so h + 2^52 holds h in its 52 fraction
+// bits; the remainder scaled by 2^24 is below 2^24, and the truncating conversion to u32 is its floor (it is >= 0).
 __device__ __forceinline__ Fx fx_of(double e) {
   const double s = e * 1099511627776.0;  // 2^40
   const double h = floor(s);
   Fx f;
-  f.hi = (uint64_t)h;
-  f.lo = (uint64_t)floor((s - h) * 16777216.0);  // 2^24
+  f.hi = (uint64_t)__double_as_longlong(h + 4503599627370496.0) & 0x000FFFFFFFFFFFFFull;  // 2^52
+  f.lo = (uint32_t)((s - h) * 16777216.0);                                                 // 2^24
   return f;
 }
 __device__ __forceinline__ Fx fx_add(Fx a, Fx b) { return Fx{a.hi + b.hi, a.lo + b.lo}; }
