@@ -208,14 +208,25 @@ __device__ __forceinline__ T bin_at(const T (&p)[PBL], int b) {
 
 __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode) {
   const int l = lane_id();
+  // the row's scalars first: their loads overlap the histogram loads (plain loads written after the ordered ones
+  // would only be issued once those had been waited for)
   const gse_row &P = ds->P;
   const float M = ds->M;
+  const uint64_t K = P.top_k > 0 ? (uint64_t)P.top_k : ~0ull;
+  const double top_p = P.top_p, min_p = P.min_p, u = ds->u;
   uint64_t c[PBL], mh[PBL], mo[PBL];
 #pragma unroll
   for (int j = 0; j < PBL; ++j) {
     c[j] = ld_ag(&gh[l * PBL + j]);
     mh[j] = ld_ag(&gh[DNB + l * PBL + j]);
     mo[j] = ld_ag(&gh[2 * DNB + l * PBL + j]);
+  }
+  // min-p keeps exp(z - M) >= min_p, i.e. d <= -ln(min_p): bins below bm - 1 are all kept, bins above bm + 1 all cut
+  const bool mp = min_p > 0.0;
+  uint32_t bm = 0;
+  if (mp) {
+    const double dm = -log(min_p) * (double)BSC;
+    bm = dm >= (double)(DNB - 1) ? (uint32_t)(DNB - 1) : (uint32_t)dm;
   }
   // inclusive prefixes through each bin: counts, exact masses (2^-40 and 2^-64 parts) and their fp64 values
   uint64_t cl = 0, hl = 0, ol = 0;
@@ -245,15 +256,7 @@ __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode
   const double S = fx_val(Fx{htot, otot});
   // the masses are exact; the margin covers the fp64 roundings of their values here (the finish decides exactly)
   const double delta = 1e-12 * S;
-  const uint64_t K = P.top_k > 0 ? (uint64_t)P.top_k : ~0ull;
-  const double tS = P.top_p * S;
-  // min-p keeps exp(z - M) >= min_p, i.e. d <= -ln(min_p): bins below bm - 1 are all kept, bins above bm + 1 all cut
-  const bool mp = P.min_p > 0.0;
-  uint32_t bm = 0;
-  if (mp) {
-    const double dm = -log(P.min_p) * (double)BSC;
-    bm = dm >= (double)(DNB - 1) ? (uint32_t)(DNB - 1) : (uint32_t)dm;
-  }
+  const double tS = top_p * S;
   // the windows of the cuts:
   //   b0, b1: first bins with inclusive mass >= tS - delta, >= tS + delta (top-p: the bin of the last kept element)
   //   b2:     first bin with inclusive count >= K (top-k: the bin of rank K - 1)
@@ -295,7 +298,6 @@ __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode
   uint32_t w2lo = w1lo, w2hi = w1hi;
   if (mode == MODE_SAMPLE) {
     const double qd0 = bin_at(pm, (int)w1lo - 1), qd1 = bin_at(pm, (int)w1hi);
-    const double u = ds->u;
     const double tlo = u * (qd0 - delta) - delta, thi = u * (qd1 + delta) + delta;
     uint32_t b3 = DNB - 1, b4 = DNB - 1;
 #pragma unroll
