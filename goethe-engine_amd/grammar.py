@@ -3,7 +3,10 @@ int32 form (token t allowed iff bit t % 32 of word t // 32 is set, LSB first; gr
 applies it on the GPU inside the fused pass instead of a host bool[V] unpack per row.
 
 Matcher: mask() -> bool tensor [vocab] (as the reference); bitmask() -> int32 tensor [ceil(vocab / 32)] (packed, what
-sample() consumes without unpacking); accept(tok) -> bool; done() -> bool.
+sample() consumes without unpacking); fill_bitmask(buf, row) writes the packed words into row `row` of an int32
+[rows, ceil(vocab / 32)] buffer; accept(tok) -> bool; done() -> bool.
+MaskBatch: the packed masks of one step's rows in one host buffer (pinned when a GPU is present) that sample() takes
+as its masks argument and sends to the device in one copy.
 Compiler: compile(kind, spec) -> object with new_matcher(). kind is "json_schema", "regex", "ebnf" or "json".
 xgrammar is imported only when a compiler is built (it is not installed in every environment).
 """
@@ -50,6 +53,10 @@ class _Matcher:
         self.m.fill_next_token_bitmask(self.bm, 0)
         return self.bm[0][:(self.v + 31) // 32]
 
+    def fill_bitmask(self, buf, row):
+        """The packed words of the allowed next tokens into row `row` of buf (int32 [rows, >= ceil(vocab / 32)])."""
+        self.m.fill_next_token_bitmask(buf, row)
+
     def mask(self):
         return unpack(self.bitmask(), self.v)
 
@@ -75,3 +82,52 @@ def pack(mask):
     b[:m.shape[0]] = m
     return torch.from_numpy((b.reshape(n, 32) << np.arange(32, dtype=np.uint64)).sum(1).astype(np.uint32)
                             .view(np.int32))
+
+
+class MaskBatch:
+    """The packed grammar masks of one step's rows (engine.py:272-273, :280 compute mask() per row and unpack it to
+    bool [V]): matchers write their rows' words in place into one host buffer, int32 [rows, ceil(vocab / 32)], pinned
+    when a GPU is present, and sample(..., masks=batch) sends the whole buffer to the device in one asynchronous copy
+    on the launch stream. Rows that were not filled since the last reset() carry no mask.
+
+    The copy reads the host buffer after sample() has been called, so refill it only once that call's results have
+    been read (sample() returns them synchronously; after sample_ex, synchronize first)."""
+
+    is_mask_batch = True
+
+    def __init__(self, rows, vocab, pin=None):
+        if rows <= 0 or vocab <= 0:
+            raise ValueError(f"rows {rows} and vocab {vocab} must be > 0")
+        self.rows, self.vocab, self.words = int(rows), int(vocab), (int(vocab) + 31) // 32
+        pin = torch.cuda.is_available() if pin is None else bool(pin)
+        self.host = torch.empty((self.rows, self.words), dtype=torch.int32, pin_memory=pin)
+        self.filled = np.zeros(self.rows, dtype=bool)
+        self._dev = None
+
+    def reset(self):
+        """Every row without a mask again (the words are left as they are and overwritten by the next fills)."""
+        self.filled[:] = False
+
+    def fill(self, row, matcher):
+        """Row `row` from a matcher's fill_bitmask(buf, row) (xgrammar's fill_next_token_bitmask(bitmask, index))."""
+        matcher.fill_bitmask(self.host, row)
+        self.filled[row] = True
+
+    def set(self, row, mask):
+        """Row `row` from a bool [vocab] mask or packed int32 words [>= ceil(vocab / 32)]."""
+        m = mask if isinstance(mask, torch.Tensor) else torch.from_numpy(np.asarray(mask))
+        if m.dtype in (torch.int32, torch.uint32) and self.words <= m.numel() < self.vocab:
+            w = m.reshape(-1)[:self.words]
+            self.host[row].copy_(w.view(torch.int32) if w.dtype == torch.uint32 else w)
+        elif m.numel() == self.vocab:
+            self.host[row].copy_(pack(m.reshape(-1).to(torch.bool)))
+        else:
+            raise ValueError(f"mask of row {row} has {m.numel()} entries, the row has {self.vocab} tokens")
+        self.filled[row] = True
+
+    def device_words(self, dev):
+        """The buffer on `dev` (one copy from the host buffer, on the current stream of dev)."""
+        if self._dev is None or self._dev.device != dev:
+            self._dev = torch.empty((self.rows, self.words), dtype=torch.int32, device=dev)
+        self._dev.copy_(self.host, non_blocking=True)
+        return self._dev

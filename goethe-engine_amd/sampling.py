@@ -146,10 +146,19 @@ def _rows(params, seeds, idxs, hist_offsets):
 
 
 def _masks(h, masks, n, v, dev, rows):
-    """Per-row masks (None, bool [V] or packed int32 [>= ceil(V / 32)]) -> device words [k, W] and rows' mask_row."""
+    """Per-row masks (None, bool [V] or packed int32 [>= ceil(V / 32)]), or a grammar.MaskBatch -> device words [k, W]
+    and rows' mask_row."""
     if masks is None:
         return None, 0
     words = (v + 31) // 32
+    if getattr(masks, "is_mask_batch", False):  # grammar.MaskBatch: every row's words in one host buffer, one copy
+        if masks.rows != n or masks.vocab != v:
+            raise ValueError(f"mask batch of {masks.rows} x {masks.vocab}, the logits are {n} x {v}")
+        if not masks.filled.any():
+            return None, 0
+        idx = np.nonzero(masks.filled)[0]
+        rows["mask_row"][idx] = idx
+        return masks.device_words(dev), masks.words
     packed, bools, where = [], [], []
     for i in range(n):
         m = masks[i]

@@ -241,3 +241,51 @@ def test_deep_slots_overflow_to_exact(ge, gpu):
     assert got == ora.sample(x, params, None, None, None, uniforms=u)
     assert (paths == ge._lib.PATH_DEEP).sum() <= 128, paths
     assert (paths == ge._lib.PATH_EXACT).sum() >= 1, paths
+
+
+def test_mask_batch_one_copy_matches_row_masks(ge, gpu):
+    """Grammar masks straight to the device (one pinned buffer, one copy): the tokens, probabilities of the kept
+    tokens and processed logits equal those of the same masks passed row by row (bool and packed), which the oracle
+    pins in the tests above; rows left unfilled sample unmasked."""
+    rng = np.random.default_rng(11)
+    n, v = 12, 20000
+    x = torch.from_numpy((rng.standard_normal((n, v)) * 2.0).astype(np.float32)).to(gpu)
+    params = [_P(ge, temperature=0.8 if i % 3 else 0.0, top_p=0.9, top_k=50 if i % 2 else 0) for i in range(n)]
+    seeds, idxs = list(range(100, 100 + n)), [3] * n
+    masks = [(rng.random(v) < 0.3) if i < 8 else None for i in range(n)]
+    mb = ge.grammar.MaskBatch(n, v)
+    assert mb.host.is_pinned()
+    for i in range(8):
+        if i % 2:
+            mb.set(i, masks[i])
+        else:
+            mb.set(i, ge.grammar.pack(masks[i]))
+    want = ge.sampling.sample_ex(x, params, seeds, idxs, masks, processed=True)
+    got = ge.sampling.sample_ex(x, params, seeds, idxs, mb, processed=True)
+    torch.cuda.synchronize()
+    assert want.tolist() == got.tolist()
+    assert torch.equal(want.processed, got.processed)
+    for i in range(8):
+        assert bool(masks[i][want.tolist()[i]])
+    # the same buffer refilled for a second step (fewer rows filled)
+    mb.reset()
+    mb.set(1, masks[1])
+    masks2 = [masks[1] if i == 1 else None for i in range(n)]
+    assert ge.sampling.sample(x, params, seeds, idxs, mb) == ge.sampling.sample(x, params, seeds, idxs, masks2)
+
+
+def test_logits_borrowed_not_copied(ge, gpu, monkeypatch):
+    """Device-resident logits hand-off: sample() reads the caller's device tensor in place (the pointer it passes is
+    the tensor's own) and never brings logits to the host (sampling.py:54-56 host() is not on the path)."""
+    rng = np.random.default_rng(12)
+    x = torch.from_numpy(rng.standard_normal((4, 5000)).astype(np.float32)).to(gpu)
+    y, _ = ge.sampling._logits(x)
+    assert y.data_ptr() == x.data_ptr()
+
+    def no_host(*_):
+        raise AssertionError("logits brought to the host")
+
+    monkeypatch.setattr(ge.sampling, "host", no_host)
+    params = [_P(ge, temperature=1.0, top_p=0.95) for _ in range(4)]
+    toks = ge.sampling.sample(x, params, [1, 2, 3, 4], [0, 0, 0, 0], None)
+    assert toks == ora.sample(x.cpu().numpy(), params, [1, 2, 3, 4], [0, 0, 0, 0], None)

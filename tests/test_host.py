@@ -43,6 +43,48 @@ def test_row_records(ge):
     assert r["repetition_penalty"][1] == np.float32(1.1) and r["logprobs"].tolist() == [0, 3, 0]
 
 
+class _PackedMatcher:
+    """A matcher with xgrammar's packed fill (fill_next_token_bitmask(bitmask, index) writes row index)."""
+
+    def __init__(self, ge, mask):
+        self.words = ge.grammar.pack(mask)
+
+    def fill_bitmask(self, buf, row):
+        buf[row, :self.words.numel()] = self.words
+
+
+def test_mask_batch_fill_and_rows(ge):
+    """grammar.MaskBatch: matcher fills and set() give the packed words of each row; unfilled rows carry no mask;
+    sample()'s mask step maps filled rows onto the batch's rows (here on the CPU device: no copy kernel involved)."""
+    rng = np.random.default_rng(2)
+    n, v = 6, 1000
+    masks = [rng.random(v) < 0.4 for _ in range(n)]
+    mb = ge.grammar.MaskBatch(n, v, pin=False)
+    assert mb.host.shape == (n, (v + 31) // 32) and not mb.filled.any()
+    mb.fill(0, _PackedMatcher(ge, masks[0]))
+    mb.set(2, masks[2])                               # bool [V]
+    mb.set(3, ge.grammar.pack(masks[3]))              # packed int32 words
+    mb.set(5, torch.from_numpy(masks[5]))             # bool tensor
+    assert mb.filled.tolist() == [True, False, True, True, False, True]
+    for i in (0, 2, 3, 5):
+        assert (mb.host[i].numpy() == ora.pack_mask(masks[i])).all()
+    with pytest.raises(ValueError):
+        mb.set(1, np.ones(v - 1, dtype=bool))
+    params = [ge.sampling.SamplingParams() for _ in range(n)]
+    rows = ge.sampling._rows(params, None, None, None)
+    words, ld = ge.sampling._masks(None, mb, n, v, torch.device("cpu"), rows)
+    assert ld == (v + 31) // 32 and words.shape == (n, ld)
+    assert rows["mask_row"].tolist() == [0, -1, 2, 3, -1, 5]
+    assert torch.equal(words, mb.host)
+    with pytest.raises(ValueError):
+        ge.sampling._masks(None, mb, n + 1, v, torch.device("cpu"), ge.sampling._rows(params + params[:1], None,
+                                                                                        None, None))
+    mb.reset()
+    rows = ge.sampling._rows(params, None, None, None)
+    assert ge.sampling._masks(None, mb, n, v, torch.device("cpu"), rows) == (None, 0)
+    assert rows["mask_row"].tolist() == [-1] * n
+
+
 def test_grammar_pack_unpack(ge):
     rng = np.random.default_rng(1)
     for v in (1, 31, 32, 33, 1000, 4097):
