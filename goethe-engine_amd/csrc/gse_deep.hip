@@ -753,6 +753,18 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
   DeepSlot *ds = a.dslot + slot;
   const float Mf = ds->M;
   const int p0 = slice * g.len, p1 = min(a.V, p0 + g.len);
+  // The slice's z, as the count item of this workgroup for the same slice wrote it: four vectors per thread, loaded
+  // unconditionally (a vector past the slice end reloads the slice's first one and is skipped; a vector that starts
+  // below p1 lies inside the row's buffer, whose length is a multiple of 64). The first round is loaded before the
+  // wait for the plan, so that it arrives while the wait lasts.
+  const float *zr = a.dz + (size_t)slot * a.dz_ld;
+  constexpr int PV = 4;
+  float4 v0[PV];
+#pragma unroll
+  for (int j = 0; j < PV; ++j) {
+    const int t = p0 + (j * MT + tid) * 4;
+    v0[j] = *reinterpret_cast<const float4 *>(zr + (t < p1 ? t : p0));
+  }
   __syncthreads();  // (LDS of the previous item)
   if (tid == 0) {
     sh.nwl = 0;
@@ -785,18 +797,13 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
         }
       }
     };
-    // the slice's z, as the count phase of this workgroup wrote it: four vectors per thread in flight, loaded
-    // unconditionally (a vector past the slice end reloads the slice's first one and is skipped; a vector that starts
-    // below p1 lies inside the row's buffer, whose length is a multiple of 64)
-    const float *zr = a.dz + (size_t)slot * a.dz_ld;
-    constexpr int PV = 4;
 #pragma unroll 1
     for (int t0 = p0; t0 < p1; t0 += PV * MT * 4) {
       float4 v[PV];
 #pragma unroll
       for (int j = 0; j < PV; ++j) {
         const int t = t0 + (j * MT + tid) * 4;
-        v[j] = *reinterpret_cast<const float4 *>(zr + (t < p1 ? t : p0));
+        v[j] = t0 == p0 ? v0[j] : *reinterpret_cast<const float4 *>(zr + (t < p1 ? t : p0));
       }
 #pragma unroll
       for (int j = 0; j < PV; ++j) {
