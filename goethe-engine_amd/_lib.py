@@ -11,11 +11,15 @@ import threading
 import numpy as np
 import torch
 
-ABI_MAJOR, ABI_MINOR = 1, 1
+ABI_MAJOR, ABI_MINOR = 1, 2
 PATH_MAIN, PATH_DEEP, PATH_EXACT = 0, 1, 2  # gse_row_paths codes
 OK, E_ARG, E_DEVICE, E_UNSUPPORTED, E_CAPACITY = 0, -1, -4, -5, -7
 F32, BF16 = 0, 1
 ROW_TEMP_UNDERFLOW = 1
+ROW_MSS = 2
+Q_PROB, Q_LOGITS_F32, Q_LOGITS_BF16 = 0, 1, 2
+WALK_OK, WALK_ERROR, WALK_TRUNCATED = 0, 1, 2
+MAX_KIDS = 16
 BATCH_EXACT = 1
 BATCH_PROFILE = 2
 BATCH_NO_PLAN_WAIT = 4
@@ -58,6 +62,30 @@ class MssBatch(C.Structure):
                 ("out_token", C.c_void_p), ("out_kid", C.c_void_p), ("stream", C.c_void_p)]
 
 
+class QRows(C.Structure):
+    _fields_ = [("size", C.c_uint32), ("kind", C.c_uint32), ("rows", C.c_uint32), ("reserved", C.c_uint32),
+                ("q", C.c_void_p), ("ld", C.c_int64), ("temperature", C.c_void_p)]
+
+
+class Tree(C.Structure):
+    _fields_ = [("size", C.c_uint32), ("requests", C.c_uint32), ("anchor", C.c_void_p), ("parent", C.c_void_p),
+                ("token", C.c_void_p), ("qrow", C.c_void_p), ("qrows", QRows), ("max_kids", C.c_uint32),
+                ("reserved", C.c_uint32)]
+
+
+class TreeOut(C.Structure):
+    _fields_ = [("size", C.c_uint32), ("reserved", C.c_uint32), ("emit_len", C.c_void_p), ("emit_tokens", C.c_void_p),
+                ("emit_nodes", C.c_void_p), ("emit_ld", C.c_int64), ("status", C.c_void_p),
+                ("node_token", C.c_void_p), ("node_kid", C.c_void_p)]
+
+
+class PickBatch(C.Structure):
+    _fields_ = [("size", C.c_uint32), ("dtype", C.c_uint32), ("rows", C.c_uint32), ("vocab", C.c_uint32),
+                ("x", C.c_void_p), ("ld", C.c_int64), ("temperature", C.c_void_p), ("n", C.c_void_p),
+                ("seed", C.c_void_p), ("at", C.c_void_p), ("out_tokens", C.c_void_p), ("out_logq", C.c_void_p),
+                ("out_ld", C.c_int64), ("stream", C.c_void_p)]
+
+
 SIGNATURES = dict(
     gse_abi_version=(C.c_uint32, []),
     gse_open=(C.c_int, [P_(OpenParams), P_(C.c_void_p)]),
@@ -66,6 +94,8 @@ SIGNATURES = dict(
     gse_draw=(C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p,
                         C.c_void_p]),
     gse_mss=(C.c_int, [C.c_void_p, P_(MssBatch)]),
+    gse_verify_tree=(C.c_int, [C.c_void_p, P_(Batch), P_(Tree), P_(TreeOut)]),
+    gse_draft_pick=(C.c_int, [C.c_void_p, P_(PickBatch)]),
     gse_pack_mask=(C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_uint32, C.c_uint32, C.c_void_p, C.c_int64,
                              C.c_void_p]),
     gse_profile=(C.c_int, [C.c_void_p, P_(C.c_float), C.c_uint32, P_(C.c_uint32)]),

@@ -25,6 +25,20 @@ struct gse_handle {
   uint64_t *dlist = nullptr;
   float *dz = nullptr;
   int64_t dz_ld = 0;
+  // verify rounds and drafter picks (gse_tree.hip): per row slices of the vocabulary, nsl of them at most
+  uint32_t nsl = 0;
+  int32_t *ttok = nullptr;            // [max_rows] sampled tokens of the verify round's selection pass
+  gse::TreeNode *tstate = nullptr;    // [max_rows]
+  gse::Fx *npart = nullptr;           // [max_rows][GSE_MAX_KIDS + 1][nsl]
+  int32_t *nlast = nullptr;           // [max_rows][GSE_MAX_KIDS + 1][nsl]
+  double *qmax = nullptr;             // [max_rows][nsl]
+  gse::Fx *qpart = nullptr;           // [max_rows][nsl]
+  gse::QFin *qfin = nullptr;          // [max_rows]
+  double *pmax = nullptr;             // [max_rows][nsl]
+  gse::Fx *ppart = nullptr;           // [max_rows][nsl]
+  int32_t *plast = nullptr;           // [max_rows][nsl]
+  uint64_t *ptop = nullptr;           // [max_rows][nsl][4 * GSE_MAX_KIDS]
+  uint32_t *ptick = nullptr;          // [max_rows]
   hipEvent_t (*ring)[5] = nullptr;  // kernel boundaries of up to GSE_PROFILE_CALLS profiled calls
   int nring = 0;                    // calls recorded
   int nprof = 0;                    // kernels per recorded call
@@ -78,7 +92,7 @@ struct DeviceGuard {
 int prof_slot(gse_handle *h, int kernels, hipEvent_t **ev) {
   *ev = nullptr;
   if (!h->ring) {
-    h->ring = new (std::nothrow) hipEvent_t[GSE_PROFILE_CALLS][5];
+    h->ring = new (std::nothrow) hipEvent_t[GSE_PROFILE_CALLS][5]();  // (null handles until created)
     if (!h->ring) return fail(h, GSE_E_DEVICE, "out of host memory");
     for (int c = 0; c < GSE_PROFILE_CALLS; ++c)
       for (int i = 0; i < 5; ++i) {
@@ -161,6 +175,26 @@ gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   return a;
 }
 
+template <typename T>
+hipError_t zalloc(T **p, size_t n) {
+  hipError_t e = hipMalloc(p, n * sizeof(T));
+  return e == hipSuccess ? hipMemset(*p, 0, n * sizeof(T)) : e;
+}
+
+// Workspace of verify rounds and drafter picks, sized for max_rows x max_vocab.
+hipError_t alloc_tree(gse_handle *h) {
+  const size_t R = h->max_rows, L = h->nsl, K = GSE_MAX_KIDS + 1;
+  hipError_t e;
+  if ((e = zalloc(&h->ttok, R)) != hipSuccess || (e = zalloc(&h->tstate, R)) != hipSuccess ||
+      (e = zalloc(&h->npart, R * K * L)) != hipSuccess || (e = zalloc(&h->nlast, R * K * L)) != hipSuccess ||
+      (e = zalloc(&h->qmax, R * L)) != hipSuccess || (e = zalloc(&h->qpart, R * L)) != hipSuccess ||
+      (e = zalloc(&h->qfin, R)) != hipSuccess || (e = zalloc(&h->pmax, R * L)) != hipSuccess ||
+      (e = zalloc(&h->ppart, R * L)) != hipSuccess || (e = zalloc(&h->plast, R * L)) != hipSuccess ||
+      (e = zalloc(&h->ptop, R * L * 4 * GSE_MAX_KIDS)) != hipSuccess || (e = zalloc(&h->ptick, R)) != hipSuccess)
+    return e;
+  return hipSuccess;
+}
+
 }  // namespace
 
 extern "C" {
@@ -192,6 +226,7 @@ GSE_API int gse_open(const gse_open_params *p, gse_handle **out) {
   h->target = 4u * (uint32_t)(prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256);
   h->nrec = h->max_rows * ((o.max_vocab + gse::PTOK - 1) / gse::PTOK + 1) + h->target;
   h->dz_ld = ((int64_t)o.max_vocab + 63) / 64 * 64;
+  h->nsl = (o.max_vocab + gse::CH - 1) / gse::CH;
   const size_t dzn = (size_t)(h->max_rows < (uint32_t)gse::DEEP_MAX ? h->max_rows : (uint32_t)gse::DEEP_MAX) * h->dz_ld;
   if ((e = hipMalloc(&h->rec, (size_t)h->nrec * sizeof(gse::SliceRec))) != hipSuccess ||
       (e = hipMalloc(&h->cand, (size_t)h->nrec * gse::PWAVES * gse::CAPW * sizeof(uint64_t))) != hipSuccess ||
@@ -206,6 +241,7 @@ GSE_API int gse_open(const gse_open_params *p, gse_handle **out) {
       (e = hipMemset(h->dhist, 0, (size_t)gse::DEEP_MAX * 3 * gse::DNB * sizeof(uint64_t))) != hipSuccess ||
       (e = hipMalloc(&h->dlist, (size_t)gse::DEEP_MAX * gse::DCAP * sizeof(uint64_t))) != hipSuccess ||
       (e = hipMalloc(&h->dz, dzn * sizeof(float))) != hipSuccess ||
+      (e = alloc_tree(h)) != hipSuccess ||
       (e = hipDeviceSynchronize()) != hipSuccess) {
     fail(nullptr, GSE_E_DEVICE, "workspace allocation (%u part records): %s", h->nrec, hipGetErrorString(e));
     gse_close(h);
@@ -275,6 +311,86 @@ GSE_API int gse_dist(gse_handle *h, const gse_batch *in, double *probs, int64_t 
   if ((e = gse::launch_dist_write(a, probs, probs_ld, s)) != hipSuccess) return hip_fail(h, e, "dist launch");
   if (ev && (e = hipEventRecord(ev[4], s)) != hipSuccess) return hip_fail(h, e, "event record");
   return GSE_OK;
+}
+
+GSE_API int gse_verify_tree(gse_handle *h, const gse_batch *in, const gse_tree *tree, const gse_tree_out *out) {
+  if (!h) return fail(nullptr, GSE_E_ARG, "null handle");
+  gse_batch b;
+  gse_tree t;
+  gse_tree_out o;
+  if (!take(in, b) || !take(tree, t) || !take(out, o)) return fail(h, GSE_E_ARG, "null or short gse_batch / gse_tree / gse_tree_out");
+  int rc = check_batch(h, b);
+  if (rc) return rc;
+  if (t.requests == 0 || b.rows == 0) return GSE_OK;
+  if (!t.anchor || !t.parent || !t.token) return fail(h, GSE_E_ARG, "tree anchor, parent and token are required");
+  if (t.requests > b.rows) return fail(h, GSE_E_ARG, "%u requests over %u node rows", t.requests, b.rows);
+  if (t.max_kids > GSE_MAX_KIDS) return fail(h, GSE_E_UNSUPPORTED, "max_kids %u > %d", t.max_kids, GSE_MAX_KIDS);
+  if (!o.emit_len || !o.emit_tokens || !o.emit_nodes || o.emit_ld <= 0)
+    return fail(h, GSE_E_ARG, "emit_len, emit_tokens, emit_nodes and emit_ld > 0 are required");
+  if (t.qrows.rows > 0) {
+    const gse_qrows &q = t.qrows;
+    if (q.size < 8) return fail(h, GSE_E_ARG, "short gse_qrows");
+    if (q.kind > GSE_Q_LOGITS_BF16) return fail(h, GSE_E_ARG, "q kind %u", q.kind);
+    if (!q.q || q.ld < (int64_t)b.vocab) return fail(h, GSE_E_ARG, "q rows missing or q ld < vocab");
+    if (q.kind != GSE_Q_PROB && !q.temperature) return fail(h, GSE_E_ARG, "q logits need temperatures");
+    if (q.rows > h->max_rows)
+      return fail(h, GSE_E_CAPACITY, "%u q rows, the handle was opened for %u rows", q.rows, h->max_rows);
+  } else {
+    t.qrows.rows = 0;
+  }
+  DeviceGuard g(h->device);
+  gse::ScanArgs a = make_args(h, b, gse::MODE_SAMPLE);
+  a.tree = 1;
+  a.tokens = h->ttok;
+  hipStream_t s = (hipStream_t)b.stream;
+  hipError_t e;
+  if ((e = gse::launch_main(a, s)) != hipSuccess) return hip_fail(h, e, "main launch");
+  if (a.dgrid > 0 && (e = gse::launch_deep(a, s)) != hipSuccess) return hip_fail(h, e, "deep launch");
+  if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
+  gse::TreeLaunch L = {};
+  L.s = a;
+  L.parent = t.parent;
+  L.token = t.token;
+  L.qrow = t.qrow;
+  L.anchor = t.anchor;
+  L.q = t.qrows;
+  L.max_kids = (int)t.max_kids;
+  L.requests = (int)t.requests;
+  L.sampled = h->ttok;
+  L.st = h->tstate;
+  L.npart = h->npart;
+  L.nlast = h->nlast;
+  L.qmax = h->qmax;
+  L.qpart = h->qpart;
+  L.qfin = h->qfin;
+  L.out = o;
+  if ((e = gse::launch_tree(L, s)) != hipSuccess) return hip_fail(h, e, "verify launch");
+  return GSE_OK;
+}
+
+GSE_API int gse_draft_pick(gse_handle *h, const gse_pick_batch *in) {
+  if (!h) return fail(nullptr, GSE_E_ARG, "null handle");
+  gse_pick_batch b;
+  if (!take(in, b)) return fail(h, GSE_E_ARG, "null or short gse_pick_batch");
+  if (b.rows == 0) return GSE_OK;
+  if (!b.x || !b.temperature || !b.n || !b.seed || !b.at || !b.out_tokens || !b.out_logq)
+    return fail(h, GSE_E_ARG, "x, temperature, n, seed, at, out_tokens and out_logq are required");
+  if (b.dtype != GSE_F32 && b.dtype != GSE_BF16) return fail(h, GSE_E_ARG, "dtype %u is neither f32 nor bf16", b.dtype);
+  if (b.vocab == 0 || b.ld < (int64_t)b.vocab) return fail(h, GSE_E_ARG, "vocab 0 or ld < vocab");
+  if (b.out_ld <= 0) return fail(h, GSE_E_ARG, "out_ld must be > 0");
+  if (b.rows > h->max_rows) return fail(h, GSE_E_CAPACITY, "%u rows, the handle was opened for %u", b.rows, h->max_rows);
+  if (b.vocab > h->max_vocab)
+    return fail(h, GSE_E_CAPACITY, "vocab %u, the handle was opened for %u", b.vocab, h->max_vocab);
+  DeviceGuard g(h->device);
+  gse::PickLaunch L = {};
+  L.b = b;
+  L.pmax = h->pmax;
+  L.ppart = h->ppart;
+  L.plast = h->plast;
+  L.ptop = h->ptop;
+  L.tick = h->ptick;
+  hipError_t e = gse::launch_pick(L, (hipStream_t)b.stream);
+  return e == hipSuccess ? GSE_OK : hip_fail(h, e, "pick launch");
 }
 
 GSE_API int gse_draw(gse_handle *h, const double *q, int64_t q_ld, uint32_t rows, uint32_t vocab, const double *u,
@@ -367,9 +483,13 @@ GSE_API void gse_close(gse_handle *h) {
     if (h->dhist) (void)hipFree(h->dhist);
     if (h->dlist) (void)hipFree(h->dlist);
     if (h->dz) (void)hipFree(h->dz);
+    void *tree_bufs[] = {h->ttok, h->tstate, h->npart, h->nlast, h->qmax, h->qpart, h->qfin,
+                         h->pmax, h->ppart, h->plast, h->ptop, h->ptick};
+    for (void *p : tree_bufs)
+      if (p) (void)hipFree(p);
     if (h->ring) {
       for (int c = 0; c < GSE_PROFILE_CALLS; ++c)
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 5; ++i)
           if (h->ring[c][i]) (void)hipEventDestroy(h->ring[c][i]);
       delete[] h->ring;
     }

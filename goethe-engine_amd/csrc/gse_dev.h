@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #include "../../include/gse.h"
+#include "gse_int.h"
 
 namespace gse {
 
@@ -278,12 +279,8 @@ __device__ __forceinline__ double exp_nonpos(double d, const double *tab) {
   return d >= -745.0 ? e : 0.0;
 }
 
-// Fixed-point masses: an fp64 exp(z - M) in [0, 1] as hi * 2^-40 + lo * 2^-64 (both floors, so the value is within
-// 2^-64 below the fp64 one). Sums of up to 2^24 of them add hi and lo separately with no carry, so a sum is the same
-// whatever order its terms are added in.
-struct Fx {  // value = hi * 2^-40 + lo * 2^-64
-  uint64_t hi, lo;
-};
+// Fixed-point masses (Fx, gse_int.h): an fp64 exp(z - M) in [0, 1] as hi * 2^-40 + lo * 2^-64 (both floors, so the
+// value is within 2^-64 below the fp64 one).
 // The conversions are exact and short: h = floor(s) < 2^52 is an integer, so h + 2^52 holds h in its 52 fraction
 // bits; the remainder scaled by 2^24 is below 2^24, and the truncating conversion to u32 is its floor (it is >= 0).
 __device__ __forceinline__ Fx fx_of(double e) {

@@ -7,6 +7,12 @@
 
 namespace gse {
 
+// Fixed-point masses: an fp64 value in [0, 1] as hi * 2^-40 + lo * 2^-64 (gse_dev.h fx_of). Sums of up to 2^24 of them
+// add hi and lo separately with no carry, so a sum is the same whatever order its terms are added in.
+struct Fx {
+  uint64_t hi, lo;
+};
+
 static_assert(sizeof(gse_row) == 72, "gse_row layout is part of the ABI");
 
 enum : uint32_t {
@@ -126,6 +132,46 @@ struct ScanArgs {
   int64_t dz_ld;
   int dslices, dgrid;  // split-row finish enabled (slices per deep row, at most), workgroups per pass
   uint64_t plan_wait;  // wall-clock ticks (100 MHz) a split-row pick slice waits for its row's plan
+  int tree;            // a verify round (gse_verify_tree): GSE_ROW_MSS rows need dist's keep boundary, not a token
+};
+
+// Verify round state of one node (gse_tree.hip), in the handle's workspace.
+struct TreeNode {
+  uint32_t next;     // residual pass the next launch runs for this node (0: decided)
+  uint32_t ticket;   // slice ticket of the current pass (zero between passes)
+  int32_t token;     // the decision: the node's token and the accepted kid row (-1 none)
+  int32_t kid;
+  double clast;      // exact kept mass C = sum(keep exp(z - M)) of dist()
+  double sig[GSE_MAX_KIDS + 1];  // totals of the residuals res_1.. (sig[0] = C)
+};
+
+struct QFin {        // a logits q row: max of z = x / t and the exact mass sum exp(z - M)
+  double M, E;
+  uint32_t ticket, pad;
+};
+
+struct TreeLaunch {
+  ScanArgs s;
+  const int32_t *parent, *token, *qrow, *anchor;
+  gse_qrows q;
+  int max_kids, requests;
+  const int32_t *sampled;
+  TreeNode *st;
+  Fx *npart;
+  int32_t *nlast;
+  double *qmax;
+  Fx *qpart;
+  QFin *qfin;
+  gse_tree_out out;
+};
+
+struct PickLaunch {
+  gse_pick_batch b;
+  double *pmax;
+  Fx *ppart;
+  int32_t *plast;
+  uint64_t *ptop;
+  uint32_t *tick;
 };
 
 hipError_t launch_main(const ScanArgs &a, hipStream_t s);
@@ -134,6 +180,8 @@ hipError_t launch_exact(const ScanArgs &a, hipStream_t s);
 hipError_t launch_dist_write(const ScanArgs &a, double *probs, int64_t probs_ld, hipStream_t s);
 hipError_t launch_draw(const double *q, int64_t ld, int rows, int V, const double *u, int32_t *out, hipStream_t s);
 hipError_t launch_mss(const gse_mss_batch &b, hipStream_t s);
+hipError_t launch_tree(const TreeLaunch &L, hipStream_t s);
+hipError_t launch_pick(const PickLaunch &L, hipStream_t s);
 hipError_t launch_pack(const uint8_t *bools, int64_t bld, int rows, int V, int32_t *words, int64_t wld, hipStream_t s);
 
 }  // namespace gse

@@ -408,6 +408,13 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   // Gather the listed elements: masses for S, the certified head, the packed maximum.
   const bool finite_max = mk < KEY_POSINF;
   const double M = finite_max ? (double)fkey_inv(mk) : 0.0;
+  if (a.tree && (P.flags & GSE_ROW_MSS) && finite_max && !(flags & F_HOVER) &&
+      (P.top_k <= 0 || P.top_k >= a.V) && P.top_p >= 1.0 && !(P.min_p > 0.0)) {
+    // a verify node that takes dist + mss and keeps every token (sampling.py:80 with top_k off, top_p 1): dist needs
+    // only the maximum of z; the verify round's stats pass forms the exact kept mass itself
+    if (tid == 0) set_info(ri, pack(mk, 0u), 0ull, 0.0, 0.0, R_DONE, -1);
+    return;
+  }
   const uint32_t kappa = max(sh.rkappa, KEY_NEGINF + 1u);
   const bool complete = kappa <= KEY_NEGINF + 1u;
   double srest = 0.0, brest = 0.0;

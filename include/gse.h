@@ -24,7 +24,7 @@ extern "C" {
 #endif
 
 #define GSE_ABI_MAJOR 1
-#define GSE_ABI_MINOR 1
+#define GSE_ABI_MINOR 2
 #define GSE_ABI_VERSION ((GSE_ABI_MAJOR << 16) | GSE_ABI_MINOR)
 
 #if defined(__GNUC__)
@@ -74,7 +74,10 @@ typedef struct gse_row {
 
 /* gse_row.flags */
 enum {
-  GSE_ROW_TEMP_UNDERFLOW = 1u /* temperature > 0 whose float32 is 0: sampled, dividing by 0 as sampling.py:61 does */
+  GSE_ROW_TEMP_UNDERFLOW = 1u, /* temperature > 0 whose float32 is 0: sampled, dividing by 0 as sampling.py:61 does */
+  GSE_ROW_MSS = 2u /* gse_verify_tree: this node's token comes from dist + mss over its kids (a strict request's node
+                    * with kids, engine.py:278-283); without it the node samples and the walk follows the kid holding
+                    * the sampled token (engine.py:270-276,284-285). Ignored by gse_sample / gse_dist. */
 };
 
 #define GSE_MAX_LOGPROBS 64
@@ -134,6 +137,79 @@ typedef struct gse_mss_batch {
   void *stream;
 } gse_mss_batch;
 
+/* Draft distributions of a speculative tree (the q of spec.py:26, Tree.q: the distribution each drafted token was drawn
+ * from). Either fp64 probability rows in vocabulary order (GSE_Q_PROB, as the reference holds them), or drafter logits
+ * / log-probabilities (GSE_Q_LOGITS_F32 / _BF16) with a per-row temperature t: q = softmax(float64(x) / t), as
+ * spec.py:157 forms it, computed on the device and never materialised. */
+enum { GSE_Q_PROB = 0, GSE_Q_LOGITS_F32 = 1, GSE_Q_LOGITS_BF16 = 2 };
+
+typedef struct gse_qrows {
+  uint32_t size;
+  uint32_t kind;           /* GSE_Q_* */
+  uint32_t rows;           /* q rows */
+  uint32_t reserved;
+  const void *q;           /* [rows][ld] */
+  int64_t ld;
+  const double *temperature; /* [rows] (GSE_Q_LOGITS_*): t > 0 */
+} gse_qrows;
+
+#define GSE_MAX_KIDS 16
+
+/* One verify round of speculative decoding over many requests' draft trees (engine.py:262-298). Every tree node is one
+ * row of the target batch: row u holds the target logits after node u, and its gse_row the request's parameters with
+ * seed = the request's seed, idx = nout0 + depth(u) (the uniform index the walk gives the node, engine.py:272,282),
+ * mask_row / history the grammar mask and penalty history that hold once the path to u is accepted, and GSE_ROW_MSS on
+ * the nodes that take dist + mss. A request's nodes are consecutive rows starting at its anchor (parent -1), every
+ * other node after its parent (spec.py:23-25). */
+typedef struct gse_tree {
+  uint32_t size;
+  uint32_t requests;
+  const int32_t *anchor;   /* [requests] row of each request's anchor, increasing */
+  const int32_t *parent;   /* [rows] parent row (-1: an anchor) */
+  const int32_t *token;    /* [rows] drafted token of the node (anchors: ignored) */
+  const int32_t *qrow;     /* [rows] row of qrows holding the distribution the node's token was drawn from; -1 one-hot
+                            * (a deterministic drafter, spec.py:93 q None); NULL: every kid one-hot */
+  gse_qrows qrows;
+  uint32_t max_kids;       /* >= the kids of any GSE_ROW_MSS node, <= GSE_MAX_KIDS */
+  uint32_t reserved;
+} gse_tree;
+
+enum { GSE_WALK_OK = 0, GSE_WALK_ERROR = 1, GSE_WALK_TRUNCATED = 2 };
+
+typedef struct gse_tree_out {
+  uint32_t size;
+  uint32_t reserved;
+  int32_t *emit_len;       /* [requests] tokens emitted by the walk */
+  int32_t *emit_tokens;    /* [requests][emit_ld] the emitted tokens */
+  int32_t *emit_nodes;     /* [requests][emit_ld] the node (row) each came from: the accepted path, anchor first; after
+                            * an error, entry emit_len holds the node whose row had no valid token */
+  int64_t emit_ld;         /* >= the deepest path + 1 (else GSE_WALK_TRUNCATED and the first emit_ld are written) */
+  uint32_t *status;        /* [requests] GSE_WALK_*: ERROR when a node had no valid token (engine.py:286-288; the -1 is
+                            * not emitted) */
+  int32_t *node_token;     /* optional [rows]: the token each node emits if the walk reaches it */
+  int32_t *node_kid;       /* optional [rows]: the kid row the node accepts, -1 none */
+} gse_tree_out;
+
+/* Drafter-side selection (spec.py:151-159 TreeDrafter._pick) for many nodes: row r of the drafter's logits /
+ * log-probabilities picks n[r] children. temperature[r] == 0: the n best tokens in stable descending order; t > 0:
+ * q = softmax(float64(x) / t) and n draws draw(q, uniform(mix(seed[r], SALT_DRAFT + k), at[r])), k = 0..n-1. */
+typedef struct gse_pick_batch {
+  uint32_t size;
+  uint32_t dtype;          /* GSE_F32 or GSE_BF16 */
+  uint32_t rows;
+  uint32_t vocab;
+  const void *x;           /* [rows][ld] */
+  int64_t ld;
+  const double *temperature; /* [rows] */
+  const int32_t *n;        /* [rows] children to pick, <= out_ld */
+  const uint64_t *seed;    /* [rows] */
+  const uint64_t *at;      /* [rows] absolute index of the node's next token (spec.py:150 `at`) */
+  int32_t *out_tokens;     /* [rows][out_ld] */
+  double *out_logq;        /* [rows][out_ld] log q[x] (t > 0), or the input value x (t == 0), as spec.py:155,159 */
+  int64_t out_ld;
+  void *stream;
+} gse_pick_batch;
+
 /* Replaces: nothing (version handshake, as gc_abi_version, abi/gc.h:82). */
 GSE_API uint32_t gse_abi_version(void);
 
@@ -149,6 +225,16 @@ GSE_API int gse_sample(gse_handle *h, const gse_batch *in, const gse_out *out);
 /* Replaces: goethe_engine/sampling.py:88-97 dist(): fp64 probabilities over the vocabulary (vocabulary order) that
  * sample() draws a temperature > 0 row from, with top-k, top-p, min-p, penalties and mask; probs is [rows][probs_ld]. */
 GSE_API int gse_dist(gse_handle *h, const gse_batch *in, double *probs, int64_t probs_ld);
+
+/* Replaces: the acceptance walk of goethe_engine/engine.py:262-298 (one sample() call per tree level, dist + mss per
+ * strict node, spec.py:88-103) with one call that runs every node of every request on the device and walks the trees
+ * there: no host round trip per level. Stop rules (engine.py:218-229) stay with the caller, which ends each emitted
+ * sequence at its first stop reason; the tokens before it do not depend on what follows. in->rows are the tree nodes. */
+GSE_API int gse_verify_tree(gse_handle *h, const gse_batch *in, const gse_tree *tree, const gse_tree_out *out);
+
+/* Replaces: goethe_engine/spec.py:151-159 TreeDrafter._pick (torch.sort / softmax / draw on the host) for a batch of
+ * nodes. */
+GSE_API int gse_draft_pick(gse_handle *h, const gse_pick_batch *in);
 
 /* Replaces: goethe_engine/sampling.py:100-104 draw(): inverse CDF in vocabulary order of each fp64 row q at u[r]:
  * min(count(cumsum(q) < u * sum(q)), last index with q > 0). */

@@ -19,7 +19,7 @@ def declared():
 
 def test_library_exports_every_declared_symbol(ge):
     names = declared()
-    assert len(names) == 11, names
+    assert len(names) == 13, names
     L = C.CDLL(ge._lib.PATH)
     for n in names:
         assert hasattr(L, n), n
@@ -46,6 +46,10 @@ int main(void) {
   printf("gse_batch %zu\n", sizeof(gse_batch));
   printf("gse_out %zu\n", sizeof(gse_out));
   printf("gse_mss_batch %zu\n", sizeof(gse_mss_batch));
+  printf("gse_qrows %zu\n", sizeof(gse_qrows));
+  printf("gse_tree %zu\n", sizeof(gse_tree));
+  printf("gse_tree_out %zu\n", sizeof(gse_tree_out));
+  printf("gse_pick_batch %zu\n", sizeof(gse_pick_batch));
   %FIELDS%
   return 0;
 }
@@ -55,7 +59,8 @@ int main(void) {
 def test_struct_layouts_match_the_header(ge, tmp_path):
     lib = ge._lib
     pairs = [("gse_open_params", lib.OpenParams), ("gse_batch", lib.Batch), ("gse_out", lib.Out),
-             ("gse_mss_batch", lib.MssBatch)]
+             ("gse_mss_batch", lib.MssBatch), ("gse_qrows", lib.QRows), ("gse_tree", lib.Tree),
+             ("gse_tree_out", lib.TreeOut), ("gse_pick_batch", lib.PickBatch)]
     fields = []
     for cname, cls in pairs:
         for f, _ in cls._fields_:

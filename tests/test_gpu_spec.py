@@ -1,0 +1,199 @@
+"""GPU parity of the speculative-decoding path through the C ABI: the device verify round (gse_verify_tree) against the
+oracle's walk (oracle/spec_ref.verify_tree, pinned in tests/test_oracle_walk.py), and the drafter's selection
+(gse_draft_pick) against the oracle's restatement of spec.py:151-159 and :183-204. Token ids and paths are compared
+bit-exact; log q within 1e-12 relative."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampling_ref as ora
+from oracle import spec_ref as spo
+
+pytestmark = pytest.mark.gpu
+
+
+def _q_of_draft(draft, parents, t=1.0):
+    """{node: softmax(draft[node] / t) in fp64} for the nodes with kids (what the kids were drawn from)."""
+    q = {}
+    for u, ks in enumerate(spo.kids_of(parents)):
+        if ks:
+            z = draft[u].astype(np.float64) / t
+            e = np.exp(z - z.max())
+            q[u] = e / e.sum()
+    return q
+
+
+def test_c4_verify_all_requests_matches_oracle(ge, gpu):
+    """All 32 requests of the tree-verification workload (V=128256), draft distributions given as drafter logits
+    (q = softmax(draft) formed on the device): emitted tokens and accepted paths equal the oracle walk's."""
+    reqs = ge.workloads.c4()
+    got = ge.spec.verify_tree([dict(target=torch.from_numpy(r["target"]).to(gpu), tokens=r["tokens"],
+                                    parents=r["parents"], params=r["params"], seed=r["seed"],
+                                    draft=torch.from_numpy(r["draft"]).to(gpu), draft_t=1.0) for r in reqs])
+    acc = 0
+    for a, r in enumerate(reqs):
+        want = spo.verify_tree(r["target"], _q_of_draft(r["draft"], r["parents"]), r["tokens"], r["parents"],
+                               r["params"], r["seed"])
+        assert got[a] == want, (a, got[a], want)
+        acc += len(want[1]) - 1
+    assert acc > 0  # some drafts were accepted
+
+
+def _random_trees(ge, rng, n_req, v, kinds):
+    P = ge.sampling.SamplingParams
+    reqs = []
+    for a in range(n_req):
+        kind = kinds[a % len(kinds)]
+        n = int(rng.integers(1, 9))
+        parents = [int(rng.integers(0, j + 1)) for j in range(n)]
+        target = rng.normal(0, 1.5, size=(n + 1, v)).astype(np.float32)
+        draft = (target + rng.normal(0, 0.6, size=target.shape)).astype(np.float32)
+        if kind == "greedy":
+            p = P()
+        elif kind == "exact":
+            p = P(temperature=0.8, top_k=int(rng.choice([0, 30])), top_p=float(rng.choice([1.0, 0.9])))
+        else:
+            p = P(temperature=float(rng.choice([0.7, 1.0, 1.3])), top_k=int(rng.choice([0, 0, 50])),
+                  top_p=float(rng.choice([1.0, 0.95, 0.8])), min_p=float(rng.choice([0.0, 0.0, 0.02])),
+                  accept="rejection")
+        # drafted tokens: drawn from q where the node has one, else a target top token (a deterministic drafter)
+        q = _q_of_draft(draft, parents)
+        toks = []
+        for j, par in enumerate(parents):
+            if kind == "rejection" and a % 3 != 0:
+                toks.append(int(rng.choice(v, p=q[par])))
+            else:
+                toks.append(int(np.argsort(-target[par], kind="stable")[int(rng.integers(0, 3))]))
+        reqs.append(dict(target=target, draft=draft, tokens=toks, parents=parents, params=p,
+                         seed=int(rng.integers(0, 1 << 62)), nout=int(rng.integers(0, 50)),
+                         onehot=kind != "rejection" or a % 3 == 0))
+    return reqs
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_verify_mixed_requests_match_oracle(ge, gpu, seed):
+    """Strict (rejection), exact-acceptance and greedy requests in one call; random trees up to 8 nodes with nodes of
+    several kids, one-hot (deterministic) and sampled drafts, top-k / top-p / min-p, per-request nout."""
+    rng = np.random.default_rng(100 + seed)
+    v = 3000
+    reqs = _random_trees(ge, rng, 24, v, ["rejection", "exact", "rejection", "greedy"])
+    calls = []
+    for r in reqs:
+        d = dict(target=r["target"], tokens=r["tokens"], parents=r["parents"], params=r["params"], seed=r["seed"],
+                 nout=r["nout"])
+        if not r["onehot"]:
+            d["q"] = _q_of_draft(r["draft"], r["parents"])
+        calls.append(d)
+    got = ge.spec.verify_tree(calls)
+    for a, r in enumerate(reqs):
+        want = spo.verify_tree(r["target"], None if r["onehot"] else _q_of_draft(r["draft"], r["parents"]),
+                               r["tokens"], r["parents"], r["params"], r["seed"], r["nout"])
+        assert got[a] == want, (a, r["params"], got[a], want)
+
+
+def test_verify_masks_history_and_stop(ge, gpu):
+    """Per-node grammar masks and penalty histories (the state once the path to the node is accepted), and a stop
+    predicate applied after each emitted token."""
+    rng = np.random.default_rng(7)
+    v = 2000
+    P = ge.sampling.SamplingParams
+    reqs = []
+    for a in range(12):
+        n = 6
+        parents = [0, 1, 2, 0, 4, 5][:n]
+        target = rng.normal(0, 2, size=(n + 1, v)).astype(np.float32)
+        masks = [rng.random(v) < 0.4 for _ in range(n + 1)]
+        hist = [rng.integers(0, v, size=20) for _ in range(n + 1)]
+        # drafted tokens allowed by their parent's mask (what a grammar-constrained drafter proposes)
+        toks = [int(np.nonzero(masks[par])[0][int(rng.integers(0, 5))]) for par in parents]
+        p = P(temperature=1.1, top_p=0.9, repetition_penalty=1.2, frequency_penalty=0.3,
+              accept="rejection" if a % 2 else "exact")
+        reqs.append(dict(target=target, tokens=toks, parents=parents, params=p, seed=1000 + a, masks=masks,
+                         history=hist))
+    stop = lambda a, emitted: "stop" if (a % 3 == 0 and len(emitted) == 2) else None
+    got = ge.spec.verify_tree(reqs, nout0=4, stop=stop)
+    for a, r in enumerate(reqs):
+        want = spo.verify_tree(r["target"], None, r["tokens"], r["parents"], r["params"], r["seed"], 4,
+                               masks=r["masks"], stop=lambda e, a=a: stop(a, e), history=r["history"])
+        assert got[a] == want, (a, got[a], want)
+        for d, t in enumerate(got[a][0]):
+            assert r["masks"][got[a][1][d]][t]
+
+
+def test_verify_prob_rows_and_bad_rows(ge, gpu):
+    """q given as fp64 probability rows (the reference's Tree.q layout), and a node whose target row holds a NaN: the
+    walk ends there as an error without emitting it (engine.py:286-288)."""
+    rng = np.random.default_rng(9)
+    v = 1500
+    P = ge.sampling.SamplingParams
+    parents = [0, 1, 2]
+    reqs = []
+    for a in range(6):
+        target = rng.normal(0, 1, size=(4, v)).astype(np.float32)
+        qd = {u: rng.dirichlet(np.ones(v) * 0.5) for u in range(3)}
+        toks = [int(np.argmax(qd[par])) for par in parents]
+        if a == 2:
+            target[1, 5] = np.nan
+        reqs.append(dict(target=target, tokens=toks, parents=parents, params=P(temperature=1.0, accept="rejection"),
+                         seed=77 + a, q=[qd[par] for par in parents]))
+    got = ge.spec.verify_tree(reqs)
+    for a, r in enumerate(reqs):
+        if a == 2 and got[a][2] == "error":
+            assert got[a][1][-1] == 1 or got[a][1] == [0]
+            continue
+        want = spo.verify_tree(r["target"], r["q"], r["tokens"], r["parents"], r["params"], r["seed"])
+        assert got[a] == want, (a, got[a], want)
+
+
+@pytest.mark.parametrize("t", [0.0, 0.7, 1.0, 1.6])
+def test_draft_pick_matches_oracle(ge, gpu, t):
+    """spec.py:151-159 for a batch of nodes: t == 0 the n best (stable descending), t > 0 n draws with the SALT_DRAFT
+    streams and their log q."""
+    rng = np.random.default_rng(int(t * 10) + 3)
+    rows, v = 20, 50000
+    x = rng.normal(0, 2, size=(rows, v)).astype(np.float32)
+    x[3, 100:110] = x[3].max() + 1.0       # ties at the top
+    n = [int(k) for k in rng.integers(1, 9, size=rows)]
+    seeds = [int(s) for s in rng.integers(0, 1 << 62, size=rows)]
+    ats = [int(s) for s in rng.integers(0, 4000, size=rows)]
+    toks, vals = ge.spec.pick_batch(torch.from_numpy(x).to(gpu), n, t, seeds, ats)
+    toks, vals = toks.cpu().numpy(), vals.cpu().numpy()
+    for r in range(rows):
+        want = spo.pick(x[r].astype(np.float64), n[r], t, seeds[r], ats[r])
+        assert list(toks[r, :n[r]]) == [w[0] for w in want], r
+        np.testing.assert_allclose(vals[r, :n[r]], [w[2] for w in want], rtol=1e-12, atol=1e-12)
+
+
+class _LM:
+    """A tiny next-token model for the drafter: log-probabilities of a hashed row (device tensor)."""
+
+    def __init__(self, v, dev):
+        self.v, self.dev = v, dev
+
+    def dist(self, s, path):
+        h = 3
+        for t in list(s.tokens) + list(path):
+            h = ora.mix(h, t + 1)
+        u = ora.uniform_np(h, np.arange(self.v, dtype=np.uint64))
+        z = (4.0 * u).astype(np.float32)
+        return torch.from_numpy(z - np.float32(np.log(np.exp(z.astype(np.float64)).sum()))).to(self.dev)
+
+
+@pytest.mark.parametrize("shape,t", [("chain", 0.0), ("chain", 1.0), ("dynamic", 0.0), ("dynamic", 1.0)])
+def test_tree_drafter_matches_oracle(ge, gpu, shape, t):
+    from types import SimpleNamespace as NS
+    v = 4000
+    m = _LM(v, gpu)
+    d = ge.spec.TreeDrafter(m, shape, topk=3, depth=3, temperature=t)
+    s = NS(tokens=[5, 9, 2], seed=4242)
+    toks, par, q = d.grow(s, 6)
+    if shape == "chain":
+        want_t, want_q = [], []
+        for k in range(6):
+            x, qq, _ = spo.pick(m.dist(s, want_t).cpu().numpy().astype(np.float64), 1, t, s.seed, 3 + k)[0]
+            want_t.append(x)
+        assert toks == want_t and par == list(range(6))
+    else:
+        wt, wp, _ = spo.grow_dynamic(lambda pt: m.dist(s, pt).cpu().numpy().astype(np.float64), s.seed, 3, 6, 3, 3, t)
+        assert (toks, par) == (wt, wp)
+    assert (q is None) == (t == 0)

@@ -289,7 +289,7 @@ def test_verify_tree_walk_follows_accepted_kids(seed):
             qrows[u] = np.exp(z - z.max()) / np.exp(z - z.max()).sum()
             for k, c in enumerate(kids[u]):
                 toks[c - 1] = int(rng.choice(v, p=qrows[u]))
-    out, path = spo.verify_tree(tgt, qrows, toks, parents, P(temperature=1.0), 1234 + seed)
+    out, path, _ = spo.verify_tree(tgt, qrows, toks, parents, P(temperature=1.0, accept="rejection"), 1234 + seed)
     assert len(out) == len(path)
     for d in range(1, len(path)):
         assert toks[path[d] - 1] == out[d - 1] and parents[path[d] - 1] == path[d - 1]
