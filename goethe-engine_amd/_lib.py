@@ -20,6 +20,7 @@ ROW_MSS = 2
 Q_PROB, Q_LOGITS_F32, Q_LOGITS_BF16 = 0, 1, 2
 WALK_OK, WALK_ERROR, WALK_TRUNCATED = 0, 1, 2
 MAX_KIDS = 16
+NOALLOC_ROWS, NOALLOC_VOCAB = 32, 163840
 BATCH_EXACT = 1
 BATCH_PROFILE = 2
 BATCH_NO_PLAN_WAIT = 4
@@ -94,6 +95,7 @@ SIGNATURES = dict(
     gse_draw=(C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p,
                         C.c_void_p]),
     gse_mss=(C.c_int, [C.c_void_p, P_(MssBatch)]),
+    gse_sample_noalloc=(C.c_int, [P_(Batch), P_(Out)]),
     gse_verify_tree=(C.c_int, [C.c_void_p, P_(Batch), P_(Tree), P_(TreeOut)]),
     gse_draft_pick=(C.c_int, [C.c_void_p, P_(PickBatch)]),
     gse_pack_mask=(C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_uint32, C.c_uint32, C.c_void_p, C.c_int64,

@@ -3,6 +3,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -15,6 +16,8 @@ struct gse_handle {
   uint32_t max_rows = 0, max_vocab = 0, nchmax = 0;
   uint32_t nrec = 0;     // part records (and wave lists) in the workspace
   uint32_t target = 0;   // main-pass workgroups to aim for (4 per CU: all resident at once)
+  bool owned = false;    // the workspace block came from hipMalloc (gse_open), not the static array
+  void *block = nullptr; // the workspace (gse::plan_layout)
   gse::SliceRec *rec = nullptr;
   uint64_t *cand = nullptr;
   gse::RowInfo *info = nullptr;
@@ -47,7 +50,7 @@ struct gse_handle {
 
 namespace {
 
-thread_local std::string g_open_err;
+thread_local char g_open_err[512];  // errors of calls without a handle (gse_open, gse_sample_noalloc)
 
 int fail(gse_handle *h, int rc, const char *fmt, ...) __attribute__((format(printf, 3, 4)));
 int fail(gse_handle *h, int rc, const char *fmt, ...) {
@@ -57,7 +60,7 @@ int fail(gse_handle *h, int rc, const char *fmt, ...) {
   vsnprintf(buf, sizeof buf, fmt, ap);
   va_end(ap);
   if (h) h->err = buf;
-  else g_open_err = buf;
+  else memcpy(g_open_err, buf, sizeof buf);
   return rc;
 }
 
@@ -175,24 +178,116 @@ gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   return a;
 }
 
-template <typename T>
-hipError_t zalloc(T **p, size_t n) {
-  hipError_t e = hipMalloc(p, n * sizeof(T));
-  return e == hipSuccess ? hipMemset(*p, 0, n * sizeof(T)) : e;
+// Points the handle's buffers into a workspace block laid out by gse::plan_layout.
+void carve(gse_handle *h, void *block, const gse::Layout &L, bool tree) {
+  char *b = (char *)block;
+  h->block = block;
+  h->nrec = L.nrec;
+  h->nsl = L.nsl;
+  h->dz_ld = L.dz_ld;
+  h->rec = (gse::SliceRec *)(b + L.rec);
+  h->cand = (uint64_t *)(b + L.cand);
+  h->info = (gse::RowInfo *)(b + L.info);
+  h->done = (uint32_t *)(b + L.done);
+  h->dctl = (uint32_t *)(b + L.dctl);
+  h->dslot = (gse::DeepSlot *)(b + L.dslot);
+  h->dhist = (uint64_t *)(b + L.dhist);
+  h->dlist = (uint64_t *)(b + L.dlist);
+  h->dz = (float *)(b + L.dz);
+  if (!tree) return;
+  h->ttok = (int32_t *)(b + L.ttok);
+  h->tstate = (gse::TreeNode *)(b + L.tstate);
+  h->npart = (gse::Fx *)(b + L.npart);
+  h->nlast = (int32_t *)(b + L.nlast);
+  h->qmax = (double *)(b + L.qmax);
+  h->qpart = (gse::Fx *)(b + L.qpart);
+  h->qfin = (gse::QFin *)(b + L.qfin);
+  h->pmax = (double *)(b + L.pmax);
+  h->ppart = (gse::Fx *)(b + L.ppart);
+  h->plast = (int32_t *)(b + L.plast);
+  h->ptop = (uint64_t *)(b + L.ptop);
+  h->ptick = (uint32_t *)(b + L.ptick);
 }
 
-// Workspace of verify rounds and drafter picks, sized for max_rows x max_vocab.
-hipError_t alloc_tree(gse_handle *h) {
-  const size_t R = h->max_rows, L = h->nsl, K = GSE_MAX_KIDS + 1;
+
+// ---- the static workspace of gse_sample_noalloc --------------------------------------------------------------------
+// One per GPU: a file-scope device array (each device holds its own copy from the library's load until the process
+// ends), laid out like a handle's workspace for NOALLOC_ROWS x NOALLOC_VOCAB. Host code never uses the array's name as
+// an address: hipGetSymbolAddress gives each device's address once, at that device's first call, and the handle of
+// that device keeps it.
+constexpr uint32_t NOALLOC_TARGET = 1024;  // main-pass workgroups aimed for (4 per CU of a 256-CU device, at most)
+constexpr gse::Layout NOALLOC_LAYOUT = gse::plan_layout(gse::NOALLOC_ROWS, gse::NOALLOC_VOCAB, NOALLOC_TARGET, false);
+static __device__ __align__(256) uint8_t scratch[NOALLOC_LAYOUT.total];
+
+constexpr int NOALLOC_DEVICES = 64;
+std::mutex g_static_mu;
+gse_handle g_static[NOALLOC_DEVICES];
+bool g_static_ready[NOALLOC_DEVICES];
+
+// The handle of the current device over its static workspace; the first call on a device finds the array's address
+// there, checks the device, and clears the workspace with a fill kernel on stream s (ordered before the call's own
+// kernels).
+int static_handle(gse_handle **out, hipStream_t s) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(nullptr, GSE_E_DEVICE, "no HIP device: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= NOALLOC_DEVICES) return fail(nullptr, GSE_E_DEVICE, "device %d: at most %d", dev, NOALLOC_DEVICES);
+  std::lock_guard<std::mutex> lk(g_static_mu);
+  gse_handle *h = &g_static[dev];
+  if (!g_static_ready[dev]) {
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop, dev)) != hipSuccess)
+      return fail(nullptr, GSE_E_DEVICE, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+      return fail(nullptr, GSE_E_DEVICE, "device %d is %s; this library is built for gfx950", dev, prop.gcnArchName);
+    void *ptr = nullptr;
+    if ((e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch))) != hipSuccess || !ptr)
+      return fail(nullptr, GSE_E_DEVICE, "static workspace address: %s", hipGetErrorString(e));
+    if ((e = gse::launch_zero(ptr, NOALLOC_LAYOUT.total, s)) != hipSuccess)
+      return fail(nullptr, GSE_E_DEVICE, "static workspace clear: %s", hipGetErrorString(e));
+    h->device = dev;
+    h->max_rows = gse::NOALLOC_ROWS;
+    h->max_vocab = gse::NOALLOC_VOCAB;
+    h->nchmax = (gse::NOALLOC_VOCAB + gse::CH - 1) / gse::CH;
+    const uint32_t t = 4u * (uint32_t)(prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256);
+    h->target = t < NOALLOC_TARGET ? t : NOALLOC_TARGET;
+    carve(h, ptr, NOALLOC_LAYOUT, false);
+    g_static_ready[dev] = true;
+  }
+  *out = h;
+  return GSE_OK;
+}
+
+// gse_sample's checks and launches on a handle (its own workspace, or the static one of gse_sample_noalloc).
+int sample_impl(gse_handle *h, const gse_batch &b, const gse_out &o) {
+  int rc = check_batch(h, b);
+  if (rc) return rc;
+  if (!o.tokens) return fail(h, GSE_E_ARG, "tokens output is required");
+  if ((o.logprob_ids == nullptr) != (o.logprobs == nullptr))
+    return fail(h, GSE_E_ARG, "logprob_ids and logprobs go together");
+  if (o.logprob_ids && o.logprobs_ld < GSE_MAX_LOGPROBS && o.logprobs_ld <= 0)
+    return fail(h, GSE_E_ARG, "logprobs_ld must be > 0");
+  if (o.processed && o.processed_ld < (int64_t)b.vocab) return fail(h, GSE_E_ARG, "processed_ld < vocab");
+  if (b.rows == 0) return GSE_OK;
+  gse::ScanArgs a = make_args(h, b, gse::MODE_SAMPLE);
+  a.processed = o.processed;
+  a.processed_ld = o.processed_ld;
+  a.tokens = o.tokens;
+  a.lp_ids = o.logprob_ids;
+  a.lps = o.logprobs;
+  a.lp_ld = o.logprobs_ld;
+  hipStream_t s = (hipStream_t)b.stream;
+  hipEvent_t *ev = nullptr;
+  if ((b.flags & GSE_BATCH_PROFILE) && (rc = prof_slot(h, 3, &ev)) != GSE_OK) return rc;
   hipError_t e;
-  if ((e = zalloc(&h->ttok, R)) != hipSuccess || (e = zalloc(&h->tstate, R)) != hipSuccess ||
-      (e = zalloc(&h->npart, R * K * L)) != hipSuccess || (e = zalloc(&h->nlast, R * K * L)) != hipSuccess ||
-      (e = zalloc(&h->qmax, R * L)) != hipSuccess || (e = zalloc(&h->qpart, R * L)) != hipSuccess ||
-      (e = zalloc(&h->qfin, R)) != hipSuccess || (e = zalloc(&h->pmax, R * L)) != hipSuccess ||
-      (e = zalloc(&h->ppart, R * L)) != hipSuccess || (e = zalloc(&h->plast, R * L)) != hipSuccess ||
-      (e = zalloc(&h->ptop, R * L * 4 * GSE_MAX_KIDS)) != hipSuccess || (e = zalloc(&h->ptick, R)) != hipSuccess)
-    return e;
-  return hipSuccess;
+  if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(h, e, "event record");
+  if ((e = gse::launch_main(a, s)) != hipSuccess) return hip_fail(h, e, "main launch");
+  if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return hip_fail(h, e, "event record");
+  if (a.dgrid > 0 && (e = gse::launch_deep(a, s)) != hipSuccess) return hip_fail(h, e, "deep launch");
+  if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return hip_fail(h, e, "event record");
+  if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
+  if (ev && (e = hipEventRecord(ev[3], s)) != hipSuccess) return hip_fail(h, e, "event record");
+  return GSE_OK;
 }
 
 }  // namespace
@@ -224,29 +319,17 @@ GSE_API int gse_open(const gse_open_params *p, gse_handle **out) {
   h->max_vocab = o.max_vocab;
   h->nchmax = (o.max_vocab + gse::CH - 1) / gse::CH;
   h->target = 4u * (uint32_t)(prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256);
-  h->nrec = h->max_rows * ((o.max_vocab + gse::PTOK - 1) / gse::PTOK + 1) + h->target;
-  h->dz_ld = ((int64_t)o.max_vocab + 63) / 64 * 64;
-  h->nsl = (o.max_vocab + gse::CH - 1) / gse::CH;
-  const size_t dzn = (size_t)(h->max_rows < (uint32_t)gse::DEEP_MAX ? h->max_rows : (uint32_t)gse::DEEP_MAX) * h->dz_ld;
-  if ((e = hipMalloc(&h->rec, (size_t)h->nrec * sizeof(gse::SliceRec))) != hipSuccess ||
-      (e = hipMalloc(&h->cand, (size_t)h->nrec * gse::PWAVES * gse::CAPW * sizeof(uint64_t))) != hipSuccess ||
-      (e = hipMalloc(&h->info, (size_t)h->max_rows * sizeof(gse::RowInfo))) != hipSuccess ||
-      (e = hipMalloc(&h->done, (size_t)h->max_rows * sizeof(uint32_t))) != hipSuccess ||
-      (e = hipMemset(h->done, 0, (size_t)h->max_rows * sizeof(uint32_t))) != hipSuccess ||
-      (e = hipMemset(h->info, 0, (size_t)h->max_rows * sizeof(gse::RowInfo))) != hipSuccess ||
-      (e = hipMalloc(&h->dctl, 64)) != hipSuccess || (e = hipMemset(h->dctl, 0, 64)) != hipSuccess ||
-      (e = hipMalloc(&h->dslot, gse::DEEP_MAX * sizeof(gse::DeepSlot))) != hipSuccess ||
-      (e = hipMemset(h->dslot, 0, gse::DEEP_MAX * sizeof(gse::DeepSlot))) != hipSuccess ||
-      (e = hipMalloc(&h->dhist, (size_t)gse::DEEP_MAX * 3 * gse::DNB * sizeof(uint64_t))) != hipSuccess ||
-      (e = hipMemset(h->dhist, 0, (size_t)gse::DEEP_MAX * 3 * gse::DNB * sizeof(uint64_t))) != hipSuccess ||
-      (e = hipMalloc(&h->dlist, (size_t)gse::DEEP_MAX * gse::DCAP * sizeof(uint64_t))) != hipSuccess ||
-      (e = hipMalloc(&h->dz, dzn * sizeof(float))) != hipSuccess ||
-      (e = alloc_tree(h)) != hipSuccess ||
+  const gse::Layout L = gse::plan_layout(h->max_rows, h->max_vocab, h->target, true);
+  void *block = nullptr;
+  if ((e = hipMalloc(&block, L.total)) != hipSuccess || (e = hipMemset(block, 0, L.total)) != hipSuccess ||
       (e = hipDeviceSynchronize()) != hipSuccess) {
-    fail(nullptr, GSE_E_DEVICE, "workspace allocation (%u part records): %s", h->nrec, hipGetErrorString(e));
-    gse_close(h);
+    if (block) (void)hipFree(block);
+    fail(nullptr, GSE_E_DEVICE, "workspace allocation (%zu bytes): %s", L.total, hipGetErrorString(e));
+    delete h;
     return GSE_E_DEVICE;
   }
+  h->owned = true;
+  carve(h, block, L, true);
   *out = h;
   return GSE_OK;
 }
@@ -256,35 +339,24 @@ GSE_API int gse_sample(gse_handle *h, const gse_batch *in, const gse_out *out) {
   gse_batch b;
   gse_out o;
   if (!take(in, b) || !take(out, o)) return fail(h, GSE_E_ARG, "null or short gse_batch / gse_out");
-  int rc = check_batch(h, b);
-  if (rc) return rc;
-  if (!o.tokens) return fail(h, GSE_E_ARG, "tokens output is required");
-  if ((o.logprob_ids == nullptr) != (o.logprobs == nullptr))
-    return fail(h, GSE_E_ARG, "logprob_ids and logprobs go together");
-  if (o.logprob_ids && o.logprobs_ld < GSE_MAX_LOGPROBS && o.logprobs_ld <= 0)
-    return fail(h, GSE_E_ARG, "logprobs_ld must be > 0");
-  if (o.processed && o.processed_ld < (int64_t)b.vocab) return fail(h, GSE_E_ARG, "processed_ld < vocab");
-  if (b.rows == 0) return GSE_OK;
   DeviceGuard g(h->device);
-  gse::ScanArgs a = make_args(h, b, gse::MODE_SAMPLE);
-  a.processed = o.processed;
-  a.processed_ld = o.processed_ld;
-  a.tokens = o.tokens;
-  a.lp_ids = o.logprob_ids;
-  a.lps = o.logprobs;
-  a.lp_ld = o.logprobs_ld;
-  hipStream_t s = (hipStream_t)b.stream;
-  hipEvent_t *ev = nullptr;
-  if ((b.flags & GSE_BATCH_PROFILE) && (rc = prof_slot(h, 3, &ev)) != GSE_OK) return rc;
-  hipError_t e;
-  if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(h, e, "event record");
-  if ((e = gse::launch_main(a, s)) != hipSuccess) return hip_fail(h, e, "main launch");
-  if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return hip_fail(h, e, "event record");
-  if (a.dgrid > 0 && (e = gse::launch_deep(a, s)) != hipSuccess) return hip_fail(h, e, "deep launch");
-  if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return hip_fail(h, e, "event record");
-  if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
-  if (ev && (e = hipEventRecord(ev[3], s)) != hipSuccess) return hip_fail(h, e, "event record");
-  return GSE_OK;
+  return sample_impl(h, b, o);
+}
+
+GSE_API int gse_sample_noalloc(const gse_batch *in, const gse_out *out) {
+  gse_batch b;
+  gse_out o;
+  if (!take(in, b) || !take(out, o)) return fail(nullptr, GSE_E_ARG, "null or short gse_batch / gse_out");
+  if (b.rows > gse::NOALLOC_ROWS || b.vocab > gse::NOALLOC_VOCAB)
+    return fail(nullptr, GSE_E_CAPACITY,
+                "gse_sample_noalloc: %u rows of %u tokens; its static workspace holds at most %u rows of at most %u "
+                "tokens (use gse_open / gse_sample for more)", b.rows, b.vocab, gse::NOALLOC_ROWS, gse::NOALLOC_VOCAB);
+  gse_handle *h = nullptr;
+  int rc = static_handle(&h, (hipStream_t)b.stream);
+  if (rc) return rc;
+  rc = sample_impl(h, b, o);
+  if (rc) fail(nullptr, rc, "%s", h->err.c_str());
+  return rc;
 }
 
 GSE_API int gse_dist(gse_handle *h, const gse_batch *in, double *probs, int64_t probs_ld) {
@@ -467,26 +539,14 @@ GSE_API int gse_row_paths(gse_handle *h, uint32_t rows, uint8_t *paths) {
   return GSE_OK;
 }
 
-GSE_API const char *gse_last_error(gse_handle *h) { return h ? h->err.c_str() : g_open_err.c_str(); }
+GSE_API const char *gse_last_error(gse_handle *h) { return h ? h->err.c_str() : g_open_err; }
 
 GSE_API void gse_close(gse_handle *h) {
   if (!h) return;
   {
     DeviceGuard g(h->device);
     (void)hipDeviceSynchronize();
-    if (h->rec) (void)hipFree(h->rec);
-    if (h->cand) (void)hipFree(h->cand);
-    if (h->info) (void)hipFree(h->info);
-    if (h->done) (void)hipFree(h->done);
-    if (h->dctl) (void)hipFree(h->dctl);
-    if (h->dslot) (void)hipFree(h->dslot);
-    if (h->dhist) (void)hipFree(h->dhist);
-    if (h->dlist) (void)hipFree(h->dlist);
-    if (h->dz) (void)hipFree(h->dz);
-    void *tree_bufs[] = {h->ttok, h->tstate, h->npart, h->nlast, h->qmax, h->qpart, h->qfin,
-                         h->pmax, h->ppart, h->plast, h->ptop, h->ptick};
-    for (void *p : tree_bufs)
-      if (p) (void)hipFree(p);
+    if (h->owned && h->block) (void)hipFree(h->block);
     if (h->ring) {
       for (int c = 0; c < GSE_PROFILE_CALLS; ++c)
         for (int i = 0; i < 5; ++i)

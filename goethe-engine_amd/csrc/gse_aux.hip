@@ -179,7 +179,19 @@ __global__ __launch_bounds__(AT) void pack_kernel(const uint8_t *bools, int64_t 
   words[(int64_t)row * wld + w] = (int32_t)v;
 }
 
+// ---- zero fill (a kernel, not hipMemsetAsync, so that a caller may capture it in a graph) ----------------------------
+__global__ __launch_bounds__(AT) void zero_kernel(uint4 *p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * AT + threadIdx.x; i < n; i += (size_t)gridDim.x * AT) p[i] = make_uint4(0, 0, 0, 0);
+}
+
 }  // namespace
+
+hipError_t launch_zero(void *p, size_t bytes, hipStream_t s) {
+  const size_t n = bytes / sizeof(uint4);  // (bytes: a multiple of 256)
+  const unsigned g = (unsigned)(n / AT < 4096 ? (n + AT - 1) / AT : 4096);
+  if (n) hipLaunchKernelGGL(zero_kernel, dim3(g > 0 ? g : 1), dim3(AT), 0, s, (uint4 *)p, n);
+  return hipGetLastError();
+}
 
 hipError_t launch_dist_write(const ScanArgs &a, double *probs, int64_t probs_ld, hipStream_t s) {
   hipLaunchKernelGGL(dist_kernel, dim3(a.nch, a.rows), dim3(AT), 0, s, a, probs, probs_ld);

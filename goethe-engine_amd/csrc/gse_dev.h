@@ -9,7 +9,6 @@
 namespace gse {
 
 constexpr int WAVE = 64;
-constexpr int CH = 8192;  // tokens per slice (one main-pass workgroup; the exact path walks rows in the same chunks)
 
 // Order-preserving 32-bit keys of fp32 values: larger value -> larger key; -0 and +0 share a key (numpy's stable
 // argsort sees them as equal); NaN -> 0, below every other key (numpy sorts NaN of -z last).

@@ -37,6 +37,12 @@ enum : uint32_t {
 
 enum { MODE_SAMPLE = 0, MODE_DIST = 1 };
 
+constexpr int CH = 8192;
+// gse_sample_noalloc's static workspace: batches of at most this many rows of at most this many tokens.
+constexpr uint32_t NOALLOC_ROWS = 32;
+constexpr uint32_t NOALLOC_VOCAB = 163840;
+static_assert(NOALLOC_ROWS == GSE_NOALLOC_ROWS && NOALLOC_VOCAB == GSE_NOALLOC_VOCAB, "gse.h states the limits");  // tokens per slice (the exact path, dist, and the verify and pick passes walk rows in these)
+
 constexpr int CAPW = 512;   // candidates listed per wave per part
 constexpr int PWAVES = 4;   // waves per part workgroup
 constexpr int MAXP = 64;    // parts per row
@@ -174,6 +180,59 @@ struct PickLaunch {
   uint32_t *tick;
 };
 
+// Byte layout of a device workspace for max_rows x max_vocab; target: main-pass workgroups to aim for (4 per CU).
+// Every buffer starts on a 256-byte boundary; the whole block starts zeroed (the kernels keep their tickets, slot
+// counters and flags zero between calls). tree: with the buffers of verify rounds and drafter picks.
+struct Layout {
+  size_t rec, cand, info, done, dctl, dslot, dhist, dlist, dz;
+  size_t ttok, tstate, npart, nlast, qmax, qpart, qfin, pmax, ppart, plast, ptop, ptick;
+  size_t total;
+  uint32_t nrec, nsl, slots;
+  int64_t dz_ld;
+};
+
+constexpr size_t al256(size_t x) { return (x + 255) / 256 * 256; }
+
+constexpr Layout plan_layout(uint32_t R, uint32_t V, uint32_t target, bool tree) {
+  Layout L = {};
+  L.nrec = R * ((V + PTOK - 1) / PTOK + 1) + target;
+  L.nsl = (V + CH - 1) / CH;
+  L.slots = R < (uint32_t)DEEP_MAX ? R : (uint32_t)DEEP_MAX;
+  L.dz_ld = ((int64_t)V + 63) / 64 * 64;
+  size_t o = 0;
+  auto put = [&o](size_t bytes) {
+    const size_t at = o;
+    o += al256(bytes);
+    return at;
+  };
+  L.rec = put((size_t)L.nrec * sizeof(SliceRec));
+  L.cand = put((size_t)L.nrec * PWAVES * CAPW * sizeof(uint64_t));
+  L.info = put((size_t)R * sizeof(RowInfo));
+  L.done = put((size_t)R * sizeof(uint32_t));
+  L.dctl = put(64);
+  L.dslot = put((size_t)L.slots * sizeof(DeepSlot));
+  L.dhist = put((size_t)L.slots * 3 * DNB * sizeof(uint64_t));
+  L.dlist = put((size_t)L.slots * DCAP * sizeof(uint64_t));
+  L.dz = put((size_t)L.slots * (size_t)L.dz_ld * sizeof(float));
+  if (tree) {
+    const size_t K = GSE_MAX_KIDS + 1, S = L.nsl;
+    L.ttok = put((size_t)R * sizeof(int32_t));
+    L.tstate = put((size_t)R * sizeof(TreeNode));
+    L.npart = put((size_t)R * K * S * sizeof(Fx));
+    L.nlast = put((size_t)R * K * S * sizeof(int32_t));
+    L.qmax = put((size_t)R * S * sizeof(double));
+    L.qpart = put((size_t)R * S * sizeof(Fx));
+    L.qfin = put((size_t)R * sizeof(QFin));
+    L.pmax = put((size_t)R * S * sizeof(double));
+    L.ppart = put((size_t)R * S * sizeof(Fx));
+    L.plast = put((size_t)R * S * sizeof(int32_t));
+    L.ptop = put((size_t)R * S * 4 * GSE_MAX_KIDS * sizeof(uint64_t));
+    L.ptick = put((size_t)R * sizeof(uint32_t));
+  }
+  L.total = o;
+  return L;
+}
+
 hipError_t launch_main(const ScanArgs &a, hipStream_t s);
 hipError_t launch_deep(const ScanArgs &a, hipStream_t s);
 hipError_t launch_exact(const ScanArgs &a, hipStream_t s);
@@ -182,6 +241,7 @@ hipError_t launch_draw(const double *q, int64_t ld, int rows, int V, const doubl
 hipError_t launch_mss(const gse_mss_batch &b, hipStream_t s);
 hipError_t launch_tree(const TreeLaunch &L, hipStream_t s);
 hipError_t launch_pick(const PickLaunch &L, hipStream_t s);
+hipError_t launch_zero(void *p, size_t bytes, hipStream_t s);
 hipError_t launch_pack(const uint8_t *bools, int64_t bld, int rows, int V, int32_t *words, int64_t wld, hipStream_t s);
 
 }  // namespace gse

@@ -222,6 +222,17 @@ GSE_API int gse_open(const gse_open_params *p, gse_handle **out);
  * sampling.py:80-83 over the stable descending order. */
 GSE_API int gse_sample(gse_handle *h, const gse_batch *in, const gse_out *out);
 
+/* No counterpart in the reference. gse_sample for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): no handle, and no hipMalloc / hipFree / allocating
+ * library call. Its workspace is a static device array of about 43 MB that each GPU holds from the library's load until
+ * the process ends, for batches of at most GSE_NOALLOC_ROWS rows of at most GSE_NOALLOC_VOCAB tokens (more:
+ * GSE_E_CAPACITY). It runs on the current HIP device; the first call on a device sets that device's workspace up and
+ * should not be captured. Every call on one GPU shares its workspace: calls that overlap on one GPU (two streams, two
+ * threads) race. Errors: gse_last_error(NULL). Results are gse_sample's. */
+#define GSE_NOALLOC_ROWS 32
+#define GSE_NOALLOC_VOCAB 163840
+GSE_API int gse_sample_noalloc(const gse_batch *in, const gse_out *out);
+
 /* Replaces: goethe_engine/sampling.py:88-97 dist(): fp64 probabilities over the vocabulary (vocabulary order) that
  * sample() draws a temperature > 0 row from, with top-k, top-p, min-p, penalties and mask; probs is [rows][probs_ld]. */
 GSE_API int gse_dist(gse_handle *h, const gse_batch *in, double *probs, int64_t probs_ld);
