@@ -26,8 +26,7 @@ struct gse_handle {
   gse::DeepSlot *dslot = nullptr;
   uint64_t *dhist = nullptr;
   uint64_t *dlist = nullptr;
-  float *dz = nullptr;
-  int64_t dz_ld = 0;
+  uint32_t dslots = 0;                // split-row slots
   // verify rounds and drafter picks (gse_tree.hip): per row slices of the vocabulary, nsl of them at most
   uint32_t nsl = 0;
   int32_t *ttok = nullptr;            // [max_rows] sampled tokens of the verify round's selection pass
@@ -140,7 +139,7 @@ void parts(const gse_handle *h, uint32_t rows, uint32_t vocab, int *nparts, int 
 
 // Workgroups of the split-row finish launches: one resident round (the kernels slice the deep rows to fit it).
 void deep_grid(const gse_handle *h, uint32_t rows, int *nsl, int *grid) {
-  const uint32_t slots = rows < (uint32_t)gse::DEEP_MAX ? rows : (uint32_t)gse::DEEP_MAX;
+  const uint32_t slots = rows < h->dslots ? rows : h->dslots;
   const uint32_t items = slots * (uint32_t)gse::DSMAX;
   *nsl = gse::DSMAX;
   *grid = (int)(items < h->target ? items : h->target);
@@ -172,8 +171,7 @@ gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   a.dslot = h->dslot;
   a.dhist = h->dhist;
   a.dlist = h->dlist;
-  a.dz = h->dz;
-  a.dz_ld = h->dz_ld;
+  a.dslots = (int)h->dslots;
   deep_grid(h, b.rows, &a.dslices, &a.dgrid);
   return a;
 }
@@ -184,7 +182,7 @@ void carve(gse_handle *h, void *block, const gse::Layout &L, bool tree) {
   h->block = block;
   h->nrec = L.nrec;
   h->nsl = L.nsl;
-  h->dz_ld = L.dz_ld;
+  h->dslots = L.slots;
   h->rec = (gse::SliceRec *)(b + L.rec);
   h->cand = (uint64_t *)(b + L.cand);
   h->info = (gse::RowInfo *)(b + L.info);
@@ -193,7 +191,6 @@ void carve(gse_handle *h, void *block, const gse::Layout &L, bool tree) {
   h->dslot = (gse::DeepSlot *)(b + L.dslot);
   h->dhist = (uint64_t *)(b + L.dhist);
   h->dlist = (uint64_t *)(b + L.dlist);
-  h->dz = (float *)(b + L.dz);
   if (!tree) return;
   h->ttok = (int32_t *)(b + L.ttok);
   h->tstate = (gse::TreeNode *)(b + L.tstate);

@@ -5,14 +5,15 @@
 // with integer atomics (the same sums in any order), and the last slice of a row to finish a phase (atomic ticket)
 // carries on with the row. Every workgroup runs all its count items before any pick item.
 //
-//   count:  each slice recomputes z exactly as the main pass does, keeps it (dz), and adds a 512-bin histogram of
+//   count:  each slice recomputes z exactly as the main pass does and adds a 512-bin histogram of
 //           d = z_max - z: counts and exact fixed-point masses (fp64 exp, whole multiples of 2^-40 and 2^-64; bins
 //           1/32 wide, the last one open-ended). d is monotone in z, so the bins follow the stable order and ties share
 //           a bin. The row's last slice plans: the bins that hold the last kept element (top-p, top-k and min-p cuts)
 //           and the bins that may hold the draw, whether they hold at most DCAP elements, and the exact masses of the
 //           regions before and between them; then it publishes the plan's status.
-//   pick:   each slice waits for its row's plan (a bounded wait: past the limit the slice spoils the row, which then
-//           takes the exact path), reads its z back and lists the window elements.
+//   pick:   each slice builds its history table, waits for its row's plan (a bounded wait: past the limit the slice
+//           spoils the row, which then takes the exact path), recomputes z and lists the window elements (no z is
+//           written between the passes).
 //           The row's last slice finishes: exact sub-bin counts and masses over the list locate the cut and the draw,
 //           only the sub-bins holding them are sorted, and their exact prefixes (one scan) give the last kept element,
 //           c_last and the token. A failed check leaves the row to the exact path (gse_exact.hip). It then clears the
@@ -65,11 +66,12 @@ __device__ __forceinline__ void atomic_add_ag(uint64_t *p, uint64_t v) {
 // double-buffered loop whose loads are the same for every chunk (a chunk past the end reads the row's first one), so
 // one chunk stays in flight while the wave works on another; the history ids and each wave's first chunks are loaded
 // before the history tables are built. A partial last chunk is taken by wave 0 afterwards, with bounds checks.
-// f(z, token, valid) is called for every element slot of each chunk by every lane of the wave (valid false past the
-// slice end), so f may use ballots. Ends with a barrier.
-template <int DT, bool AL, typename F>
+// pre() runs (every thread) once the history tables are built, before the first chunk is used. f(z, token, valid) is
+// called for every element slot of each chunk by every lane of the wave (valid false past the slice end), so f may use
+// ballots. Ends with a barrier.
+template <int DT, bool AL, typename Pre, typename F>
 __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c, int row, int p0, int p1,
-                                             DeepShared &sh, float *zrow, F f) {
+                                             DeepShared &sh, Pre pre, F f) {
   using L = Lay<DT>;
   const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
   const int nfull = (p1 - p0) / CHK;
@@ -89,6 +91,7 @@ __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c,
   if (tid == 0) sh.hover = 0;
   if (c.pen) build_history(c, a.hist, hid, p0, p1, sh.h, sh.wsum, sh.hover);
   else __syncthreads();
+  pre();
   Lane ln;
   ln.m = -INFINITY;
   ln.s = 0.0;
@@ -115,21 +118,6 @@ __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c,
 #pragma unroll
     for (int v = 0; v < L::NV; ++v) asm volatile("" : "+v"(mw[v]));
     (void)chunk_phase1<DT>(a, c, row, cb, p0, p1, x, mw, ln, sh.h);
-#pragma unroll
-    for (int v = 0; v < L::NV; ++v) {  // z into the row's buffer (four elements per store)
-#pragma unroll
-      for (int q = 0; q < L::VEC; q += 4) {
-        const int t = cb + v * L::STRIDE + lane * L::VEC + q;
-        const int i = v * L::VEC + q;
-        if (t + 4 <= p1) {
-          *reinterpret_cast<float4 *>(zrow + t) = make_float4(x[i], x[i + 1], x[i + 2], x[i + 3]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (t + e < p1) zrow[t + e] = x[i + e];
-        }
-      }
-    }
 #pragma unroll
     for (int v = 0; v < L::NV; ++v) {
 #pragma unroll
@@ -358,8 +346,7 @@ __device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slic
     sh.c.hi[b] = 0;
     sh.c.lo[b] = 0;
   }
-  stream_slice<DT, AL>(a, c, row, p0, p1, sh, a.dz + (size_t)slot * a.dz_ld,
-                       [&](float z, int, bool ok) __attribute__((always_inline)) {
+  stream_slice<DT, AL>(a, c, row, p0, p1, sh, [] {}, [&](float z, int, bool ok) __attribute__((always_inline)) {
     if (ok && z > -INFINITY) {
       const uint32_t b = dbin(z, M);
       const Fx f = fx_of(exp_nonpos((double)z - Md, etab));
@@ -746,76 +733,60 @@ union PickShared {
   FinShared f;
 };
 
+template <int DT, bool AL>
 __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice, const DGeom &g, PickShared &ps,
                                           const double *etab) {
   DeepShared &sh = ps.d;
   const int tid = threadIdx.x;
   DeepSlot *ds = a.dslot + slot;
+  const int row = ds->row;
+  const gse_row P = ds->P;
   const float Mf = ds->M;
+  const RowCtx c = make_ctx(a, row, P);
   const int p0 = slice * g.len, p1 = min(a.V, p0 + g.len);
-  // The slice's z, as the count item of this workgroup for the same slice wrote it: four vectors per thread, loaded
-  // unconditionally (a vector past the slice end reloads the slice's first one and is skipped; a vector that starts
-  // below p1 lies inside the row's buffer, whose length is a multiple of 64). The first round is loaded before the
-  // wait for the plan, so that it arrives while the wait lasts.
-  const float *zr = a.dz + (size_t)slot * a.dz_ld;
-  constexpr int PV = 4;
-  float4 v0[PV];
-#pragma unroll
-  for (int j = 0; j < PV; ++j) {
-    const int t = p0 + (j * MT + tid) * 4;
-    v0[j] = *reinterpret_cast<const float4 *>(zr + (t < p1 ? t : p0));
-  }
   __syncthreads();  // (LDS of the previous item)
-  if (tid == 0) {
-    sh.nwl = 0;
-    uint32_t st = ld_ag(&ds->status);
-    if (st == DS_PENDING) {
-      const uint64_t t0 = wall_clock64();
-      while ((st = ld_ag(&ds->status)) == DS_PENDING) {
-        // (every slice of the grid is resident at once and a plan takes microseconds: the limit, a.plan_wait, only
-        // ends the wait when the device could not hold the whole grid)
-        if (wall_clock64() - t0 >= a.plan_wait) {
-          (void)__hip_atomic_fetch_or(&ds->spoil, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          st = DS_FAIL;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(16);  // (about 1000 clocks between polls)
-      }
-    }
-    sh.pstat = st;
-  }
-  __syncthreads();
-  const bool planned = sh.pstat == DS_PLANNED;
-  if (planned) {
-    const uint32_t w2lo = ld_ag(&ds->w2lo), w2hi = ld_ag(&ds->w2hi), w1lo = ld_ag(&ds->w1lo), w1hi = ld_ag(&ds->w1hi);
-    auto elem = [&](float z, int t) __attribute__((always_inline)) {
-      if (z > -INFINITY) {
-        const uint32_t b = dbin(z, Mf);
-        if ((b >= w2lo && b <= w2hi) || (b >= w1lo && b <= w1hi)) {
-          const uint32_t pos = atomicAdd(&sh.nwl, 1u);
-          if (pos < (uint32_t)WLC) sh.wl[pos] = pack(fkey(z), (uint32_t)t);
+  bool planned = false;
+  uint32_t w2lo = 0, w2hi = 0, w1lo = 0, w1hi = 0;
+  // The wait for the plan comes after this slice's history tables are built and its first chunks are loading, so that
+  // both overlap it.
+  auto wait_plan = [&]() __attribute__((always_inline)) {
+    if (tid == 0) {
+      sh.nwl = 0;
+      uint32_t st = ld_ag(&ds->status);
+      if (st == DS_PENDING) {
+        const uint64_t t0 = wall_clock64();
+        while ((st = ld_ag(&ds->status)) == DS_PENDING) {
+          // (every slice of the grid is resident at once and a plan takes microseconds: the limit, a.plan_wait, only
+          // ends the wait when the device could not hold the whole grid)
+          if (wall_clock64() - t0 >= a.plan_wait) {
+            (void)__hip_atomic_fetch_or(&ds->spoil, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            st = DS_FAIL;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(16);  // (about 1000 clocks between polls)
         }
       }
-    };
-#pragma unroll 1
-    for (int t0 = p0; t0 < p1; t0 += PV * MT * 4) {
-      float4 v[PV];
-#pragma unroll
-      for (int j = 0; j < PV; ++j) {
-        const int t = t0 + (j * MT + tid) * 4;
-        v[j] = t0 == p0 ? v0[j] : *reinterpret_cast<const float4 *>(zr + (t < p1 ? t : p0));
-      }
-#pragma unroll
-      for (int j = 0; j < PV; ++j) {
-        const int t = t0 + (j * MT + tid) * 4;
-        const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          if (t + k < p1) elem(e[k], t + k);
+      sh.pstat = st;
+    }
+    __syncthreads();
+    planned = sh.pstat == DS_PLANNED;
+    if (planned) {
+      w2lo = ld_ag(&ds->w2lo);
+      w2hi = ld_ag(&ds->w2hi);
+      w1lo = ld_ag(&ds->w1lo);
+      w1hi = ld_ag(&ds->w1hi);
+    }
+  };
+  stream_slice<DT, AL>(a, c, row, p0, p1, sh, wait_plan, [&](float z, int t, bool ok) __attribute__((always_inline)) {
+    if (planned && ok && z > -INFINITY) {
+      const uint32_t b = dbin(z, Mf);
+      if ((b >= w2lo && b <= w2hi) || (b >= w1lo && b <= w1hi)) {
+        const uint32_t pos = atomicAdd(&sh.nwl, 1u);
+        if (pos < (uint32_t)WLC) sh.wl[pos] = pack(fkey(z), (uint32_t)t);
       }
     }
-    // the slice's window elements into the row list
-    __syncthreads();  // (sh.nwl)
+  });
+  if (planned) {  // the slice's window elements into the row list (stream_slice ends with a barrier: sh.nwl)
     const uint32_t nw = sh.nwl;
     if (tid == 0 && nw) {
       // a slice with more window elements than it can hold spoils the row's count (the row takes the exact path)
@@ -857,12 +828,12 @@ template <int DT, bool AL>
 __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void deep_kernel(ScanArgs a) {
   __shared__ PickShared sh;
   __shared__ double etab[64];
-  const int nd = (int)min(a.dctl[0], (uint32_t)DEEP_MAX);
+  const int nd = (int)min(a.dctl[0], (uint32_t)a.dslots);
   if (nd == 0) return;
   if (threadIdx.x < 64) etab[threadIdx.x] = EXP2_64[threadIdx.x];  // (published by the first barrier of an item)
   const DGeom g = deep_geom(a, nd);
   for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) count_item<DT, AL>(a, i / g.S, i % g.S, g, sh.d, etab);
-  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) pick_item(a, i / g.S, i % g.S, g, sh, etab);
+  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) pick_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab);
 }
 
 template <int DT, bool AL>

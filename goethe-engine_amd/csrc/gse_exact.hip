@@ -454,12 +454,9 @@ __device__ uint32_t collect_top(const XCtx &x, ExactShared &sh, uint64_t pk) {
   return n;
 }
 
-__global__ __launch_bounds__(XT) void exact_kernel(ScanArgs a) {
-  const int row = blockIdx.x;
+// Finishes one hard row (every thread of the workgroup calls it; its LDS is free again when it returns).
+__device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShared &sh) {
   RowInfo *ri = a.info + row;
-  if (row == 0 && threadIdx.x == 0) a.dctl[0] = 0u;  // the deep rows of this call are finished
-  if (!(ri->flags & R_HARD)) return;
-  __shared__ ExactShared sh;
   const int tid = threadIdx.x;
   const gse_row P = a.params[row];
   const bool greedy = is_greedy(a.mode, P);
@@ -611,10 +608,43 @@ __global__ __launch_bounds__(XT) void exact_kernel(ScanArgs a) {
   }
 }
 
+constexpr int XGRID = 64;  // workgroups of the exact pass (unless every row is forced through it)
+
+// The exact pass: with GSE_BATCH_EXACT one workgroup per row; otherwise a small grid, workgroup g owning the rows
+// r = g (mod grid): it finds its hard ones (those the main pass and the split-row finish left: one scan of their flags,
+// compacted in row order) and finishes them, so that a call with no hard row costs a launch and one round of loads.
+__global__ __launch_bounds__(XT) void exact_kernel(ScanArgs a) {
+  __shared__ ExactShared sh;
+  __shared__ uint32_t wn[XT / WAVE];
+  __shared__ int hrow[XT];
+  if (blockIdx.x == 0 && threadIdx.x == 0) a.dctl[0] = 0u;  // the deep rows of this call are finished
+  const int G = (int)gridDim.x, w = threadIdx.x / WAVE;
+  for (int j0 = 0; (int)blockIdx.x + j0 * G < a.rows; j0 += XT) {
+    const int r = (int)blockIdx.x + (j0 + (int)threadIdx.x) * G;
+    const bool hard = r < a.rows && (a.info[r].flags & R_HARD);
+    const uint64_t bl = ballot64(hard);
+    if (lane_id() == 0) wn[w] = (uint32_t)__popcll(bl);
+    __syncthreads();
+    uint32_t base = 0, n = 0;
+#pragma unroll
+    for (int k = 0; k < XT / WAVE; ++k) {
+      base += k < w ? wn[k] : 0u;
+      n += wn[k];
+    }
+    if (hard) hrow[base + lanes_below(bl)] = r;
+    __syncthreads();
+    for (uint32_t i = 0; i < n; ++i) {
+      exact_row(a, hrow[i], sh);
+      __syncthreads();  // (LDS of the row)
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_exact(const ScanArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL(exact_kernel, dim3(a.rows), dim3(XT), 0, s, a);
+  const int grid = a.force_exact ? a.rows : (a.rows < XGRID ? a.rows : XGRID);  // (forced: one row per workgroup)
+  hipLaunchKernelGGL(exact_kernel, dim3(grid), dim3(XT), 0, s, a);
   return hipGetLastError();
 }
 

@@ -65,7 +65,8 @@ struct SliceRec {    // 64 bytes
 static_assert(sizeof(SliceRec) == 64, "");
 
 // Split-row finish of deep rows (gse_deep.hip).
-constexpr int DEEP_MAX = 128;  // deep rows per call (more: the exact path takes them)
+constexpr int DEEP_MAX = 1024;  // split-row slots at most (a handle has min(max_rows, DEEP_MAX); more deep rows: the
+                                // exact path takes them)
 constexpr int DSMAX = 64;      // slices per deep row, at most
 constexpr int DNB = 512;       // histogram bins of d = z_max - z, 1/32 wide (the last one open-ended)
 constexpr int DCAP = 8192;     // window elements listed per deep row
@@ -134,8 +135,7 @@ struct ScanArgs {
   DeepSlot *dslot;   // [DEEP_MAX]
   uint64_t *dhist;   // [DEEP_MAX][3][DNB]: per bin, element count and exact mass (2^-40 and 2^-64 parts), atomic adds
   uint64_t *dlist;   // [DEEP_MAX][DCAP]: packed keys of the window elements
-  float *dz;         // [DEEP_MAX][dz_ld]: z of the deep rows, written by the count phase, read back by the pick phase
-  int64_t dz_ld;
+  int dslots;          // split-row slots of the workspace
   int dslices, dgrid;  // split-row finish enabled (slices per deep row, at most), workgroups per pass
   uint64_t plan_wait;  // wall-clock ticks (100 MHz) a split-row pick slice waits for its row's plan
   int tree;            // a verify round (gse_verify_tree): GSE_ROW_MSS rows need dist's keep boundary, not a token
@@ -184,11 +184,10 @@ struct PickLaunch {
 // Every buffer starts on a 256-byte boundary; the whole block starts zeroed (the kernels keep their tickets, slot
 // counters and flags zero between calls). tree: with the buffers of verify rounds and drafter picks.
 struct Layout {
-  size_t rec, cand, info, done, dctl, dslot, dhist, dlist, dz;
+  size_t rec, cand, info, done, dctl, dslot, dhist, dlist;
   size_t ttok, tstate, npart, nlast, qmax, qpart, qfin, pmax, ppart, plast, ptop, ptick;
   size_t total;
   uint32_t nrec, nsl, slots;
-  int64_t dz_ld;
 };
 
 constexpr size_t al256(size_t x) { return (x + 255) / 256 * 256; }
@@ -198,7 +197,6 @@ constexpr Layout plan_layout(uint32_t R, uint32_t V, uint32_t target, bool tree)
   L.nrec = R * ((V + PTOK - 1) / PTOK + 1) + target;
   L.nsl = (V + CH - 1) / CH;
   L.slots = R < (uint32_t)DEEP_MAX ? R : (uint32_t)DEEP_MAX;
-  L.dz_ld = ((int64_t)V + 63) / 64 * 64;
   size_t o = 0;
   auto put = [&o](size_t bytes) {
     const size_t at = o;
@@ -213,7 +211,6 @@ constexpr Layout plan_layout(uint32_t R, uint32_t V, uint32_t target, bool tree)
   L.dslot = put((size_t)L.slots * sizeof(DeepSlot));
   L.dhist = put((size_t)L.slots * 3 * DNB * sizeof(uint64_t));
   L.dlist = put((size_t)L.slots * DCAP * sizeof(uint64_t));
-  L.dz = put((size_t)L.slots * (size_t)L.dz_ld * sizeof(float));
   if (tree) {
     const size_t K = GSE_MAX_KIDS + 1, S = L.nsl;
     L.ttok = put((size_t)R * sizeof(int32_t));

@@ -64,9 +64,9 @@ struct Shared {
   uint64_t wtop[NWV];
   double wred[NWV], wred2[NWV];
   // resolve
-  uint32_t loff[NSL];
+  uint32_t loff[NSL];           // wave list lengths
   uint64_t rtop, rtopL;
-  uint32_t rflags, rkappa, rmkey, ltot, nh, mfail_sure, mfail_maybe, jcount, bmax, lpw;
+  uint32_t rflags, rkappa, rmkey, nh, mfail_sure, mfail_maybe, jcount, bmax, lpw;
   double rsc;
   double etab[64];             // 2^(j / 64) for exp_nonpos
 };
@@ -205,15 +205,15 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
     sh.jcount = 0;
   }
   // Exact masses e_r of the sorted ranks, then their inclusive prefixes I_r in place (in LDS). Wave w takes ranks
-  // [512 w, 512 w + 512), 64 consecutive ranks per step: conflict-free LDS accesses and wave scans (the additions are
-  // the same, in the same order, every time). A_r = I_{r-1} is the exclusive prefix.
+  // [RPW w, RPW w + RPW), 64 consecutive ranks per step: conflict-free LDS accesses and wave scans (the additions are
+  // the same, in the same order, for the same head). A_r = I_{r-1} is the exclusive prefix.
   double *ee = reinterpret_cast<double *>(sh.r.tmp);
   const double M = ev.M;
   const int lane = lane_id(), w = tid >> 6;
 #pragma unroll 1
   for (int i = tid; i < n; i += MT) ee[i] = exp_nonpos((double)fkey_inv(pk_key(arr[i])) - M, sh.etab);
   __syncthreads();
-  constexpr int RPW = NH / NWV;  // ranks per wave
+  const int RPW = ((n + NWV - 1) / NWV + WAVE - 1) / WAVE * WAVE;  // ranks per wave (a multiple of 64, 4 RPW >= n)
   double carry = 0.0;
 #pragma unroll 1
   for (int s = 0; s < RPW / WAVE; ++s) {
@@ -331,7 +331,17 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
     sh.nh = 0;
     sh.lpw = 0;
   }
-  // One round of record loads: thread j holds wave list j (part j / 4), threads j % 4 == 0 the part's record.
+  // One round of loads: the records (thread j holds wave list j (part j / 4), threads j % 4 == 0 the part's record) and,
+  // before the list lengths are known, the first SPEC slots of every wave list (slot o of list j in thread
+  // (j SPEC + o) % MT, round (j SPEC + o) / MT); slots past a list's length are dropped once it is known.
+  const uint64_t *cl0 = a.cand + (size_t)row * nsl * CAPW;
+  const int SPEC = max(1, (MT * GPT) / nsl);
+  uint64_t pks[GPT];
+#pragma unroll
+  for (int g = 0; g < GPT; ++g) {
+    const int e = g * MT + tid, j = e / SPEC;
+    pks[g] = j < nsl ? ld_ag(&cl0[(size_t)j * CAPW + (e - j * SPEC)]) : 0ull;
+  }
   const int prt = tid / PWAVES;
   uint32_t r_nc = 0, r_mkey = 0, r_kap = 0, r_fl = 0;
   uint64_t r_top = 0;
@@ -355,19 +365,21 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
     atomicMax(&sh.rkappa, r_kap);
     atomicMax(&sh.rmkey, r_mkey);
   }
-  // exclusive prefix of the list lengths (one list per thread)
+  // the list lengths (sh.loff), and the exclusive prefix of the slots past SPEC of the longer lists (sh.lmax)
   {
-    const uint32_t inc = wave_incl_scan_u32(r_nc);
-    if (lane_id() == WAVE - 1) sh.wcnt[tid >> 6] = inc;
+    if (tid < nsl) sh.loff[tid] = r_nc;
+    const uint32_t rem = r_nc > (uint32_t)SPEC ? r_nc - (uint32_t)SPEC : 0u;
+    const uint32_t rinc = wave_incl_scan_u32(rem);
+    if (lane_id() == WAVE - 1) sh.wcnt[tid >> 6] = rinc;
     __syncthreads();
-    uint32_t pre = 0, tot = 0;
+    uint32_t rpre = 0, rtot = 0;
 #pragma unroll
     for (int w = 0; w < NWV; ++w) {
-      pre += w < (tid >> 6) ? sh.wcnt[w] : 0u;
-      tot += sh.wcnt[w];
+      rpre += w < (tid >> 6) ? sh.wcnt[w] : 0u;
+      rtot += sh.wcnt[w];
     }
-    if (tid < nsl) sh.loff[tid] = pre + inc - r_nc;
-    if (tid == 0) sh.ltot = tot;
+    if (tid < nsl) sh.lmax[tid] = rpre + rinc - rem;
+    if (tid == 0) sh.jcount = rtot;
   }
   __syncthreads();
   const uint32_t flags = sh.rflags;
@@ -424,34 +436,20 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
     brest = f * r_b;
   }
   double scand = 0.0;
-  const uint64_t *cl0 = a.cand + (size_t)row * nsl * CAPW;
-  const uint32_t ltot = sh.ltot;
   uint64_t bestL = 0;
-  for (uint32_t f0 = 0; f0 < ltot; f0 += MT * GPT) {
-    uint64_t pk[GPT];
+  // One batch of listed entries (raw, valid): the packed maximum, the masses of the entries below the certified key
+  // (the head's masses are summed by the evaluation, which takes them anyway), head appends (one LDS atomic per wave).
+  // Through LDS, so that the processing loop stays rolled: this code runs once per row, with a cold instruction cache,
+  // and its length is its cost.
+  auto batch = [&](const uint64_t(&pk)[GPT], const bool(&ok)[GPT]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int g = 0; g < GPT; ++g) {
-      const uint32_t f = f0 + g * MT + tid;
-      int lo = 0;  // the wave list whose range [loff, loff + count) holds f: the last with loff <= f (fixed steps)
-#pragma unroll
-      for (int st = NSL / 2; st > 0; st >>= 1) {
-        const int m = lo + st;
-        if (m < nsl && sh.loff[m] <= f) lo = m;
-      }
-      pk[g] = f < ltot ? ld_ag(&cl0[(size_t)lo * CAPW + min(f - sh.loff[lo], (uint32_t)CAPW - 1u)]) : 0ull;
-    }
-    // (through LDS, so that the processing loop stays rolled: this code runs once per row, with a cold instruction
-    // cache, and its length is its cost)
-#pragma unroll
-    for (int g = 0; g < GPT; ++g) sh.r.tmp[g * MT + tid] = f0 + g * MT + tid < ltot ? key_of_raw(pk[g]) : 0ull;
+    for (int g = 0; g < GPT; ++g) sh.r.tmp[g * MT + tid] = ok[g] ? key_of_raw(pk[g]) : 0ull;
 #pragma unroll 1
     for (int g = 0; g < GPT; ++g) {
       const uint64_t v = sh.r.tmp[g * MT + tid];
       const uint32_t k = pk_key(v);
       bestL = v > bestL ? v : bestL;
-      // (the head's masses are summed by the evaluation, which takes them anyway)
       if (v && finite_max && k > KEY_NEGINF && k < kappa) scand += exp_nonpos((double)fkey_inv(k) - M, sh.etab);
-      // head appends: one LDS atomic per wave
       const bool h = v && k >= kappa;
       const uint64_t bl = ballot64(h);
       if (bl) {
@@ -462,6 +460,35 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
         if (h && pos < (uint32_t)NH) sh.r.head[pos] = v;
       }
     }
+  };
+  {
+    bool ok[GPT];
+#pragma unroll
+    for (int g = 0; g < GPT; ++g) {
+      const int e = g * MT + tid, j = e / SPEC;
+      ok[g] = j < nsl && (uint32_t)(e - j * SPEC) < sh.loff[j];
+    }
+    batch(pks, ok);
+  }
+  // the slots past SPEC of the longer lists (flat index f over them; the list holding f: the last with prefix <= f)
+  const uint32_t rtot = sh.jcount;
+  for (uint32_t f0 = 0; f0 < rtot; f0 += MT * GPT) {
+    uint64_t pk[GPT];
+    bool ok[GPT];
+#pragma unroll
+    for (int g = 0; g < GPT; ++g) {
+      const uint32_t f = f0 + g * MT + tid;
+      int lo = 0;
+#pragma unroll
+      for (int st = NSL / 2; st > 0; st >>= 1) {
+        const int m = lo + st;
+        if (m < nsl && sh.lmax[m] <= f) lo = m;
+      }
+      ok[g] = f < rtot;
+      pk[g] = ok[g] ? ld_ag(&cl0[(size_t)lo * CAPW + min((uint32_t)SPEC + f - sh.lmax[lo], (uint32_t)CAPW - 1u)])
+                    : 0ull;
+    }
+    batch(pk, ok);
   }
   bestL = wave_max_u64(bestL);
   if (lane_id() == 0) atomicMax((unsigned long long *)&sh.rtopL, (unsigned long long)bestL);
@@ -513,7 +540,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
       const bool deep = a.dslices > 0 && !greedy && !(flags & F_HOVER) && !a.force_exact && (nlp == 0 || sh.lpw);
       if (deep) {
         const uint32_t slot = atomicAdd(a.dctl, 1u);
-        if (slot < (uint32_t)DEEP_MAX) {
+        if (slot < (uint32_t)a.dslots) {
           DeepSlot *ds = a.dslot + slot;
           ds->P = P;
           ds->row = row;
@@ -545,9 +572,10 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
 // Per-lane running state of a wave.
 struct Run {
   float m;         // running maximum of this lane's z
-  double s;        // sum of this lane's unlisted exp(z - m) (fp32 terms)
+  double s;        // sum of this lane's unlisted exp(z - tau) (fp32 terms), tau the wave's threshold value
   double b;        // its error bound
   uint32_t kap;    // the wave's listing threshold key (uniform in the wave; only rises)
+  float tau;       // its value: every element at or above it is listed, so every unlisted term is at most 1
   uint32_t woff;   // elements the wave has listed (uniform)
   uint32_t vnext;  // list length at which the valve next recomputes the threshold (uniform)
   float g;         // greedy rows: largest nan_to_num(x) so far, at the lowest token gid holding it
@@ -612,27 +640,42 @@ __device__ __forceinline__ void load_u(const RowCtx &c, const RowBufs &rb, int c
   (void)pv;
 }
 
-// z of one chunk in place: the mask and the history exclusion (one select; -inf for tokens the stream does not carry),
-// the NaN flag (every loaded value is one of the row's own, so any NaN seen is the row's), the division by T
-// (div_exact), the lane's chunk maximum; greedy rows track the first maximum of nan_to_num(x).
+// The history words of a chunk's vectors (bit o of the part's history bitset = token p0 + o is in the row's history),
+// read from LDS with the chunk's loads, so that the read is done by the time the chunk is processed.
+template <int DT>
+__device__ __forceinline__ void hist_words(const HistTab &h, int cb, int p0, int p1, uint32_t (&hw)[Lay<DT>::NV]) {
+  using L = Lay<DT>;
+  const int l = lane_id();
+#pragma unroll
+  for (int v = 0; v < L::NV; ++v) {
+    const int o = min(cb + v * L::STRIDE + l * L::VEC, p1 - 1) - p0;  // (a vector past the end reads a valid word)
+    hw[v] = h.bits[o >> 5] >> (o & 31);
+  }
+}
+
+// z of one chunk in place: the mask and the history exclusion (-inf for tokens the stream does not carry; a select only
+// in chunks where some lane has such a token), the NaN flag (every loaded value is one of the row's own, so any NaN seen
+// is the row's), the division by T (div_exact), the lane's chunk maximum; greedy rows track the first maximum of
+// nan_to_num(x).
 template <int DT, bool AL, bool MASKED, bool GREEDY, bool DIV>
 __device__ __forceinline__ float chunk_z(const RowCtx &c, int cb, int p0, int pv, int p1, float (&xr)[EPL],
-                                         const uint32_t (&mw)[Lay<DT>::NV], const HistTab &h, Run &rn, float *proc) {
+                                         const uint32_t (&mw)[Lay<DT>::NV], const uint32_t (&hw)[Lay<DT>::NV],
+                                         Run &rn, float *proc) {
   using L = Lay<DT>;
   constexpr uint32_t VMASK = (1u << L::VEC) - 1u;
   const int l = lane_id();
-  uint32_t inr[L::NV];
+  uint32_t inr[L::NV], keep[L::NV];
+  bool full = true;
 #pragma unroll
   for (int v = 0; v < L::NV; ++v) {
     const int t0 = cb + v * L::STRIDE + l * L::VEC;
     uint32_t in;
     if constexpr (AL) in = t0 + L::VEC <= pv ? VMASK : 0u;
     else in = t0 + L::VEC <= pv ? VMASK : (t0 >= pv ? 0u : (1u << (pv - t0)) - 1u);
-    if (c.pen) {
-      const int o = min(t0, p1 - 1) - p0;  // (a vector past the end reads a valid word; its bits are cleared)
-      in &= ~(h.bits[o >> 5] >> (o & 31));
-    }
+    if (c.pen) in &= ~hw[v];
     inr[v] = in & VMASK;
+    keep[v] = (MASKED ? (mw[v] >> ((l * L::VEC) & 31)) : VMASK) & inr[v];
+    full = full && keep[v] == VMASK;
   }
   if (proc) {  // processed logits (after penalties and mask, before T) of the streamed tokens
 #pragma unroll
@@ -644,28 +687,35 @@ __device__ __forceinline__ float chunk_z(const RowCtx &c, int cb, int p0, int pv
         if ((inr[v] >> k) & 1u) proc[t0 + k] = keep_or_ninf(xr[v * L::VEC + k], al, k);
     }
   }
-  float cmax = -INFINITY;
 #pragma unroll
   for (int i = 0; i < EPL; i += 2) rn.nanm |= ballot64(__builtin_isunordered(xr[i], xr[i + 1]));  // (a NaN in either)
+  float cmax = -INFINITY;
+  if (!GREEDY && ballot64(!full) == 0ull) {  // every token of the chunk is carried and allowed: no select
 #pragma unroll
-  for (int v = 0; v < L::NV; ++v) {
-    const int t0 = cb + v * L::STRIDE + l * L::VEC;
-    const uint32_t keep = (MASKED ? (mw[v] >> ((l * L::VEC) & 31)) : VMASK) & inr[v];
-#pragma unroll
-    for (int k = 0; k < L::VEC; ++k) {
-      const int i = v * L::VEC + k;
-      const float x = xr[i];
-      const float xm = keep_or_ninf(x, keep, k);
-      if constexpr (GREEDY) {  // masked tokens take part in the argmax as -FLT_MAX
-        const float g = fminf(fmaxf(xm, -FLTMAX), FLTMAX);
-        if (((inr[v] >> k) & 1u) && xm == xm && (g > rn.g || rn.gid == 0xFFFFFFFFu)) {
-          rn.g = g;
-          rn.gid = (uint32_t)(t0 + k);
-        }
-      }
-      const float z = DIV ? div_exact(xm, c.Rd) : xm;
+    for (int i = 0; i < EPL; ++i) {
+      const float z = DIV ? div_exact(xr[i], c.Rd) : xr[i];
       xr[i] = z;
       cmax = fmaxf(cmax, z);
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < L::NV; ++v) {
+      const int t0 = cb + v * L::STRIDE + l * L::VEC;
+#pragma unroll
+      for (int k = 0; k < L::VEC; ++k) {
+        const int i = v * L::VEC + k;
+        const float xm = keep_or_ninf(xr[i], keep[v], k);
+        if constexpr (GREEDY) {  // masked tokens take part in the argmax as -FLT_MAX
+          const float g = fminf(fmaxf(xm, -FLTMAX), FLTMAX);
+          if (((inr[v] >> k) & 1u) && xm == xm && (g > rn.g || rn.gid == 0xFFFFFFFFu)) {
+            rn.g = g;
+            rn.gid = (uint32_t)(t0 + k);
+          }
+        }
+        const float z = DIV ? div_exact(xm, c.Rd) : xm;
+        xr[i] = z;
+        cmax = fmaxf(cmax, z);
+      }
     }
   }
   if (rn.fid == 0xFFFFFFFFu) {  // the lane's first chunk: its lowest token whose value is not NaN
@@ -692,29 +742,36 @@ __device__ __forceinline__ float pairwise(F &f) {
   }
 }
 
-// The lane maximum, the threshold valve, the unlisted terms exp2(t), t = (z - m) log2(e) (fp32 per chunk, fp64 across
-// chunks), the listing. tok(i) gives the token of slot i.
+// Raises the wave's threshold to kap (uniform) and rescales the lanes' sums to the new reference (fp64).
+__device__ __forceinline__ void set_tau(Run &rn, uint32_t kap) {
+  const float tnew = fkey_inv(kap);
+  if (rn.tau > -INFINITY && tnew > rn.tau) {
+    const double f = exp((double)rn.tau - (double)tnew);
+    rn.s *= f;
+    rn.b *= f;
+  }
+  rn.kap = kap;
+  rn.tau = tnew;
+}
+
+// The lane maximum, the threshold valve, the unlisted terms exp2(t), t = (z - tau) log2(e) (fp32 per chunk, fp64
+// across chunks; z < tau for every unlisted element, so t < 0), the listing. tok(i) gives the token of slot i.
 template <int N, typename Tok>
 __device__ __forceinline__ void chunk_sum(const ScanArgs &a, int row, int wl, float cmax, const float (&zr)[N],
                                           Run &rn, Tok tok) {
   static_assert((N & (N - 1)) == 0 && N <= 256, "");
-  const float mnew = fmaxf(rn.m, cmax);
+  rn.m = fmaxf(rn.m, cmax);
   if (rn.woff >= rn.vnext) {  // (again after every KV / 2 more listed elements)
-    rn.kap = max(rn.kap, wave_kth_largest_u16(fkey(mnew) >> 16, KV) << 16);
+    const uint32_t k = max(rn.kap, wave_kth_largest_u16(fkey(rn.m) >> 16, KV) << 16);
+    if (k > rn.kap) set_tau(rn, k);
     rn.vnext = rn.woff + KV / 2;
   }
-  const float tauf = fkey_inv(rn.kap);
-  if (mnew > rn.m && rn.m > -INFINITY) {  // rescale the lane's sum to its new maximum (fp64)
-    const double f = exp((double)rn.m - (double)mnew);
-    rn.s *= f;
-    rn.b *= f;
-  }
-  rn.m = mnew;
+  const float tauf = rn.tau;
   // -inf (masked, excluded) gives t = -256 and e = 0
   float e[N], t[N];
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    t[i] = fmaxf((zr[i] - mnew) * LOG2E, -256.0f);
+    t[i] = fmaxf((zr[i] - tauf) * LOG2E, -256.0f);
     e[i] = __builtin_amdgcn_exp2f(t[i]);
   }
   if (ballot64(cmax >= tauf)) {  // some lane holds an element at or above the threshold: list them (they leave the sum)
@@ -729,6 +786,7 @@ __device__ __forceinline__ void chunk_sum(const ScanArgs &a, int row, int wl, fl
           const uint32_t pos = woff + lanes_below(bl);
           if (pos < (uint32_t)CAPW) st_ag(&cl[pos], raw_entry(zr[i], tok(i)));
           e[i] = 0.0f;
+          t[i] = 0.0f;
         }
         woff += (uint32_t)__popcll(bl);
       }
@@ -739,13 +797,10 @@ __device__ __forceinline__ void chunk_sum(const ScanArgs &a, int row, int wl, fl
 #pragma unroll
   for (int i = 0; i < N; ++i) mom = fmaf(e[i], t[i], mom);
   auto term = [&](auto ic) __attribute__((always_inline)) { return e[decltype(ic)::value]; };
-  float s = pairwise<0, N>(term);
-  if (!(fabsf(mnew) < INFINITY)) {  // nothing above -inf yet (or +inf): no sum
-    s = 0.0f;
-    mom = 0.0f;
-  }
-  // error bound: v_exp_f32 (2 ulp), log2(N) fp32 pairwise additions, flushed subnormal results; the exponent's three
-  // roundings (3 ulp of |t|, times ln 2; mom = -sum e |t|)
+  const float s = pairwise<0, N>(term);
+  // error bound: v_exp_f32 (2 ulp), log2(N) fp32 pairwise additions, flushed subnormal results; the exponent's
+  // roundings (z - tau exact or rounded once, the product by log2(e) rounded, log2(e) rounded: 3 ulp of |t|, times
+  // ln 2; mom = -sum e |t|)
   constexpr double LV = N >= 16 ? 4.0 : N >= 8 ? 3.0 : N >= 4 ? 2.0 : 1.0;
   rn.s += (double)s;
   rn.b += (double)s * (2.4e-7 + LV * 6.0e-8 + 5e-8) - (double)mom * 1.25e-7 + 1e-36;
@@ -817,16 +872,18 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     }
   }
   const RowBufs rbuf = row_bufs(c);
-  float xa[EPL], xb[EPL], xc[EPL];
-  uint32_t ma[L::NV], mb[L::NV], mcw[L::NV];
+  float xa[EPL], xb[EPL], xc[EPL], xd[EPL];
+  uint32_t ma[L::NV], mb[L::NV], mcw[L::NV], md[L::NV];
+  uint32_t ha[L::NV] = {}, hb[L::NV] = {}, hc[L::NV] = {}, hd[L::NV] = {};  // history words (penalized rows)
   const int wu = __builtin_amdgcn_readfirstlane(w);  // (the wave index as a scalar: the chunk loop stays uniform)
-  int c0 = wu, c1 = wu + NWV;  // wave w takes chunks w, w + 4, w + 8, ...
+  int c0 = wu, c1 = wu + NWV, c3 = wu + 2 * NWV;  // wave w takes chunks w, w + 4, w + 8, ...
   // First token of chunk ck for its loads. A chunk past the stream gets a start far past the row (vocabularies are at
   // most 2^21 tokens): its buffer loads fail the range check and return zeros without a memory access (unaligned rows
   // clamp to the part instead), so the loads a wave issues ahead of its last chunk fetch nothing.
   const auto cst = [&](int ck) -> int { return ck < nck ? p0 + ck * CHK : (1 << 28); };
   load_u<DT, AL, MASKED>(c, rbuf, cst(c0), pv, p1, xa, ma);
   load_u<DT, AL, MASKED>(c, rbuf, cst(c1), pv, p1, xb, mb);
+  load_u<DT, AL, MASKED>(c, rbuf, cst(c3), pv, p1, xd, md);
   // allowed tokens of the part's stream range (masked rows: popcounts of its mask words, every load issued before the
   // first is used; the sum comes after the history build)
   constexpr int APW = (PTOK / 32 + MT - 1) / MT;  // mask words per thread
@@ -855,11 +912,17 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     apc = tid == 0 ? (uint32_t)(pv - p0) : 0u;
   }
 
+  if (c.pen) {  // (the first two chunks were loaded before the history tables existed)
+    hist_words<DT>(sh.h, cst(c0), p0, p1, ha);
+    hist_words<DT>(sh.h, cst(c1), p0, p1, hb);
+    hist_words<DT>(sh.h, cst(c3), p0, p1, hd);
+  }
   Run rn;
   rn.m = -INFINITY;
   rn.s = 0.0;
   rn.b = 0.0;
   rn.kap = 0;
+  rn.tau = -INFINITY;
   rn.woff = 0;
   rn.vnext = CAPW / 4 + 1;
   rn.g = -INFINITY;
@@ -867,7 +930,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   rn.fid = 0xFFFFFFFFu;
   rn.nanm = 0;
   // the next chunks (scalar arithmetic: no LDS round trip and no vector temporary between a chunk's loads and its use)
-  int nxt = wu + 2 * NWV;
+  int nxt = wu + 3 * NWV;
   auto grab = [&]() -> int {
     const int n = nxt;
     nxt += NWV;
@@ -878,7 +941,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   };
   // First chunk of each wave; the part's listing threshold from the 256 lane maxima.
   float cmax = -INFINITY;
-  if (c0 < nck) cmax = chunk_z<DT, AL, MASKED, GREEDY, DIV>(c, p0 + c0 * CHK, p0, pv, p1, xa, ma, sh.h, rn, proc);
+  if (c0 < nck) cmax = chunk_z<DT, AL, MASKED, GREEDY, DIV>(c, p0 + c0 * CHK, p0, pv, p1, xa, ma, ha, rn, proc);
   if (listing) {
     // The listing threshold: the rank-kp largest of the 256 lane maxima of the waves' first chunks (a 2048-token
     // sample). kp is scaled so that about T tokens of the part lie above it: kp = T * (allowed tokens in the sample) /
@@ -915,34 +978,45 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
       for (int q = 0; q < NWV; ++q) cnt += (uint32_t)__popcll(ballot64(sh.lmax[q * WAVE + lane] >= cand));
       if ((int)cnt >= (int)kp) r = cand;
     }
-    rn.kap = max(r << 16, KEY_NEGINF + 1u);
+    set_tau(rn, max(r << 16, KEY_NEGINF + 1u));
   }
   int c2 = grab();
   load_u<DT, AL, MASKED>(c, rbuf, cst(c2), pv, p1, xc, mcw);
+  if (c.pen) hist_words<DT>(sh.h, cst(c2), p0, p1, hc);
   if (c0 < nck) {
     if (listing) chunk_sum<EPL>(a, row, wl, cmax, xa, rn, tok_of(p0 + c0 * CHK));
     else rn.m = fmaxf(rn.m, cmax);
   }
-  // Steady state: two chunks loading while the wave works on a third (chunk indices rise, so the first past the end
-  // ends the wave's stream).
-  auto step = [&](int ck, float(&x)[EPL], const uint32_t(&mw)[L::NV]) __attribute__((always_inline)) {
-    const float cm = chunk_z<DT, AL, MASKED, GREEDY, DIV>(c, p0 + ck * CHK, p0, pv, p1, x, mw, sh.h, rn, proc);
+  // Steady state: three chunks loading while the wave works on a fourth (chunk indices rise, so the first past the end
+  // ends the wave's stream). In processing order: b, d, c, a, b, d, ... (a was processed above).
+  auto step = [&](int ck, float(&x)[EPL], const uint32_t(&mw)[L::NV], const uint32_t(&hw)[L::NV])
+                  __attribute__((always_inline)) {
+    const float cm = chunk_z<DT, AL, MASKED, GREEDY, DIV>(c, p0 + ck * CHK, p0, pv, p1, x, mw, hw, rn, proc);
     if (listing) chunk_sum<EPL>(a, row, wl, cm, x, rn, tok_of(p0 + ck * CHK));
     else rn.m = fmaxf(rn.m, cm);
   };
+  // (c2 was issued above; c3 before the history build: processing order c1, c3, c2, then the next grabs)
   while (true) {
     c0 = grab();
     load_u<DT, AL, MASKED>(c, rbuf, cst(c0), pv, p1, xa, ma);
+    if (c.pen) hist_words<DT>(sh.h, cst(c0), p0, p1, ha);
     if (c1 >= nck) break;
-    step(c1, xb, mb);
+    step(c1, xb, mb, hb);
     c1 = grab();
     load_u<DT, AL, MASKED>(c, rbuf, cst(c1), pv, p1, xb, mb);
+    if (c.pen) hist_words<DT>(sh.h, cst(c1), p0, p1, hb);
+    if (c3 >= nck) break;
+    step(c3, xd, md, hd);
+    c3 = grab();
+    load_u<DT, AL, MASKED>(c, rbuf, cst(c3), pv, p1, xd, md);
+    if (c.pen) hist_words<DT>(sh.h, cst(c3), p0, p1, hd);
     if (c2 >= nck) break;
-    step(c2, xc, mcw);
+    step(c2, xc, mcw, hc);
     c2 = grab();
     load_u<DT, AL, MASKED>(c, rbuf, cst(c2), pv, p1, xc, mcw);
+    if (c.pen) hist_words<DT>(sh.h, cst(c2), p0, p1, hc);
     if (c0 >= nck) break;
-    step(c0, xa, ma);
+    step(c0, xa, ma, ha);
   }
   // the history tokens of the part (the tables are still in LDS: the resolve has not started), then the ragged ones
   if (c.pen) {
@@ -989,8 +1063,8 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
 #pragma unroll
   for (int k = 1; k < NWV; ++k) M = fmaxf(M, sh.wmax[k]);
   double s = 0.0, b = 0.0;
-  if (rn.m > -INFINITY && fabsf(M) < INFINITY) {
-    const double f = exp((double)rn.m - (double)M);
+  if (rn.tau > -INFINITY && fabsf(M) < INFINITY) {  // the lane's sum, relative to its wave's threshold, to M
+    const double f = exp((double)rn.tau - (double)M);
     s = rn.s * f;
     b = rn.b * f;
   }
