@@ -174,17 +174,20 @@ class Handle:
 
 
 def handle(device, rows, vocab):
-    """A handle on device that fits rows x vocab (one per device, grown on demand)."""
+    """A handle on device that fits rows x vocab, grown on demand. There is one per (device, current stream, thread):
+    a handle's workspace must not serve two calls that can overlap, on the device (two streams) or on the host (two
+    threads: a handle is not thread safe), so each stream a thread launches on gets its own."""
     if not torch.cuda.is_available():
         raise RuntimeError("goethe-engine_amd needs a HIP device (torch.cuda.is_available() is False)")
+    key = (device, torch.cuda.current_stream(device).cuda_stream, threading.get_ident())
     with _lock:
-        h = _handles.get(device)
+        h = _handles.get(key)
         if h is None or h.rows < rows or h.vocab < vocab:
             if h is not None:
                 torch.cuda.synchronize(device)
                 h.close()
             h = Handle(device, max(rows, h.rows if h else 0, 64), max(vocab, h.vocab if h else 0))
-            _handles[device] = h
+            _handles[key] = h
         return h
 
 

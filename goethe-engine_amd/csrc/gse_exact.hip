@@ -619,6 +619,10 @@ __global__ __launch_bounds__(XT) void exact_kernel(ScanArgs a) {
   __shared__ int hrow[XT];
   if (blockIdx.x == 0 && threadIdx.x == 0) a.dctl[0] = 0u;  // the deep rows of this call are finished
   const int G = (int)gridDim.x, w = threadIdx.x / WAVE;
+  // A workgroup with no hard row ends here, before the set-up of the row code (its registers and spill slots).
+  bool any = false;
+  for (int r = (int)blockIdx.x + (int)threadIdx.x * G; r < a.rows; r += XT * G) any |= (a.info[r].flags & R_HARD) != 0;
+  if (!__syncthreads_or(any)) return;
   for (int j0 = 0; (int)blockIdx.x + j0 * G < a.rows; j0 += XT) {
     const int r = (int)blockIdx.x + (j0 + (int)threadIdx.x) * G;
     const bool hard = r < a.rows && (a.info[r].flags & R_HARD);

@@ -88,7 +88,8 @@ class MaskBatch:
     """The packed grammar masks of one step's rows (engine.py:272-273, :280 compute mask() per row and unpack it to
     bool [V]): matchers write their rows' words in place into one host buffer, int32 [rows, ceil(vocab / 32)], pinned
     when a GPU is present, and sample(..., masks=batch) sends the whole buffer to the device in one asynchronous copy
-    on the launch stream. Rows that were not filled since the last reset() carry no mask.
+    on the launch stream. Rows that were not filled since the last reset() carry no mask. A batch may hold more rows
+    than a call samples (one buffer sized for the largest batch): a call over n rows uses its first n.
 
     The copy reads the host buffer after sample() has been called, so refill it only once that call's results have
     been read (sample() returns them synchronously; after sample_ex, synchronize first)."""
@@ -125,9 +126,11 @@ class MaskBatch:
             raise ValueError(f"mask of row {row} has {m.numel()} entries, the row has {self.vocab} tokens")
         self.filled[row] = True
 
-    def device_words(self, dev):
-        """The buffer on `dev` (one copy from the host buffer, on the current stream of dev)."""
+    def device_words(self, dev, n=None):
+        """The first n rows (all by default) of the buffer on `dev`: one copy from the host buffer, on the current
+        stream of dev."""
+        n = self.rows if n is None else int(n)
         if self._dev is None or self._dev.device != dev:
             self._dev = torch.empty((self.rows, self.words), dtype=torch.int32, device=dev)
-        self._dev.copy_(self.host, non_blocking=True)
-        return self._dev
+        self._dev[:n].copy_(self.host[:n], non_blocking=True)
+        return self._dev[:n]

@@ -152,13 +152,13 @@ def _masks(h, masks, n, v, dev, rows):
         return None, 0
     words = (v + 31) // 32
     if getattr(masks, "is_mask_batch", False):  # grammar.MaskBatch: every row's words in one host buffer, one copy
-        if masks.rows != n or masks.vocab != v:
+        if masks.rows < n or masks.vocab != v:
             raise ValueError(f"mask batch of {masks.rows} x {masks.vocab}, the logits are {n} x {v}")
-        if not masks.filled.any():
+        if not masks.filled[:n].any():
             return None, 0
-        idx = np.nonzero(masks.filled)[0]
+        idx = np.nonzero(masks.filled[:n])[0]
         rows["mask_row"][idx] = idx
-        return masks.device_words(dev), masks.words
+        return masks.device_words(dev, n), masks.words
     packed, bools, where = [], [], []
     for i in range(n):
         m = masks[i]

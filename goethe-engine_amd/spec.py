@@ -142,147 +142,172 @@ def verify_tree(reqs, nout0=0, stop=None, emit_ld=None):
     no valid token (engine.py:286-288, the -1 is not emitted), what stop returned, or None."""
     if not reqs:
         return []
-    dev = _device()
-    sizes = [len(r["tokens"]) + 1 for r in reqs]
-    anchors = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int32)
-    nodes = int(sum(sizes))
-    parents = np.full(nodes, -1, np.int32)
-    toks = np.zeros(nodes, np.int32)
-    qrow = np.full(nodes, -1, np.int32)
-    params, seeds, idxs, masks, hists = [], [], [], [], []
-    qprob, qlog, qtemp, qkey = [], [], [], {}
-    max_kids = 1
-    for a, r in enumerate(reqs):
-        n, base, p = sizes[a], int(anchors[a]), r["params"]
-        par = list(r["parents"])
-        if len(par) != n - 1 or not all(0 <= q <= j for j, q in enumerate(par)):
-            raise ValueError(f"request {a}: parents must give node j + 1 a parent in [0, j]")
-        kids = kids_of(par)
-        max_kids = max(max_kids, max(len(k) for k in kids))
-        depth = [0] * n
-        for j, q in enumerate(par):
-            depth[j + 1] = depth[q] + 1
-            parents[base + j + 1] = base + q
-        toks[base + 1:base + n] = r["tokens"]
-        n0 = int(r.get("nout", nout0))
-        qsrc = r.get("q")
-        for u in range(n):
-            params.append(p)
-            seeds.append(r["seed"])
-            idxs.append(n0 + depth[u])
-        for j in range(1, n):
-            c_parent = par[j - 1]
-            qd = None
-            if r.get("draft") is not None:
-                qd = ("draft", a, c_parent)
-            elif isinstance(qsrc, dict):
-                qd = qsrc.get(c_parent)
-            elif qsrc is not None:
-                qd = qsrc[j - 1]
-            if qd is None:
-                continue
-            if isinstance(qd, tuple):  # the request's drafter logits row of the parent
-                key = qd
-                if key not in qkey:
-                    qkey[key] = len(qlog)
-                    qlog.append(_as_row(r["draft"], c_parent, dev))
-                    qtemp.append(float(r.get("draft_t", 1.0)))
-            elif isinstance(qd, QRef):
-                key = ("ref", id(qd))
-                if key not in qkey:
-                    qkey[key] = len(qlog)
-                    qlog.append(qd.x.reshape(-1))
-                    qtemp.append(qd.t)
-            else:
-                key = ("prob", id(qd))
-                if key not in qkey:
-                    qkey[key] = len(qprob)
-                    qprob.append(qd)
-            qrow[base + j] = qkey[key]
-        masks += _per_node(r.get("masks"), n)
-        hists += _per_node_history(r.get("history"), n)
-    if qprob and qlog:
-        raise ValueError("one verify call takes its draft distributions either as fp64 rows or as drafter logits")
-    if max_kids > _lib.MAX_KIDS:
-        raise ValueError(f"a node with {max_kids} kids; at most {_lib.MAX_KIDS}")
-    x = _stack_targets([r["target"] for r in reqs], sizes, dev)
-    x, code = _logits(x)
-    v = x.shape[1]
-    if np.any((toks < 0) | (toks >= v)):
-        raise ValueError("drafted token outside the vocabulary")
-    h = _lib.handle(dev.index, nodes, v)
-    hist_dev, offs = _history(hists if any(hh is not None for hh in hists) else None, nodes, dev)
-    rows = _rows(params, seeds, idxs, offs)
-    for a, r in enumerate(reqs):
-        if strict(r["params"]):
-            base = int(anchors[a])
-            for u, k in enumerate(kids_of(list(r["parents"]))):
-                if k:
-                    rows["flags"][base + u] |= _lib.ROW_MSS
-    mask_dev, mask_ld = _masks(h, masks if any(m is not None for m in masks) else None, nodes, v, dev, rows)
-    rows_dev = torch.from_numpy(rows.view(np.uint8)).to(dev, non_blocking=True)
-    b = _lib.Batch()
-    b.size = C.sizeof(_lib.Batch)
-    b.dtype, b.rows, b.vocab, b.ld = code, nodes, v, x.stride(0)
-    b.logits, b.params = x.data_ptr(), rows_dev.data_ptr()
-    b.mask = mask_dev.data_ptr() if mask_dev is not None else None
-    b.mask_ld = mask_ld
-    b.hist = hist_dev.data_ptr() if hist_dev is not None else None
-    b.stream = torch.cuda.current_stream(dev).cuda_stream
-    t = _lib.Tree()
-    t.size = C.sizeof(_lib.Tree)
-    t.requests = len(reqs)
-    anc_d = torch.from_numpy(anchors).to(dev)
-    par_d = torch.from_numpy(parents).to(dev)
-    tok_d = torch.from_numpy(toks).to(dev)
-    qrow_d = torch.from_numpy(qrow).to(dev)
-    t.anchor, t.parent, t.token, t.qrow = anc_d.data_ptr(), par_d.data_ptr(), tok_d.data_ptr(), qrow_d.data_ptr()
-    t.max_kids = max_kids
-    keep = [anc_d, par_d, tok_d, qrow_d, rows_dev, mask_dev, hist_dev, x]
-    t.qrows.size = C.sizeof(_lib.QRows)
-    if qprob:
-        qt = _f64_rows(qprob, dev)
-        t.qrows.kind, t.qrows.rows, t.qrows.q, t.qrows.ld = _lib.Q_PROB, len(qprob), qt.data_ptr(), qt.stride(0)
-        keep.append(qt)
-    elif qlog:
-        ql = torch.stack([q.to(dev) for q in qlog])
-        if ql.dtype not in (torch.float32, torch.bfloat16):
-            ql = ql.float()
-        ql = ql.contiguous()
-        tt = torch.tensor(qtemp, dtype=torch.float64, device=dev)
-        t.qrows.kind = _lib.Q_LOGITS_BF16 if ql.dtype == torch.bfloat16 else _lib.Q_LOGITS_F32
-        t.qrows.rows, t.qrows.q, t.qrows.ld, t.qrows.temperature = len(qlog), ql.data_ptr(), ql.stride(0), tt.data_ptr()
-        keep += [ql, tt]
-    ld = int(emit_ld or max(sizes))
-    e_len = torch.empty(len(reqs), dtype=torch.int32, device=dev)
-    e_tok = torch.empty((len(reqs), ld), dtype=torch.int32, device=dev)
-    e_node = torch.empty((len(reqs), ld), dtype=torch.int32, device=dev)
-    e_st = torch.empty(len(reqs), dtype=torch.int32, device=dev)
-    o = _lib.TreeOut()
-    o.size = C.sizeof(_lib.TreeOut)
-    o.emit_len, o.emit_tokens, o.emit_nodes, o.emit_ld = e_len.data_ptr(), e_tok.data_ptr(), e_node.data_ptr(), ld
-    o.status = e_st.data_ptr()
-    h.ck(h.L.gse_verify_tree(h.h, C.byref(b), C.byref(t), C.byref(o)), "gse_verify_tree")
-    out = torch.cat([e_len[:, None], e_st[:, None], e_tok, e_node], 1).cpu().numpy()  # (one copy back)
-    del keep
-    res = []
-    for a in range(len(reqs)):
-        n, stt = int(out[a, 0]), int(out[a, 1])
-        tk = [int(v) for v in out[a, 2:2 + min(n, ld)]]
-        nd = [int(v) - int(anchors[a]) for v in out[a, 2 + ld:2 + ld + min(n, ld)]]
-        why = None
-        if stt == _lib.WALK_ERROR:  # the path also holds the node whose row had no valid token
-            why = "error"
-            if n < ld:
-                nd.append(int(out[a, 2 + ld + n]) - int(anchors[a]))
-        if stop is not None:
-            for d in range(len(tk)):
-                w = stop(a, tk[:d + 1])
-                if w:
-                    tk, nd, why = tk[:d + 1], nd[:d + 1], w
-                    break
-        res.append((tk, nd, why))
-    return res
+    call = VerifyCall(reqs, nout0, emit_ld)
+    call.launch()
+    return call.result(stop)
+
+
+class VerifyCall:
+    """verify_tree's device call with its inputs resident: built once from the requests (the same arguments as
+    verify_tree), launch() enqueues gse_verify_tree on the current stream (as often as wanted: the inputs are left as
+    they are), result(stop) copies the emitted tokens back (one copy) and applies the stop predicate."""
+
+    def __init__(self, reqs, nout0=0, emit_ld=None):
+        if not reqs:
+            raise ValueError("no requests")
+        self._build(reqs, nout0, emit_ld)
+
+    def launch(self):
+        self.b.stream = torch.cuda.current_stream(self.dev).cuda_stream
+        h = _lib.handle(self.dev.index, self.nodes, self.vocab)  # (this stream's handle, grown by other calls or not)
+        h.ck(h.L.gse_verify_tree(h.h, C.byref(self.b), C.byref(self.t), C.byref(self.o)), "gse_verify_tree")
+
+    def result(self, stop=None):
+        out = torch.cat([self.e_len[:, None], self.e_st[:, None], self.e_tok, self.e_node], 1).cpu().numpy()
+        ld, anchors = self.ld, self.anchors
+        res = []
+        for a in range(self.n_req):
+            n, stt = int(out[a, 0]), int(out[a, 1])
+            tk = [int(v) for v in out[a, 2:2 + min(n, ld)]]
+            nd = [int(v) - int(anchors[a]) for v in out[a, 2 + ld:2 + ld + min(n, ld)]]
+            why = None
+            if stt == _lib.WALK_ERROR:  # the path also holds the node whose row had no valid token
+                why = "error"
+                if n < ld:
+                    nd.append(int(out[a, 2 + ld + n]) - int(anchors[a]))
+            if stop is not None:
+                for d in range(len(tk)):
+                    w = stop(a, tk[:d + 1])
+                    if w:
+                        tk, nd, why = tk[:d + 1], nd[:d + 1], w
+                        break
+            res.append((tk, nd, why))
+        return res
+
+    def _build(self, reqs, nout0, emit_ld):
+        dev = _device()
+        sizes = [len(r["tokens"]) + 1 for r in reqs]
+        anchors = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int32)
+        nodes = int(sum(sizes))
+        parents = np.full(nodes, -1, np.int32)
+        toks = np.zeros(nodes, np.int32)
+        qrow = np.full(nodes, -1, np.int32)
+        params, seeds, idxs, masks, hists = [], [], [], [], []
+        qprob, qlog, qtemp, qkey = [], [], [], {}
+        max_kids = 1
+        for a, r in enumerate(reqs):
+            n, base, p = sizes[a], int(anchors[a]), r["params"]
+            par = list(r["parents"])
+            if len(par) != n - 1 or not all(0 <= q <= j for j, q in enumerate(par)):
+                raise ValueError(f"request {a}: parents must give node j + 1 a parent in [0, j]")
+            kids = kids_of(par)
+            max_kids = max(max_kids, max(len(k) for k in kids))
+            depth = [0] * n
+            for j, q in enumerate(par):
+                depth[j + 1] = depth[q] + 1
+                parents[base + j + 1] = base + q
+            toks[base + 1:base + n] = r["tokens"]
+            n0 = int(r.get("nout", nout0))
+            qsrc = r.get("q")
+            for u in range(n):
+                params.append(p)
+                seeds.append(r["seed"])
+                idxs.append(n0 + depth[u])
+            for j in range(1, n):
+                c_parent = par[j - 1]
+                qd = None
+                if r.get("draft") is not None:
+                    qd = ("draft", a, c_parent)
+                elif isinstance(qsrc, dict):
+                    qd = qsrc.get(c_parent)
+                elif qsrc is not None:
+                    qd = qsrc[j - 1]
+                if qd is None:
+                    continue
+                if isinstance(qd, tuple):  # the request's drafter logits row of the parent
+                    key = qd
+                    if key not in qkey:
+                        qkey[key] = len(qlog)
+                        qlog.append(_as_row(r["draft"], c_parent, dev))
+                        qtemp.append(float(r.get("draft_t", 1.0)))
+                elif isinstance(qd, QRef):
+                    key = ("ref", id(qd))
+                    if key not in qkey:
+                        qkey[key] = len(qlog)
+                        qlog.append(qd.x.reshape(-1))
+                        qtemp.append(qd.t)
+                else:
+                    key = ("prob", id(qd))
+                    if key not in qkey:
+                        qkey[key] = len(qprob)
+                        qprob.append(qd)
+                qrow[base + j] = qkey[key]
+            masks += _per_node(r.get("masks"), n)
+            hists += _per_node_history(r.get("history"), n)
+        if qprob and qlog:
+            raise ValueError("one verify call takes its draft distributions either as fp64 rows or as drafter logits")
+        if max_kids > _lib.MAX_KIDS:
+            raise ValueError(f"a node with {max_kids} kids; at most {_lib.MAX_KIDS}")
+        x = _stack_targets([r["target"] for r in reqs], sizes, dev)
+        x, code = _logits(x)
+        v = x.shape[1]
+        if np.any((toks < 0) | (toks >= v)):
+            raise ValueError("drafted token outside the vocabulary")
+        h = _lib.handle(dev.index, nodes, v)
+        hist_dev, offs = _history(hists if any(hh is not None for hh in hists) else None, nodes, dev)
+        rows = _rows(params, seeds, idxs, offs)
+        for a, r in enumerate(reqs):
+            if strict(r["params"]):
+                base = int(anchors[a])
+                for u, k in enumerate(kids_of(list(r["parents"]))):
+                    if k:
+                        rows["flags"][base + u] |= _lib.ROW_MSS
+        mask_dev, mask_ld = _masks(h, masks if any(m is not None for m in masks) else None, nodes, v, dev, rows)
+        rows_dev = torch.from_numpy(rows.view(np.uint8)).to(dev, non_blocking=True)
+        b = _lib.Batch()
+        b.size = C.sizeof(_lib.Batch)
+        b.dtype, b.rows, b.vocab, b.ld = code, nodes, v, x.stride(0)
+        b.logits, b.params = x.data_ptr(), rows_dev.data_ptr()
+        b.mask = mask_dev.data_ptr() if mask_dev is not None else None
+        b.mask_ld = mask_ld
+        b.hist = hist_dev.data_ptr() if hist_dev is not None else None
+        b.stream = torch.cuda.current_stream(dev).cuda_stream
+        t = _lib.Tree()
+        t.size = C.sizeof(_lib.Tree)
+        t.requests = len(reqs)
+        anc_d = torch.from_numpy(anchors).to(dev)
+        par_d = torch.from_numpy(parents).to(dev)
+        tok_d = torch.from_numpy(toks).to(dev)
+        qrow_d = torch.from_numpy(qrow).to(dev)
+        t.anchor, t.parent, t.token, t.qrow = anc_d.data_ptr(), par_d.data_ptr(), tok_d.data_ptr(), qrow_d.data_ptr()
+        t.max_kids = max_kids
+        keep = [anc_d, par_d, tok_d, qrow_d, rows_dev, mask_dev, hist_dev, x]
+        t.qrows.size = C.sizeof(_lib.QRows)
+        if qprob:
+            qt = _f64_rows(qprob, dev)
+            t.qrows.kind, t.qrows.rows, t.qrows.q, t.qrows.ld = _lib.Q_PROB, len(qprob), qt.data_ptr(), qt.stride(0)
+            keep.append(qt)
+        elif qlog:
+            ql = torch.stack([q.to(dev) for q in qlog])
+            if ql.dtype not in (torch.float32, torch.bfloat16):
+                ql = ql.float()
+            ql = ql.contiguous()
+            tt = torch.tensor(qtemp, dtype=torch.float64, device=dev)
+            t.qrows.kind = _lib.Q_LOGITS_BF16 if ql.dtype == torch.bfloat16 else _lib.Q_LOGITS_F32
+            t.qrows.rows, t.qrows.q, t.qrows.ld, t.qrows.temperature = len(qlog), ql.data_ptr(), ql.stride(0), tt.data_ptr()
+            keep += [ql, tt]
+        ld = int(emit_ld or max(sizes))
+        e_len = torch.empty(len(reqs), dtype=torch.int32, device=dev)
+        e_tok = torch.empty((len(reqs), ld), dtype=torch.int32, device=dev)
+        e_node = torch.empty((len(reqs), ld), dtype=torch.int32, device=dev)
+        e_st = torch.empty(len(reqs), dtype=torch.int32, device=dev)
+        o = _lib.TreeOut()
+        o.size = C.sizeof(_lib.TreeOut)
+        o.emit_len, o.emit_tokens, o.emit_nodes, o.emit_ld = e_len.data_ptr(), e_tok.data_ptr(), e_node.data_ptr(), ld
+        o.status = e_st.data_ptr()
+        self.dev, self.b, self.t, self.o, self.keep = dev, b, t, o, keep
+        self.e_len, self.e_tok, self.e_node, self.e_st = e_len, e_tok, e_node, e_st
+        self.ld, self.anchors, self.n_req, self.nodes, self.vocab = ld, anchors, len(reqs), nodes, v
 
 
 def _as_row(x, u, dev):

@@ -242,35 +242,41 @@ def test_deep_slots_overflow_to_exact(ge, gpu):
     assert (paths == ge._lib.PATH_EXACT).sum() >= 1, paths
 
 
-def test_mask_batch_one_copy_matches_row_masks(ge, gpu):
-    """Grammar masks straight to the device (one pinned buffer, one copy): the tokens, probabilities of the kept
-    tokens and processed logits equal those of the same masks passed row by row (bool and packed), which the oracle
-    pins in the tests above; rows left unfilled sample unmasked."""
+def test_mask_batch_one_copy_matches_oracle(ge, gpu):
+    """Grammar masks straight to the device (one pinned buffer, one copy; engine.py:272-273 applies each row's mask
+    before sampling, grammar.py:42-45 unpacks it): tokens and processed logits equal the oracle's on the same logits and
+    masks; rows left unfilled sample unmasked; a buffer sized for more rows than the call serves its first rows."""
     rng = np.random.default_rng(11)
     n, v = 12, 20000
-    x = torch.from_numpy((rng.standard_normal((n, v)) * 2.0).astype(np.float32)).to(gpu)
+    xn = (rng.standard_normal((n, v)) * 2.0).astype(np.float32)
+    x = torch.from_numpy(xn).to(gpu)
     params = [_P(ge, temperature=0.8 if i % 3 else 0.0, top_p=0.9, top_k=50 if i % 2 else 0) for i in range(n)]
     seeds, idxs = list(range(100, 100 + n)), [3] * n
     masks = [(rng.random(v) < 0.3) if i < 8 else None for i in range(n)]
-    mb = ge.grammar.MaskBatch(n, v)
+    mb = ge.grammar.MaskBatch(n + 5, v)
     assert mb.host.is_pinned()
     for i in range(8):
         if i % 2:
             mb.set(i, masks[i])
         else:
             mb.set(i, ge.grammar.pack(masks[i]))
-    want = ge.sampling.sample_ex(x, params, seeds, idxs, masks, processed=True)
+    mb.set(n + 2, np.zeros(v, dtype=bool))  # a row past the call's rows: not read
     got = ge.sampling.sample_ex(x, params, seeds, idxs, mb, processed=True)
     torch.cuda.synchronize()
-    assert want.tolist() == got.tolist()
-    assert torch.equal(want.processed, got.processed)
-    for i in range(8):
-        assert bool(masks[i][want.tolist()[i]])
-    # the same buffer refilled for a second step (fewer rows filled)
+    want = ora.sample_full(xn, params, seeds, idxs, masks)
+    assert got.tolist() == [w["token"] for w in want]
+    proc = got.processed.cpu().numpy()
+    for i in range(n):
+        assert np.array_equal(proc[i].view(np.uint32), want[i]["processed"].view(np.uint32)), i
+        if i < 8:
+            assert bool(masks[i][got.tolist()[i]])
+    # the same buffer refilled for a second step with fewer rows filled and fewer rows sampled
     mb.reset()
     mb.set(1, masks[1])
-    masks2 = [masks[1] if i == 1 else None for i in range(n)]
-    assert ge.sampling.sample(x, params, seeds, idxs, mb) == ge.sampling.sample(x, params, seeds, idxs, masks2)
+    m2 = 6
+    masks2 = [masks[1] if i == 1 else None for i in range(m2)]
+    got2 = ge.sampling.sample(x[:m2], params[:m2], seeds[:m2], idxs[:m2], mb)
+    assert got2 == ora.sample(xn[:m2], params[:m2], seeds[:m2], idxs[:m2], masks2)
 
 
 def test_logits_borrowed_not_copied(ge, gpu, monkeypatch):
