@@ -124,11 +124,14 @@ int check_batch(gse_handle *h, const gse_batch &b) {
 }
 
 // Parts per row for the main pass: each at most PTOK tokens, a multiple of PCHUNK long, and enough of them over the
-// batch to give every CU about four workgroups. rows * parts <= rows * (ceil(vocab / PTOK) + 1) + target.
+// batch to give every CU about four workgroups, as long as a part keeps at least PMIN tokens.
+// rows * parts <= rows * (ceil(vocab / PTOK) + 1) + target.
 void parts(const gse_handle *h, uint32_t rows, uint32_t vocab, int *nparts, int *plen) {
   const uint32_t nck = (vocab + gse::PCHUNK - 1) / gse::PCHUNK;
   uint32_t np = (vocab + gse::PTOK - 1) / gse::PTOK;
-  const uint32_t want = (h->target + rows - 1) / rows;
+  uint32_t want = (h->target + rows - 1) / rows;
+  const uint32_t cap = vocab / gse::PMIN > 1u ? vocab / gse::PMIN : 1u;
+  if (want > cap) want = cap;
   if (want > np) np = want;
   if (np > (uint32_t)gse::MAXP) np = gse::MAXP;
   if (np > nck) np = nck;

@@ -48,6 +48,8 @@ constexpr int PWAVES = 4;   // waves per part workgroup
 constexpr int MAXP = 64;    // parts per row
 constexpr int PTOK = 40960; // tokens per part, at most
 constexpr int PCHUNK = 1024;  // part lengths are multiples of this (one wave chunk)
+constexpr int PMIN = 8192;    // tokens per part, at least, when a small batch is split to fill the device: every part
+                              // lists its own candidates, so more parts make a longer row resolve
 
 // One per (row, part), written by the part's workgroup with agent-scope stores, read by the row's resolve.
 struct SliceRec {    // 64 bytes
