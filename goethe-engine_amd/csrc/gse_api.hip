@@ -32,6 +32,7 @@ struct gse_handle {
   int32_t *ttok = nullptr;            // [max_rows] sampled tokens of the verify round's selection pass
   gse::TreeNode *tstate = nullptr;    // [max_rows]
   gse::Fx *npart = nullptr;           // [max_rows][GSE_MAX_KIDS + 1][nsl]
+  uint64_t *tseg = nullptr;           // [max_rows][nsl][2 * 128]
   int32_t *nlast = nullptr;           // [max_rows][GSE_MAX_KIDS + 1][nsl]
   double *qmax = nullptr;             // [max_rows][nsl]
   gse::Fx *qpart = nullptr;           // [max_rows][nsl]
@@ -198,6 +199,7 @@ void carve(gse_handle *h, void *block, const gse::Layout &L, bool tree) {
   h->ttok = (int32_t *)(b + L.ttok);
   h->tstate = (gse::TreeNode *)(b + L.tstate);
   h->npart = (gse::Fx *)(b + L.npart);
+  h->tseg = (uint64_t *)(b + L.tseg);
   h->nlast = (int32_t *)(b + L.nlast);
   h->qmax = (double *)(b + L.qmax);
   h->qpart = (gse::Fx *)(b + L.qpart);
@@ -431,6 +433,7 @@ GSE_API int gse_verify_tree(gse_handle *h, const gse_batch *in, const gse_tree *
   L.sampled = h->ttok;
   L.st = h->tstate;
   L.npart = h->npart;
+  L.tseg = h->tseg;
   L.nlast = h->nlast;
   L.qmax = h->qmax;
   L.qpart = h->qpart;

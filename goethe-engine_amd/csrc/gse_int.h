@@ -167,6 +167,7 @@ struct TreeLaunch {
   TreeNode *st;
   Fx *npart;
   int32_t *nlast;
+  uint64_t *tseg;
   double *qmax;
   Fx *qpart;
   QFin *qfin;
@@ -187,7 +188,7 @@ struct PickLaunch {
 // counters and flags zero between calls). tree: with the buffers of verify rounds and drafter picks.
 struct Layout {
   size_t rec, cand, info, done, dctl, dslot, dhist, dlist;
-  size_t ttok, tstate, npart, nlast, qmax, qpart, qfin, pmax, ppart, plast, ptop, ptick;
+  size_t ttok, tstate, npart, nlast, tseg, qmax, qpart, qfin, pmax, ppart, plast, ptop, ptick;
   size_t total;
   uint32_t nrec, nsl, slots;
 };
@@ -219,6 +220,7 @@ constexpr Layout plan_layout(uint32_t R, uint32_t V, uint32_t target, bool tree)
     L.tstate = put((size_t)R * sizeof(TreeNode));
     L.npart = put((size_t)R * K * S * sizeof(Fx));
     L.nlast = put((size_t)R * K * S * sizeof(int32_t));
+    L.tseg = put((size_t)R * S * 2 * (CH / 64) * sizeof(uint64_t));  // the last residual's 64-token segment sums
     L.qmax = put((size_t)R * S * sizeof(double));
     L.qpart = put((size_t)R * S * sizeof(Fx));
     L.qfin = put((size_t)R * sizeof(QFin));

@@ -21,6 +21,8 @@
 // Pick. t == 0: the n largest tokens in stable descending order (ties to the lowest id), per slice then merged by the
 // row's last slice. t > 0: the maximum of z = x / t, the exact mass E = sum(exp(z - M)) in fixed point per slice, then
 // one workgroup per draw k finds the first index whose inclusive prefix reaches uniform(mix(seed, 2^42 + k), at) * E.
+#include <type_traits>
+
 #include "gse_rowctx.h"
 
 namespace gse {
@@ -89,22 +91,67 @@ __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t *red) {
   return m;
 }
 
+// ---- per-slice partials, read by one wave (lane l takes slices l, l + 64, ...: every load of a round at once) ------
+
+// The exact total of the fixed-point partials p[0, n) (every lane gets it).
+template <typename LD>
+__device__ __forceinline__ Fx wave_fx_total(int n, LD ld) {
+  Fx t = fx_zero();
+  for (int j = lane_id(); j < n; j += WAVE) t = fx_add(t, ld(j));
+  return Fx{wave_sum_u64(t.hi), wave_sum_u64(t.lo)};
+}
+
+// The first j whose inclusive prefix of the partials reaches thr, with the exact prefix before it (every lane gets
+// them); when none does, n - 1 with the total of all n.
+template <typename LD>
+__device__ __forceinline__ int wave_fx_cross(int n, double thr, LD ld, Fx &before) {
+  const int ln = lane_id();
+  Fx run = fx_zero();
+  for (int j0 = 0; j0 < n; j0 += WAVE) {
+    const int j = j0 + ln;
+    const Fx v = j < n ? ld(j) : fx_zero();
+    const uint64_t ih = wave_incl_scan_u64(v.hi), il = wave_incl_scan_u64(v.lo);
+    const Fx inc = fx_add(run, Fx{ih, il});
+    const uint64_t hit = ballot64(j < n && fx_val(inc) >= thr);
+    if (hit) {
+      const int l = __builtin_ctzll(hit);
+      before = Fx{shfl_u64(inc.hi - v.hi, l), shfl_u64(inc.lo - v.lo, l)};
+      return j0 + l;
+    }
+    run = fx_add(run, Fx{shfl_u64(ih, WAVE - 1), shfl_u64(il, WAVE - 1)});
+  }
+  before = run;
+  return n - 1;
+}
+
+__device__ __forceinline__ double wave_max_f64(double v) {
+  return lane63(wave_scan(v, (double)-INFINITY, [](double x, double y) { return fmax(x, y); }));
+}
+
 // ---- q rows: softmax(x / t) of drafter logits, or fp64 probability rows -------------------------------------------
 
 struct QRow {
   int kind;
   const char *base;
-  double t, M, E;  // logits: z = x / t, M = max z, E = sum exp(z - M) (exact fixed point)
+  bool t1;                // t == 1: z = x
+  double t, M, invE;      // logits: z = x / t, M = max z, invE = 1 / sum exp(z - M)
 };
 
-__device__ __forceinline__ double qz(const QRow &q, int i) {
-  const double x = q.kind == GSE_Q_LOGITS_BF16 ? (double)bf16_to_f32(((const uint16_t *)q.base)[i])
-                                                : (double)((const float *)q.base)[i];
-  return x / q.t;
-}
-__device__ __forceinline__ double q_at(const QRow &q, int i) {
+// The raw value of token i (the probability, or the logit widened to fp64).
+__device__ __forceinline__ double q_raw(const QRow &q, int i) {
   if (q.kind == GSE_Q_PROB) return ((const double *)q.base)[i];
-  return exp(qz(q, i) - q.M) / q.E;
+  if (q.kind == GSE_Q_LOGITS_BF16) return (double)bf16_to_f32(((const uint16_t *)q.base)[i]);
+  return (double)((const float *)q.base)[i];
+}
+// q at a token from its raw value: the probability, or exp(z - M) / E (every evaluation of one row takes this same
+// path, so the sums and the tests of a round see one set of values).
+__device__ __forceinline__ double q_of_raw(const QRow &q, double r, const double *etab) {
+  if (q.kind == GSE_Q_PROB) return r;
+  const double z = q.t1 ? r : r / q.t;
+  return exp_nonpos(z - q.M, etab) * q.invE;
+}
+__device__ __forceinline__ double q_at(const QRow &q, int i, const double *etab) {
+  return q_of_raw(q, q_raw(q, i), etab);
 }
 
 // ---- the dist() of a node's target row: p0_i = keep_i e_i / C -----------------------------------------------------
@@ -115,13 +162,210 @@ struct Tgt {
   uint64_t kkeep;  // packed key of the last kept rank (0: every token with z > -inf is kept)
 };
 
-__device__ __forceinline__ double tgt_e(const Tgt &g, int t, uint32_t cnt) {
+// keep_i e_i of token t from its raw logit x, its mask word and its history count.
+__device__ __forceinline__ double tgt_e(const Tgt &g, int t, float x, uint32_t mword, uint32_t cnt,
+                                        const double *etab) {
   bool fn = false, ff = false;
   float xm;
-  const uint32_t k = elem_key(g.c, load_one(g.c, t), cnt, mask_bit(g.c, t), fn, ff, xm);
+  const uint32_t k = elem_key(g.c, x, cnt, (mword >> (t & 31)) & 1u, fn, ff, xm);
   if (k <= KEY_NEGINF || pack(k, (uint32_t)t) < g.kkeep) return 0.0;
-  return exp((double)fkey_inv(k) - g.M);
+  return exp_nonpos((double)fkey_inv(k) - g.M, etab);
 }
+__device__ __forceinline__ uint32_t mask_word(const RowCtx &c, int t) { return c.mw ? c.mw[t >> 5] : 0xFFFFFFFFu; }
+__device__ __forceinline__ double tgt_e_at(const Tgt &g, int t, uint32_t cnt, const double *etab) {
+  return tgt_e(g, t, load_one(g.c, t), mask_word(g.c, t), cnt, etab);
+}
+
+// The same weight for the streaming loops, with the division by the temperature chosen at compile time (a live node
+// is never greedy, so z is x / T or x): the value tgt_e gives, with fewer instructions.
+template <bool DIV>
+__device__ __forceinline__ double tgt_w(const Tgt &g, int t, float x, uint32_t mword, uint32_t cnt,
+                                        const double *etab) {
+  if (cnt) x = penalize(x, cnt, g.c.rp, g.c.fp, g.c.pp);
+  const float z = DIV ? div_rn(x, g.c.T, g.c.Td, g.c.Rd) : x;
+  if (!((mword >> (t & 31)) & 1u) || !(z > -INFINITY)) return 0.0;
+  if (g.kkeep && pack(fkey(z), (uint32_t)t) < g.kkeep) return 0.0;
+  return exp_nonpos((double)z - g.M, etab);
+}
+
+// q from its raw value with its kind chosen at compile time: QK 0 probabilities, 1 logits with t == 1, 2 logits with
+// another t (the value q_of_raw gives).
+template <int QK>
+__device__ __forceinline__ double q_w(const QRow &q, double r, const double *etab) {
+  if constexpr (QK == 0) {
+    return r;
+  } else {
+    const double z = QK == 1 ? r : r / q.t;
+    return exp_nonpos(z - q.M, etab) * q.invE;
+  }
+}
+
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
+};
+template <int N>
+struct IntC {
+  static constexpr int value = N;
+};
+template <typename F>
+__device__ __forceinline__ void with_bool(bool d, F f) {
+  if (d) f(BoolC<true>{});
+  else f(BoolC<false>{});
+}
+template <typename F>
+__device__ __forceinline__ void with_div(bool d, F f) {
+  with_bool(d, f);
+}
+
+// ---- streaming a slice --------------------------------------------------------------------------------------------
+// Thread tid takes the groups g < NG of its slice, group g holding the tokens t_e = s0 + g * 4 TT + e * TT + tid,
+// e < 4 (each of the four loads of a group is one coalesced 256-token read per wave). The loop over the groups stays
+// rolled (it is the kernel's hot code) and its loads run QD groups ahead. The loads go through buffer resources: no
+// branch around a load (a load in a branch is waited for where the branch joins), and a token past the row reads 0.
+constexpr int NG = TS / (4 * TT);  // groups per thread per slice
+constexpr int Q_NONE = 3;          // q loader kind of a node whose kids are all one-hot (GSE_Q_* otherwise)
+
+__device__ const uint32_t ALL_ALLOWED = 0xFFFFFFFFu;  // the mask word of a row without a mask
+
+struct TBuf {                    // a target row's logits and mask words
+  __amdgpu_buffer_rsrc_t x, m;
+  int mstep;                     // bytes per 32 tokens in m: 4, or 0 (the one word ALL_ALLOWED)
+};
+__device__ __forceinline__ TBuf tbuf(const RowCtx &c) {
+  constexpr int FMT = 0x00020000;  // raw 32-bit buffer (GFX9 resource word 3)
+  TBuf b;
+  b.x = __builtin_amdgcn_make_buffer_rsrc((void *)c.base, (short)0, c.V * (c.dtype == GSE_BF16 ? 2 : 4), FMT);
+  b.m = __builtin_amdgcn_make_buffer_rsrc(c.mw ? (void *)c.mw : (void *)&ALL_ALLOWED, (short)0,
+                                          c.mw ? (c.V + 31) / 32 * 4 : 4, FMT);
+  b.mstep = c.mw ? 4 : 0;
+  return b;
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t qbuf(const QRow &q, int V) {
+  const int es = q.kind == GSE_Q_PROB ? 8 : q.kind == GSE_Q_LOGITS_BF16 ? 2 : 4;
+  return __builtin_amdgcn_make_buffer_rsrc((void *)q.base, (short)0, V * es, 0x00020000);
+}
+
+template <int DT>
+__device__ __forceinline__ float ld_x(const TBuf &b, int t) {
+  if constexpr (DT == GSE_BF16) {
+    return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(b.x, t * 2, 0, 0));
+  } else {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(b.x, t * 4, 0, 0));
+  }
+}
+__device__ __forceinline__ uint32_t ld_m(const TBuf &b, int t) {
+  return __builtin_amdgcn_raw_buffer_load_b32(b.m, (t >> 5) * b.mstep, 0, 0);
+}
+// A q value as loaded: a probability (fp64), or a logit (f32, exact for bf16 too); widened by the caller.
+template <int QL>
+using QRaw = typename std::conditional<QL == GSE_Q_PROB, double, float>::type;
+template <int QL>
+__device__ __forceinline__ QRaw<QL> ld_q(__amdgpu_buffer_rsrc_t q, int t) {
+  if constexpr (QL == GSE_Q_PROB) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(q, t * 8, 0, 0);
+    return __longlong_as_double((long long)(((uint64_t)v[1] << 32) | v[0]));
+  } else if constexpr (QL == GSE_Q_LOGITS_BF16) {
+    return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(q, t * 2, 0, 0));
+  } else if constexpr (QL == GSE_Q_LOGITS_F32) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(q, t * 4, 0, 0));
+  } else {
+    return 0.0f;
+  }
+}
+
+template <int DT, int QL>
+struct Grp {  // one group's loads: target logits and mask words, and q values (QL != Q_NONE)
+  float x[4];
+  uint32_t mw[4];
+  QRaw<QL> q[QL == Q_NONE ? 1 : 4];
+};
+template <int DT, int QL>
+__device__ __forceinline__ Grp<DT, QL> ld_grp(const TBuf &b, __amdgpu_buffer_rsrc_t qb, int t0) {
+  Grp<DT, QL> r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int t = t0 + e * TT;
+    r.x[e] = ld_x<DT>(b, t);
+    r.mw[e] = ld_m(b, t);
+    if constexpr (QL != Q_NONE) r.q[e] = ld_q<QL>(qb, t);
+  }
+  return r;
+}
+// q values only (the q rows' statistics)
+template <int QL>
+struct QGrp {
+  QRaw<QL> q[4];
+};
+template <int QL>
+__device__ __forceinline__ QGrp<QL> ld_qgrp(__amdgpu_buffer_rsrc_t qb, int t0) {
+  QGrp<QL> r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r.q[e] = ld_q<QL>(qb, t0 + e * TT);
+  return r;
+}
+
+// f(t0, group) for the thread's groups of slice s0 (token t0 + e TT is element e). Four groups are in registers: the
+// loop is unrolled by four so that each one is reloaded in place after its use (a copy of a register whose load is
+// still in flight would wait for the load), so every group is loaded three groups ahead of its use.
+template <typename Ld, typename F>
+__device__ __forceinline__ void slice_groups(int s0, Ld ld, F f) {
+  static_assert(NG % 4 == 0, "");
+  const int tid = threadIdx.x;
+  auto t0_of = [&](int g) { return s0 + min(g, NG - 1) * 4 * TT + tid; };  // (past the end: the last group again)
+  auto b0 = ld(t0_of(0));
+  auto b1 = ld(t0_of(1));
+  auto b2 = ld(t0_of(2));
+  auto b3 = ld(t0_of(3));
+#pragma unroll 1
+  for (int g = 0; g < NG; g += 4) {
+    f(t0_of(g), b0);
+    b0 = ld(t0_of(g + 4));
+    f(t0_of(g + 1), b1);
+    b1 = ld(t0_of(g + 5));
+    f(t0_of(g + 2), b2);
+    b2 = ld(t0_of(g + 6));
+    f(t0_of(g + 3), b3);
+    b3 = ld(t0_of(g + 7));
+  }
+}
+
+// tgt_w with the division chosen at run time (one uniform test per token).
+__device__ __forceinline__ double tgt_wr(const Tgt &g, int t, float x, uint32_t mword, uint32_t cnt,
+                                         const double *etab) {
+  if (cnt) x = penalize(x, cnt, g.c.rp, g.c.fp, g.c.pp);
+  float z = x;
+  if (g.c.divide) z = div_rn(x, g.c.T, g.c.Td, g.c.Rd);
+  if (!((mword >> (t & 31)) & 1u) || !(z > -INFINITY)) return 0.0;
+  if (g.kkeep && pack(fkey(z), (uint32_t)t) < g.kkeep) return 0.0;
+  return exp_nonpos((double)z - g.M, etab);
+}
+
+// A node's q variant: 0 no q row (every kid one-hot), 1 probabilities, 2 / 3 f32 logits with t == 1 / another t,
+// 4 / 5 bf16 logits likewise; its loader kind and its q_w kind.
+template <int QKK, typename F>
+__device__ __forceinline__ void with_qv(bool has_q, bool t1, F f) {
+  if (!has_q) {
+    f(IntC<0>{});
+  } else if constexpr (QKK == GSE_Q_PROB) {
+    f(IntC<1>{});
+  } else if constexpr (QKK == GSE_Q_LOGITS_F32) {
+    if (t1) f(IntC<2>{});
+    else f(IntC<3>{});
+  } else if constexpr (QKK == GSE_Q_LOGITS_BF16) {
+    if (t1) f(IntC<4>{});
+    else f(IntC<5>{});
+  } else {
+    f(IntC<0>{});
+  }
+}
+constexpr int ql_of(int qv) {
+  return qv == 0 ? Q_NONE : qv == 1 ? (int)GSE_Q_PROB : qv <= 3 ? (int)GSE_Q_LOGITS_F32 : (int)GSE_Q_LOGITS_BF16;
+}
+constexpr int qk_of(int qv) { return qv == 0 ? 3 : qv == 1 ? 0 : (qv == 2 || qv == 4) ? 1 : 2; }
+
+// The streaming kernels are compiled per logits type DTK and per q kind QKK of the call (GSE_Q_*, or Q_NONE when
+// the call has no q rows): launch_tree picks the instance.
 
 // History count of token x in the row (every thread of the block calls it; all get the count).
 __device__ __forceinline__ uint32_t hist_count(const RowCtx &c, const int32_t *hist, int x, uint32_t *red) {
@@ -136,11 +380,16 @@ struct TreeShared {
   uint64_t seg[2 * TSEG];      // segment sums (Fx hi, lo)
   uint64_t red[16];
   double redd[8];
+  double etab[64];             // 2^(k/64), the table of exp_nonpos
   int redi[8];
   uint32_t redu[8];
   uint32_t ticket;
   int found;
 };
+
+__device__ __forceinline__ void load_etab(TreeShared &sh) {
+  if (threadIdx.x < 64) sh.etab[threadIdx.x] = EXP2_64[threadIdx.x];
+}
 
 // Kids of node u in draft order: rows j > u with parent[j] == u, up to the next anchor (parent -1).
 struct Kids {
@@ -164,58 +413,82 @@ struct TreeArgs {
   TreeNode *st;            // [nodes]
   Fx *npart;               // [nodes][GSE_MAX_KIDS + 1][nsl]
   int32_t *nlast;          // [nodes][GSE_MAX_KIDS + 1][nsl]
-  double *qmax;            // [qrows][nsl]
-  Fx *qpart;               // [qrows][nsl]
+  uint64_t *tseg;          // [nodes][nsl][2 TSEG]: segment sums {hi, lo} of the residual the node draws from
+  double *qmax;            // [qrows][nsl] slice maxima of z
+  Fx *qpart;               // [qrows][nsl] slice masses exp(z - slice maximum)
   QFin *qfin;              // [qrows]
   gse_tree_out out;
 };
 
+// Kids of node u found by one wave: lanes read 64 rows after u at a time, the kids (parent u) before the first row of
+// another request (parent -1) are appended in row order by lane 0 of the wave.
 __device__ __forceinline__ void find_kids(const TreeArgs &a, int u, Kids &k) {
-  k.n = 0;
-  k.nq = 0;
-  k.over = false;
-  for (int j = u + 1; j < a.nodes; ++j) {
-    const int pj = a.parent[j];
-    if (pj < 0) break;
-    if (pj != u) continue;
-    if (k.n >= a.max_kids || k.n >= GSE_MAX_KIDS) {
-      k.over = true;
-      break;
-    }
-    k.row[k.n] = j;
-    k.tok[k.n] = a.token[j];
-    const int qr = a.qrow ? a.qrow[j] : -1;
-    int qs = -1;
-    if (qr >= 0 && qr < (int)a.q.rows) {
-      for (int m = 0; m < k.nq; ++m)
-        if (k.qrow[m] == qr) qs = m;
-      if (qs < 0) {
-        qs = k.nq++;
-        k.qrow[qs] = qr;
+  const int ln = lane_id();
+  if (ln == 0) {
+    k.n = 0;
+    k.nq = 0;
+    k.over = false;
+  }
+  for (int base = u + 1; base < a.nodes; base += WAVE) {
+    const int j = base + ln;
+    const int pj = j < a.nodes ? a.parent[j] : -1;
+    const bool kid = pj == u;
+    const int tok = kid ? a.token[j] : 0;
+    const int qr = kid && a.qrow ? a.qrow[j] : -1;
+    const uint64_t endm = ballot64(pj < 0);
+    const uint64_t before_end = endm ? (endm & (0ull - endm)) - 1ull : ~0ull;
+    uint64_t km = ballot64(kid) & before_end;
+    while (km) {  // (uniform: every lane follows, lane 0 writes)
+      const int l = __builtin_ctzll(km);
+      km &= km - 1ull;
+      const int tk = __shfl(tok, l, WAVE), q = __shfl(qr, l, WAVE);
+      if (ln == 0) {
+        if (k.n >= a.max_kids || k.n >= GSE_MAX_KIDS) {
+          k.over = true;
+        } else {
+          int qs = -1;
+          if (q >= 0 && q < (int)a.q.rows) {
+            for (int m = 0; m < k.nq; ++m)
+              if (k.qrow[m] == q) qs = m;
+            if (qs < 0) {
+              qs = k.nq++;
+              k.qrow[qs] = q;
+            }
+          }
+          k.row[k.n] = base + l;
+          k.tok[k.n] = tk;
+          k.qs[k.n] = qs;
+          ++k.n;
+        }
       }
     }
-    k.qs[k.n] = qs;
-    ++k.n;
+    if (endm) break;
   }
+}
+
+__device__ __forceinline__ const char *qbase(const TreeArgs &a, int qr) {
+  const size_t es = a.q.kind == GSE_Q_PROB ? 8 : a.q.kind == GSE_Q_LOGITS_BF16 ? 2 : 4;
+  return (const char *)a.q.q + (size_t)qr * (size_t)a.q.ld * es;
 }
 
 __device__ __forceinline__ QRow qrow_of(const TreeArgs &a, int qr) {
   QRow q;
   q.kind = (int)a.q.kind;
-  const size_t es = a.q.kind == GSE_Q_PROB ? 8 : a.q.kind == GSE_Q_LOGITS_BF16 ? 2 : 4;
-  q.base = (const char *)a.q.q + (size_t)qr * (size_t)a.q.ld * es;
+  q.base = qbase(a, qr);
   q.t = a.q.kind == GSE_Q_PROB ? 1.0 : a.q.temperature[qr];
+  q.t1 = q.t == 1.0;
   q.M = a.qfin[qr].M;
-  q.E = a.qfin[qr].E;
+  q.invE = 1.0 / a.qfin[qr].E;
   return q;
 }
 
-// The chain of residuals at token i (spec.py:95-102): p_0 = p0; res_{r+1} = max(p_r - q_r, 0) (one-hot kid: p_r with
-// the kid's token set to 0); p_{r+1} = res_{r+1} / sig[r + 1], or p_r when that total is 0. Returns res_d (norm false)
-// or p_d (norm true); d == 0 returns p0. The kids' q values are formed as the chain needs them (kids that share a q row,
-// as SpecInfer's do, share one evaluation).
-__device__ __forceinline__ double chain(const Kids &k, const QRow *qr, double p0, int i, const double *sig, int d,
-                                        bool norm) {
+// The chain of residuals at one token (spec.py:95-102): p_0 = p0; res_{r+1} = max(p_r - q_r, 0) (one-hot kid: p_r with
+// the kid's token set to 0); p_{r+1} = res_{r+1} / sig[r + 1] (a product by isig[r + 1] = 1 / sig[r + 1]), or p_r when
+// that total is 0. Returns res_d (norm false) or p_d (norm true); d == 0 returns p0. qf(m) gives the node's distinct q
+// row m at the token (called once per run of kids that share it, as SpecInfer's kids do).
+template <typename QF>
+__device__ __forceinline__ double chain(const Kids &k, QF qf, double p0, int i, const double *sig, const double *isig,
+                                        int d, bool norm) {
   double p = p0;
   int qid = -2;
   double qv = 0.0;
@@ -226,38 +499,132 @@ __device__ __forceinline__ double chain(const Kids &k, const QRow *qr, double p0
     } else {
       if (k.qs[r] != qid) {
         qid = k.qs[r];
-        qv = q_at(qr[qid], i);
+        qv = qf(qid);
       }
       res = fmax(p - qv, 0.0);
     }
-    const double pn = sig[r + 1] > 0.0 ? res / sig[r + 1] : p;
+    const double pn = sig[r + 1] > 0.0 ? res * isig[r + 1] : p;
     if (r == d - 1) return norm ? pn : res;
     p = pn;
   }
   return p;
 }
 
-// The node's p0 at one token (every thread calls; all get it).
-__device__ __forceinline__ double p0_at(const TreeArgs &a, const Tgt &g, int x, double clast, TreeShared &sh) {
-  const uint32_t cnt = hist_count(g.c, a.s.hist, x, sh.redu);
-  return tgt_e(g, x, cnt) / clast;
+// The first two chain levels in registers, for nodes whose kids share at most one q row (the usual tree): chain_r<D>
+// gives chain(...) for d = D <= 2 with qv the shared row's value at the token, in the same operations.
+struct ChainR {
+  int qs[2], tok[2];
+  double sig[3], isig[3];
+};
+template <int D>
+__device__ __forceinline__ double chain_r(const ChainR &c, double qv, double p0, int i, bool norm) {
+  static_assert(D >= 1 && D <= 2, "");
+  double p = p0;
+#pragma unroll
+  for (int r = 0; r < D; ++r) {
+    const double res = c.qs[r] < 0 ? (i == c.tok[r] ? 0.0 : p) : fmax(p - qv, 0.0);
+    const double pn = c.sig[r + 1] > 0.0 ? res * c.isig[r + 1] : p;
+    if (r == D - 1) return norm ? pn : res;
+    p = pn;
+  }
+  return p;
 }
 
-// The first index of slice [s0, s1) whose inclusive prefix of the weights wfn (after `before`, the exact mass of the
-// slices ahead) reaches thr; -1 if none. Exact fixed-point prefixes: 64-token segment sums (wave w takes segments w,
-// w + 4, ...), the crossing segment, then its weights again and their scan. Every thread gets the result.
-template <typename W>
-__device__ int slice_find(int s0, int s1, Fx before, double thr, W wfn, TreeShared &sh) {
+// A node's uniform data for one workgroup, in LDS: its kids, their q rows, the residual totals and their inverses.
+struct NodeShared {
+  Kids k;
+  QRow qr[GSE_MAX_KIDS];
+  double sig[GSE_MAX_KIDS + 1];
+  double isig[GSE_MAX_KIDS + 1];
+  double clast, iclast;
+};
+
+// chain_r for a chain depth d of 1 or 2 known at run time.
+__device__ __forceinline__ double chain_rd(const ChainR &c, double qv, double p0, int i, int d, bool norm) {
+  const double res1 = c.qs[0] < 0 ? (i == c.tok[0] ? 0.0 : p0) : fmax(p0 - qv, 0.0);
+  const double p1 = c.sig[1] > 0.0 ? res1 * c.isig[1] : p0;
+  if (d == 1) return norm ? p1 : res1;
+  const double res2 = c.qs[1] < 0 ? (i == c.tok[1] ? 0.0 : p1) : fmax(p1 - qv, 0.0);
+  const double p2 = c.sig[2] > 0.0 ? res2 * c.isig[2] : p1;
+  return norm ? p2 : res2;
+}
+
+__device__ __forceinline__ ChainR chain_regs(const NodeShared &ns) {
+  ChainR c;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    c.qs[r] = r < ns.k.n ? ns.k.qs[r] : -1;
+    c.tok[r] = r < ns.k.n ? ns.k.tok[r] : -1;
+  }
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+    c.sig[r] = ns.sig[r];
+    c.isig[r] = ns.isig[r];
+  }
+  return c;
+}
+
+// The node's p0 at one token (every thread calls; all get it).
+__device__ __forceinline__ double p0_at(const TreeArgs &a, const Tgt &g, int x, const NodeShared &ns,
+                                        TreeShared &sh) {
+  const uint32_t cnt = hist_count(g.c, a.s.hist, x, sh.redu);
+  return tgt_e_at(g, x, cnt, sh.etab) * ns.iclast;
+}
+
+// The 64-token segment sums of slice [s0, s1) into sh.seg (see slice_find).
+template <typename LD, typename EV>
+__device__ __forceinline__ void slice_segs(int s0, int s1, LD ld, EV ev, TreeShared &sh) {
+  constexpr int NS = TSEG / (TT / WAVE);  // segments per wave
   const int tid = threadIdx.x;
   const int wv = tid >> 6, ln = lane_id();
-  for (int g = wv; g < TSEG; g += TT / WAVE) {
-    const int i = s0 + g * WAVE + ln;
-    const Fx f = fx_of(i < s1 ? wfn(i) : 0.0);
+  auto tok = [&](int j) { return s0 + (j * (TT / WAVE) + wv) * WAVE + ln; };  // this lane's token of segment j
+  auto load = [&](int j) {
+    const int i = tok(j);
+    return ld(i < s1 ? i : s0);
+  };
+  auto seg = [&](int j, const auto &r) {
+    const int i = tok(j), g = j * (TT / WAVE) + wv;
+    const Fx f = fx_of(i < s1 ? ev(i, r) : 0.0);
     const uint64_t hi = wave_sum_u64(f.hi), lo = wave_sum_u64(f.lo);
     if (ln == 0) {
       sh.seg[2 * g] = hi;
       sh.seg[2 * g + 1] = lo;
     }
+  };
+  // four segments in registers, each reloaded in place after its use (see slice_groups)
+  auto r0 = load(0);
+  auto r1 = load(1);
+  auto r2 = load(2);
+  auto r3 = load(3);
+#pragma unroll 1
+  for (int j = 0; j < NS; j += 4) {
+    seg(j, r0);
+    r0 = load(min(j + 4, NS - 1));
+    seg(j + 1, r1);
+    r1 = load(min(j + 5, NS - 1));
+    seg(j + 2, r2);
+    r2 = load(min(j + 6, NS - 1));
+    seg(j + 3, r3);
+    r3 = load(min(j + 7, NS - 1));
+  }
+}
+
+// The first index of slice [s0, s1) whose inclusive prefix of the weights (after `before`, the exact mass of the
+// slices ahead) reaches thr; -1 if none. The weight of token i is ev(i, ld(i)): ld does the loads, which run three
+// segments ahead of the weights. Exact fixed-point prefixes: 64-token segment sums (wave w takes segments w, w + 4,
+// ...), the crossing segment, then its weights again and their scan. pre: the slice's segment sums when a pass kept
+// them ({hi, lo} per segment), else null. Every thread gets the result.
+template <typename LD, typename EV>
+__device__ __forceinline__ int slice_find(int s0, int s1, Fx before, double thr, LD ld, EV ev, TreeShared &sh,
+                                          const uint64_t *pre = nullptr) {
+  constexpr int NS = TSEG / (TT / WAVE);  // segments per wave
+  static_assert(NS % 4 == 0 && 2 * TSEG == TT, "");
+  const int tid = threadIdx.x;
+  const int wv = tid >> 6, ln = lane_id();
+  if (pre) {
+    sh.seg[tid] = ld_ag(&pre[tid]);
+  } else {
+    slice_segs(s0, s1, ld, ev, sh);
   }
   if (tid == 0) sh.found = -1;
   __syncthreads();
@@ -276,7 +643,7 @@ __device__ int slice_find(int s0, int s1, Fx before, double thr, W wfn, TreeShar
       const int g = 2 * l + (first ? 0 : 1);
       const Fx gb = first ? Fx{shfl_u64(ex.hi, l), shfl_u64(ex.lo, l)} : Fx{shfl_u64(i0.hi, l), shfl_u64(i0.lo, l)};
       const int i = s0 + g * WAVE + ln;
-      const Fx f = fx_of(i < s1 ? wfn(i) : 0.0);
+      const Fx f = fx_of(i < s1 ? ev(i, ld(i)) : 0.0);
       const uint64_t ch = wave_incl_scan_u64(f.hi), cl = wave_incl_scan_u64(f.lo);
       const uint64_t hb = ballot64(fx_val(fx_add(gb, Fx{ch, cl})) >= thr);
       if (ln == 0) sh.found = hb ? s0 + g * WAVE + __builtin_ctzll(hb) : -1;
@@ -287,6 +654,8 @@ __device__ int slice_find(int s0, int s1, Fx before, double thr, W wfn, TreeShar
   __syncthreads();
   return r;
 }
+
+
 
 // ---- verify: stats --------------------------------------------------------------------------------------------------
 
@@ -305,23 +674,10 @@ __device__ __forceinline__ Tgt tgt_of(const TreeArgs &a, int u, const gse_row &P
   return g;
 }
 
-// Maximum of z = x / t over each slice of each logits q row.
-__global__ __launch_bounds__(TT) void qmax_kernel(TreeArgs a) {
-  __shared__ double red[8];
-  const int s = blockIdx.x, qr = blockIdx.y;
-  QRow q;
-  q.kind = (int)a.q.kind;
-  q.base = (const char *)a.q.q + (size_t)qr * (size_t)a.q.ld * (a.q.kind == GSE_Q_LOGITS_BF16 ? 2 : 4);
-  q.t = a.q.temperature[qr];
-  const int V = a.s.V, s0 = s * TS, s1 = min(V, s0 + TS);
-  double m = -INFINITY;
-  for (int i = s0 + (int)threadIdx.x; i < s1; i += TT) m = fmax(m, qz(q, i));
-  m = block_max_f64(m, red);
-  if (threadIdx.x == 0) a.qmax[(size_t)qr * a.nsl + s] = m;
-}
-
-// Per MSS node: the exact kept mass per slice (the last slice forms C); per logits q row: exp(z - M) per slice (the
-// last slice forms E).
+// Per MSS node: the exact kept mass per slice (the last slice forms C). Per logits q row: the slice maximum m of z and
+// the slice mass exp(z - m) (the last slice forms M = max m and E = sum over slices of mass * exp(m - M), in slice
+// order: within a few ulp of the sum of exp(z - M) over the row).
+template <int DTK, int QKK>
 __global__ __launch_bounds__(TT) void tstats_kernel(TreeArgs a) {
   __shared__ TreeShared sh;
   const int s = blockIdx.x, y = blockIdx.y, tid = threadIdx.x;
@@ -331,15 +687,30 @@ __global__ __launch_bounds__(TT) void tstats_kernel(TreeArgs a) {
     const gse_row P = a.s.params[u];
     if (!node_live(a, u, P)) return;
     const Tgt g = tgt_of(a, u, P);
-    if (g.c.pen) build_counts(g.c, a.s.hist, s0, sh.cnt);
+    load_etab(sh);
+    if (g.c.pen) build_counts(g.c, a.s.hist, s0, sh.cnt);  // (its barriers publish the table)
+    else __syncthreads();
+    const TBuf tb = tbuf(g.c);
+    const uint32_t *cnt = g.c.pen ? sh.cnt : nullptr;
     Fx f = fx_zero();
     int last = -1;
-    for (int k = 0; k < TK; ++k) {
-      const int i = s0 + k * TT + tid;
-      if (i >= s1) break;
-      const double e = tgt_e(g, i, g.c.pen ? sh.cnt[i - s0] : 0u);
-      f = fx_add(f, fx_of(e));
-      if (e > 0.0) last = i;
+    {
+      with_div(g.c.divide, [&](auto dv) {
+        constexpr int DT = DTK;
+        constexpr bool DIV = decltype(dv)::value;
+        slice_groups(s0, [&](int t0) { return ld_grp<DT, Q_NONE>(tb, tb.x, t0); },
+                     [&](int t0, const Grp<DT, Q_NONE> &gr) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int i = t0 + e * TT;
+            if (i < s1) {
+              const double w = tgt_w<DIV>(g, i, gr.x[e], gr.mw[e], cnt ? cnt[i - s0] : 0u, sh.etab);
+              f = fx_add(f, fx_of(w));
+              if (w > 0.0) last = i;
+            }
+          }
+        });
+      });
     }
     f = block_fx_sum(f, sh.red);
     last = block_max_i32(last, sh.redi);
@@ -354,16 +725,18 @@ __global__ __launch_bounds__(TT) void tstats_kernel(TreeArgs a) {
     if (tid == 0) sh.ticket = ticket_add(&a.st[u].ticket);
     __syncthreads();
     if (sh.ticket != (uint32_t)(a.nsl - 1)) return;
-    if (tid == 0) {
-      Fx t = fx_zero();
-      for (int j = 0; j < a.nsl; ++j) t = fx_add(t, Fx{ld_ag(&a.npart[o - s + j].hi), ld_ag(&a.npart[o - s + j].lo)});
-      TreeNode &nd = a.st[u];
-      nd.clast = fx_val(t);
-      nd.sig[0] = nd.clast;
-      nd.next = 1;
-      nd.token = -1;
-      nd.kid = -1;
-      nd.ticket = 0;
+    if (tid < WAVE) {
+      const Fx *pp = a.npart + (o - s);
+      const Fx t = wave_fx_total(a.nsl, [&](int j) { return Fx{ld_ag(&pp[j].hi), ld_ag(&pp[j].lo)}; });
+      if (tid == 0) {
+        TreeNode &nd = a.st[u];
+        nd.clast = fx_val(t);
+        nd.sig[0] = nd.clast;
+        nd.next = 1;
+        nd.token = -1;
+        nd.kid = -1;
+        nd.ticket = 0;
+      }
     }
     return;
   }
@@ -371,19 +744,47 @@ __global__ __launch_bounds__(TT) void tstats_kernel(TreeArgs a) {
   if (a.q.kind == GSE_Q_PROB) return;
   QRow q;
   q.kind = (int)a.q.kind;
-  q.base = (const char *)a.q.q + (size_t)qr * (size_t)a.q.ld * (a.q.kind == GSE_Q_LOGITS_BF16 ? 2 : 4);
+  q.base = qbase(a, qr);
   q.t = a.q.temperature[qr];
-  double M = -INFINITY;
-  for (int j = 0; j < a.nsl; ++j) M = fmax(M, a.qmax[(size_t)qr * a.nsl + j]);
+  q.t1 = q.t == 1.0;
+  const auto qb = qbuf(q, V);
+  // the slice maximum first (z = x / t is monotone in x for t > 0 and rounds once: the maximum of z is the maximum of x
+  // divided once), then the masses (a second read of the slice, from the cache)
+  double xm = -INFINITY;
   Fx f = fx_zero();
-  for (int k = 0; k < TK; ++k) {
-    const int i = s0 + k * TT + tid;
-    if (i >= s1) break;
-    f = fx_add(f, fx_of(exp(qz(q, i) - M)));
+  load_etab(sh);
+  {
+    constexpr int QL = QKK;
+    if constexpr (QL == GSE_Q_LOGITS_F32 || QL == GSE_Q_LOGITS_BF16) {
+      slice_groups(s0, [&](int t0) { return ld_qgrp<QL>(qb, t0); }, [&](int t0, const QGrp<QL> &gr) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (t0 + e * TT < s1) xm = fmax(xm, (double)gr.q[e]);
+      });
+      const double xmax = block_max_f64(xm, sh.redd);  // (its barriers publish the table)
+      const double m = q.t1 ? xmax : xmax / q.t;
+      xm = m;
+      if (m > -INFINITY) {
+        with_bool(q.t1, [&](auto t1c) {
+          constexpr bool T1 = decltype(t1c)::value;
+          slice_groups(s0, [&](int t0) { return ld_qgrp<QL>(qb, t0); }, [&](int t0, const QGrp<QL> &gr) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if (t0 + e * TT < s1) {
+                const double z = T1 ? (double)gr.q[e] : (double)gr.q[e] / q.t;
+                f = fx_add(f, fx_of(exp_nonpos(z - m, sh.etab)));
+              }
+            }
+          });
+        });
+      }
+    }
   }
+  const double m = xm;
   f = block_fx_sum(f, sh.red);
   const size_t o = (size_t)qr * a.nsl + s;
   if (tid == 0) {
+    st_ag(&a.qmax[o], m);
     st_ag(&a.qpart[o].hi, f.hi);
     st_ag(&a.qpart[o].lo, f.lo);
   }
@@ -392,34 +793,48 @@ __global__ __launch_bounds__(TT) void tstats_kernel(TreeArgs a) {
   if (tid == 0) sh.ticket = ticket_add(&a.qfin[qr].ticket);
   __syncthreads();
   if (sh.ticket != (uint32_t)(a.nsl - 1)) return;
-  if (tid == 0) {
-    Fx t = fx_zero();
-    for (int j = 0; j < a.nsl; ++j)
-      t = fx_add(t, Fx{ld_ag(&a.qpart[o - s + j].hi), ld_ag(&a.qpart[o - s + j].lo)});
-    a.qfin[qr].M = M;
-    a.qfin[qr].E = fx_val(t);
-    a.qfin[qr].ticket = 0;
+  if (tid < WAVE) {
+    // M = max of the slice maxima; E = sum of mass_j exp(m_j - M), each lane its slices, then a wave sum in a fixed
+    // order (the same E every call)
+    const double *mq = a.qmax + (o - s);
+    const Fx *pq = a.qpart + (o - s);
+    double M = -INFINITY;
+    for (int j = tid; j < a.nsl; j += WAVE) M = fmax(M, ld_ag(&mq[j]));
+    M = wave_max_f64(M);
+    double E = 0.0;
+    for (int j = tid; j < a.nsl; j += WAVE) {
+      const double mj = ld_ag(&mq[j]);
+      if (mj > -INFINITY) E += fx_val(Fx{ld_ag(&pq[j].hi), ld_ag(&pq[j].lo)}) * exp_nonpos(mj - M, sh.etab);
+    }
+    E = wave_sum_f64(E);
+    if (tid == 0) {
+      a.qfin[qr].M = M;
+      a.qfin[qr].E = E;
+      a.qfin[qr].ticket = 0;
+    }
   }
 }
 
 // ---- verify: residual passes ----------------------------------------------------------------------------------------
 
-
-// A node's uniform data for one workgroup, in LDS: its kids, their q rows, the residual totals.
-struct NodeShared {
-  Kids k;
-  QRow qr[GSE_MAX_KIDS];
-  double sig[GSE_MAX_KIDS + 1];
-  double clast;
-};
-
+// The node's kids, q rows and totals into LDS, by wave 0 (every load of a round issued at once).
 __device__ __forceinline__ void load_node(const TreeArgs &a, int u, NodeShared &ns) {
-  if (threadIdx.x == 0) {
-    find_kids(a, u, ns.k);
-    for (int m = 0; m < ns.k.nq; ++m) ns.qr[m] = qrow_of(a, ns.k.qrow[m]);
+  if (threadIdx.x < WAVE) {
+    const int ln = lane_id();
     const TreeNode &nd = a.st[u];
-    ns.clast = nd.clast;
-    for (int r = 0; r <= GSE_MAX_KIDS; ++r) ns.sig[r] = nd.sig[r];
+    if (ln <= GSE_MAX_KIDS) {
+      const double sg = nd.sig[ln];
+      ns.sig[ln] = sg;
+      ns.isig[ln] = 1.0 / sg;
+    }
+    if (ln == 0) {
+      ns.clast = nd.clast;
+      ns.iclast = 1.0 / nd.clast;
+    }
+    find_kids(a, u, ns.k);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // (lane 0's LDS writes, then every lane reads them)
+    if (ln < ns.k.nq) ns.qr[ln] = qrow_of(a, ns.k.qrow[ln]);
   }
   __syncthreads();
 }
@@ -428,35 +843,61 @@ __device__ __forceinline__ void load_node(const TreeArgs &a, int u, NodeShared &
 // positive total (sig[0] = C > 0 for a live node), in vocabulary order (sampling.py:100-104), with the uniform
 // uniform(mix(seed, 2^41), i) (spec.py:103). The unnormalised weights (keep e for d = 0, res_d otherwise) give the same
 // count(c < u c[-1]) as the normalised p_d.
-__device__ int node_draw(const TreeArgs &a, int u, const gse_row &P, const Tgt &g, const NodeShared &ns, int kdone,
-                         TreeShared &sh) {
+template <int DTK, int QKK>
+__device__ __forceinline__ int node_draw(const TreeArgs &a, int u, const gse_row &P, const Tgt &g, const NodeShared &ns,
+                                         int kdone, TreeShared &sh, bool segs_kept = false) {
   int d = kdone;
   while (d > 0 && !(ns.sig[d] > 0.0)) --d;
   const size_t o = ((size_t)u * (GSE_MAX_KIDS + 1) + d) * a.nsl;
-  Fx tot = fx_zero();
-  int last = -1;
-  for (int j = 0; j < a.nsl; ++j) {
-    tot = fx_add(tot, Fx{ld_ag(&a.npart[o + j].hi), ld_ag(&a.npart[o + j].lo)});
-    last = max(last, ld_ag(&a.nlast[o + j]));
-  }
+  const Fx *pp = a.npart + o;
+  auto part = [&](int j) { return Fx{ld_ag(&pp[j].hi), ld_ag(&pp[j].lo)}; };
+  const uint64_t *pre_all = segs_kept && d == kdone ? a.tseg + (size_t)u * a.nsl * 2 * TSEG : nullptr;
+  const Fx tot = wave_fx_total(a.nsl, part);  // (every wave reads the partials itself)
+  int lastl = -1;
+  for (int j = lane_id(); j < a.nsl; j += WAVE) lastl = max(lastl, ld_ag(&a.nlast[o + j]));
+  const int last = (int)wave_max_u32((uint32_t)(lastl + 1)) - 1;
   if (last < 0) return -1;
   const double thr = uniform64(mix64(P.seed, SALT_RES), P.idx) * fx_val(tot);
-  Fx before = fx_zero();  // the crossing slice
-  int sx = a.nsl - 1;
-  for (int j = 0; j < a.nsl; ++j) {
-    const Fx nxt = fx_add(before, Fx{ld_ag(&a.npart[o + j].hi), ld_ag(&a.npart[o + j].lo)});
-    if (fx_val(nxt) >= thr) {
-      sx = j;
-      break;
-    }
-    before = nxt;
-  }
+  Fx before;  // the crossing slice and the exact mass ahead of it
+  const int sx = wave_fx_cross(a.nsl, thr, part, before);
   const int s0 = sx * TS, s1 = min(a.s.V, s0 + TS);
   if (g.c.pen) build_counts(g.c, a.s.hist, s0, sh.cnt);
-  const int j = slice_find(s0, s1, before, thr, [&](int i) {
-    const double e = tgt_e(g, i, g.c.pen ? sh.cnt[i - s0] : 0u);
-    return d == 0 ? e : chain(ns.k, ns.qr, e / ns.clast, i, ns.sig, d, false);
-  }, sh);
+  const TBuf tb = tbuf(g.c);
+  const uint32_t *cnt = g.c.pen ? sh.cnt : nullptr;
+  int j = -1;
+  {
+    constexpr int DT = DTK;
+    if (ns.k.nq <= 1 && d <= 2) {
+      const ChainR cr = chain_regs(ns);
+      const QRow q = ns.qr[0];
+      const auto qb = qbuf(q, a.s.V);
+      const double iclast = ns.iclast;
+      with_qv<QKK>(ns.k.nq > 0 && d > 0, q.t1, [&](auto qvc) {
+        constexpr int QL = ql_of(decltype(qvc)::value), QK = qk_of(decltype(qvc)::value);
+        struct El {
+          float x;
+          uint32_t mw;
+          QRaw<QL> q;
+        };
+        j = slice_find(s0, s1, before, thr, [&](int i) {
+          return El{ld_x<DT>(tb, i), ld_m(tb, i), ld_q<QL>(qb, i)};
+        }, [&](int i, const El &w) {
+          const double e = tgt_wr(g, i, w.x, w.mw, cnt ? cnt[i - s0] : 0u, sh.etab);
+          if (d == 0) return e;
+          double qx = 0.0;
+          if constexpr (QL != Q_NONE) qx = q_w<QK>(q, w.q, sh.etab);
+          return chain_rd(cr, qx, e * iclast, i, d, false);
+        }, sh, pre_all ? pre_all + (size_t)sx * 2 * TSEG : nullptr);
+      });
+    } else {
+      j = slice_find(s0, s1, before, thr, [&](int i) { return ld_x<DT>(tb, i); }, [&](int i, float x) {
+        const double e = tgt_wr(g, i, x, ld_m(tb, i), cnt ? cnt[i - s0] : 0u, sh.etab);
+        if (d == 0) return e;
+        return chain(ns.k, [&](int m) { return q_at(ns.qr[m], i, sh.etab); }, e * ns.iclast, i, ns.sig, ns.isig, d,
+                     false);
+      }, sh);
+    }
+  }
   const int jj = j < 0 ? last : j;
   return jj < last ? jj : last;
 }
@@ -470,13 +911,35 @@ __device__ __forceinline__ bool test_kid(const TreeArgs &a, const gse_row &P, co
                                          TreeShared &sh) {
   const int x = ns.k.tok[r];
   if (x < 0 || x >= a.s.V) return false;  // (not a token of this vocabulary: never accepted)
-  const double p0 = p0_at(a, g, x, ns.clast, sh);
-  const double px = chain(ns.k, ns.qr, p0, x, ns.sig, r, true);
-  const double qx = ns.k.qs[r] < 0 ? 1.0 : q_at(ns.qr[ns.k.qs[r]], x);
+  const double p0 = p0_at(a, g, x, ns, sh);
+  const double px = chain(ns.k, [&](int m) { return q_at(ns.qr[m], x, sh.etab); }, p0, x, ns.sig, ns.isig, r, true);
+  const double qx = ns.k.qs[r] < 0 ? 1.0 : q_at(ns.qr[ns.k.qs[r]], x, sh.etab);
   return kid_accepts(P, r, px, qx);
 }
 
+// Kid 0 of every live node with kids (spec.py:93-94 against p0), one workgroup per node, between the statistics and
+// pass 1: an accepted node is decided here and pass 1 skips it.
+__global__ __launch_bounds__(TT) void tkid0_kernel(TreeArgs a) {
+  __shared__ TreeShared sh;
+  __shared__ NodeShared ns;
+  const int u = blockIdx.x;
+  const gse_row P = a.s.params[u];
+  if (!node_live(a, u, P)) return;
+  TreeNode &nd = a.st[u];
+  if ((int)nd.next != 1) return;
+  load_etab(sh);
+  load_node(a, u, ns);  // (its barrier publishes the table)
+  if (ns.k.n == 0) return;
+  const Tgt g = tgt_of(a, u, P);
+  if (test_kid(a, P, g, ns, 0, sh) && threadIdx.x == 0) {
+    nd.token = ns.k.tok[0];
+    nd.kid = ns.k.row[0];
+    nd.next = 0;
+  }
+}
+
 // Pass r over slice blockIdx.x of node blockIdx.y (see the file comment).
+template <int DTK, int QKK>
 __global__ __launch_bounds__(TT) void tpass_kernel(TreeArgs a, int r) {
   __shared__ TreeShared sh;
   __shared__ NodeShared ns;
@@ -485,13 +948,14 @@ __global__ __launch_bounds__(TT) void tpass_kernel(TreeArgs a, int r) {
   if (!node_live(a, u, P)) return;
   TreeNode &nd = a.st[u];
   if ((int)nd.next != r) return;
-  load_node(a, u, ns);
   const Tgt g = tgt_of(a, u, P);
   const int V = a.s.V, s0 = s * TS, s1 = min(V, s0 + TS);
+  load_etab(sh);
+  load_node(a, u, ns);  // (its barrier publishes the table)
   if (r == 1) {
     if (ns.k.n == 0) {  // no kids: mss returns draw(p0, uniform(mix(seed, 2^41), i)) (spec.py:103)
       if (s == 0) {
-        const int j = node_draw(a, u, P, g, ns, 0, sh);
+        const int j = node_draw<DTK, QKK>(a, u, P, g, ns, 0, sh);
         if (tid == 0) {
           nd.token = j;
           nd.kid = -1;
@@ -500,27 +964,73 @@ __global__ __launch_bounds__(TT) void tpass_kernel(TreeArgs a, int r) {
       }
       return;
     }
-    if (test_kid(a, P, g, ns, 0, sh)) {  // kid 0, tested alike by every slice
-      if (s == 0 && tid == 0) {
-        nd.token = ns.k.tok[0];
-        nd.kid = ns.k.row[0];
-        nd.next = 0;
-      }
-      return;
-    }
+    // (kid 0 was tested and rejected by tkid0_kernel)
   }
   // res_r over this slice: kid r - 1 was rejected
   if (g.c.pen) build_counts(g.c, a.s.hist, s0, sh.cnt);
   Fx f = fx_zero();
   int last = -1;
-  for (int kk = 0; kk < TK; ++kk) {
-    const int i = s0 + kk * TT + tid;
-    if (i >= s1) break;
-    const double e = tgt_e(g, i, g.c.pen ? sh.cnt[i - s0] : 0u);
-    const double res = chain(ns.k, ns.qr, e / ns.clast, i, ns.sig, r, false);
-    f = fx_add(f, fx_of(res));
-    if (res > 0.0) last = i;
+  const TBuf tb = tbuf(g.c);
+  const uint32_t *cnt = g.c.pen ? sh.cnt : nullptr;
+  const bool keep_seg = ns.k.nq <= 1 && r <= 2 && r == ns.k.n;
+  {
+    constexpr int DT = DTK;
+    if (ns.k.nq <= 1 && r <= 2) {
+      // the usual tree (kids sharing at most one q row, a chain of one or two levels): the chain in registers, the q
+      // row streaming with the logits
+      const ChainR cr = chain_regs(ns);
+      const QRow q = ns.qr[0];
+      const auto qb = qbuf(q, V);
+      const double iclast = ns.iclast;
+      // the pass after which the node draws (its last kid was rejected) keeps its 64-token segment sums for the draw
+      uint64_t *sg = keep_seg ? a.tseg + ((size_t)u * a.nsl + s) * 2 * TSEG : nullptr;
+      const int wv = tid >> 6;
+      with_qv<QKK>(ns.k.nq > 0, q.t1, [&](auto qvc) {
+        constexpr int QL = ql_of(decltype(qvc)::value), QK = qk_of(decltype(qvc)::value);
+        slice_groups(s0, [&](int t0) { return ld_grp<DT, QL>(tb, qb, t0); }, [&](int t0, const Grp<DT, QL> &gr) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int i = t0 + e * TT;
+            Fx fe = fx_zero();
+            if (i < s1) {
+              const double w = tgt_wr(g, i, gr.x[e], gr.mw[e], cnt ? cnt[i - s0] : 0u, sh.etab);
+              double qx = 0.0;
+              if constexpr (QL != Q_NONE) qx = q_w<QK>(q, gr.q[e], sh.etab);
+              const double res = chain_rd(cr, qx, w * iclast, i, r, false);
+              fe = fx_of(res);
+              f = fx_add(f, fe);
+              if (res > 0.0) last = i;
+            }
+            if (sg) {  // (the wave's 64 tokens of this element form segment ((t0 - s0 - tid) / 4 TT) 16 + 4 e + wave)
+              const uint64_t hi = wave_sum_u64(fe.hi), lo = wave_sum_u64(fe.lo);
+              const int k = ((t0 - s0 - tid) >> 10) * 16 + 4 * e + wv;
+              if (lane_id() == 0) {
+                st_ag(&sg[2 * k], hi);
+                st_ag(&sg[2 * k + 1], lo);
+              }
+            }
+          }
+        });
+      });
+    } else {
+      // deeper chains or kids with several q rows: the q values read token by token
+      slice_groups(s0, [&](int t0) { return ld_grp<DT, Q_NONE>(tb, tb.x, t0); },
+                   [&](int t0, const Grp<DT, Q_NONE> &gr) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = t0 + e * TT;
+          if (i < s1) {
+            const double w = tgt_wr(g, i, gr.x[e], gr.mw[e], cnt ? cnt[i - s0] : 0u, sh.etab);
+            const double res = chain(ns.k, [&](int m) { return q_at(ns.qr[m], i, sh.etab); }, w * ns.iclast, i,
+                                     ns.sig, ns.isig, r, false);
+            f = fx_add(f, fx_of(res));
+            if (res > 0.0) last = i;
+          }
+        }
+      });
+    }
   }
+
   f = block_fx_sum(f, sh.red);
   last = block_max_i32(last, sh.redi);
   const size_t o = ((size_t)u * (GSE_MAX_KIDS + 1) + r) * a.nsl + s;
@@ -535,12 +1045,15 @@ __global__ __launch_bounds__(TT) void tpass_kernel(TreeArgs a, int r) {
   __syncthreads();
   if (sh.ticket != (uint32_t)(a.nsl - 1)) return;
   // the node's last slice: the total of res_r, then kid r or the draw
-  if (tid == 0) {
-    Fx t = fx_zero();
-    for (int j = 0; j < a.nsl; ++j) t = fx_add(t, Fx{ld_ag(&a.npart[o - s + j].hi), ld_ag(&a.npart[o - s + j].lo)});
-    ns.sig[r] = fx_val(t);
-    nd.sig[r] = ns.sig[r];
-    nd.ticket = 0;
+  if (tid < WAVE) {
+    const Fx *pp = a.npart + (o - s);
+    const Fx t = wave_fx_total(a.nsl, [&](int j) { return Fx{ld_ag(&pp[j].hi), ld_ag(&pp[j].lo)}; });
+    if (tid == 0) {
+      ns.sig[r] = fx_val(t);
+      ns.isig[r] = 1.0 / ns.sig[r];
+      nd.sig[r] = ns.sig[r];
+      nd.ticket = 0;
+    }
   }
   __syncthreads();
   if (r < ns.k.n) {
@@ -556,7 +1069,7 @@ __global__ __launch_bounds__(TT) void tpass_kernel(TreeArgs a, int r) {
     }
     return;
   }
-  const int j = node_draw(a, u, P, g, ns, r, sh);
+  const int j = node_draw<DTK, QKK>(a, u, P, g, ns, r, sh, keep_seg);
   if (tid == 0) {
     nd.token = j;
     nd.kid = -1;
@@ -724,7 +1237,8 @@ __global__ __launch_bounds__(TT) void pick2_kernel(PickArgs a) {
   if (!(t > 0.0) || a.b.n[row] <= 0) return;
   const int V = (int)a.b.vocab, s0 = s * TS, s1 = min(V, s0 + TS);
   double M = -INFINITY;
-  for (int j = 0; j < a.nsl; ++j) M = fmax(M, a.pmax[(size_t)row * a.nsl + j]);
+  for (int j = lane_id(); j < a.nsl; j += WAVE) M = fmax(M, a.pmax[(size_t)row * a.nsl + j]);
+  M = wave_max_f64(M);
   Fx f = fx_zero();
   int last = -1;
   for (int k = 0; k < TK; ++k) {
@@ -750,31 +1264,30 @@ __global__ __launch_bounds__(TT) void pick3_kernel(PickArgs a) {
   const int n = min(max(a.b.n[row], 0), (int)min((int64_t)GSE_MAX_KIDS, a.b.out_ld));
   if (!(t > 0.0) || kd >= n) return;
   const int V = (int)a.b.vocab;
+  // (every wave reads the row's partials itself, a slice per lane)
+  const double *pm = a.pmax + (size_t)row * a.nsl;
+  const Fx *pp = a.ppart + (size_t)row * a.nsl;
+  const int32_t *pl = a.plast + (size_t)row * a.nsl;
   double M = -INFINITY;
-  Fx tot = fx_zero();
-  int last = -1;
-  for (int j = 0; j < a.nsl; ++j) {
-    M = fmax(M, a.pmax[(size_t)row * a.nsl + j]);
-    tot = fx_add(tot, a.ppart[(size_t)row * a.nsl + j]);
-    last = max(last, a.plast[(size_t)row * a.nsl + j]);
+  int lastl = -1;
+  for (int j = lane_id(); j < a.nsl; j += WAVE) {
+    M = fmax(M, pm[j]);
+    lastl = max(lastl, pl[j]);
   }
+  M = wave_max_f64(M);
+  const int last = (int)wave_max_u32((uint32_t)(lastl + 1)) - 1;
+  auto part = [&](int j) { return pp[j]; };
+  const Fx tot = wave_fx_total(a.nsl, part);
   int tok = -1;
   double lq = __builtin_nan("");
   if (last >= 0) {
     const double E = fx_val(tot);
     const double thr = uniform64(mix64(a.b.seed[row], SALT_DRAFT + (uint64_t)kd), a.b.at[row]) * E;
-    Fx before = fx_zero();
-    int sx = a.nsl - 1;
-    for (int j = 0; j < a.nsl; ++j) {
-      const Fx nxt = fx_add(before, a.ppart[(size_t)row * a.nsl + j]);
-      if (fx_val(nxt) >= thr) {
-        sx = j;
-        break;
-      }
-      before = nxt;
-    }
+    Fx before;
+    const int sx = wave_fx_cross(a.nsl, thr, part, before);
     const int s0 = sx * TS, s1 = min(V, s0 + TS);
-    const int j = slice_find(s0, s1, before, thr, [&](int i) { return exp((double)pick_x(a, row, i) / t - M); }, sh);
+    const int j = slice_find(s0, s1, before, thr, [&](int i) { return pick_x(a, row, i); },
+                             [&](int, float x) { return exp((double)x / t - M); }, sh);
     tok = j < 0 ? last : min(j, last);
     lq = ((double)pick_x(a, row, tok) / t - M) - log(E);
   }
@@ -802,15 +1315,29 @@ hipError_t launch_tree(const TreeLaunch &L, hipStream_t s) {
   a.st = L.st;
   a.npart = L.npart;
   a.nlast = L.nlast;
+  a.tseg = L.tseg;
   a.qmax = L.qmax;
   a.qpart = L.qpart;
   a.qfin = L.qfin;
   a.out = L.out;
   const bool qlog = L.q.rows > 0 && L.q.kind != GSE_Q_PROB;
-  if (qlog) hipLaunchKernelGGL(qmax_kernel, dim3(a.nsl, L.q.rows), dim3(TT), 0, s, a);
-  hipLaunchKernelGGL(tstats_kernel, dim3(a.nsl, a.nodes + (qlog ? L.q.rows : 0)), dim3(TT), 0, s, a);
-  // pass r: kid r - 1 rejected -> res_r; a node with k kids needs passes 1..k (one without kids draws in pass 1)
-  for (int r = 1; r <= max(L.max_kids, 1); ++r) hipLaunchKernelGGL(tpass_kernel, dim3(a.nsl, a.nodes), dim3(TT), 0, s, a, r);
+  // the instances for the call's logits type and q kind
+  auto go = [&](auto dtc, auto qkc) {
+    constexpr int DT = decltype(dtc)::value, QK = decltype(qkc)::value;
+    hipLaunchKernelGGL((tstats_kernel<DT, QK>), dim3(a.nsl, a.nodes + (qlog ? L.q.rows : 0)), dim3(TT), 0, s, a);
+    hipLaunchKernelGGL(tkid0_kernel, dim3(a.nodes), dim3(TT), 0, s, a);
+    // pass r: kid r - 1 rejected -> res_r; a node with k kids needs passes 1..k (one without kids draws in pass 1)
+    for (int r = 1; r <= max(L.max_kids, 1); ++r)
+      hipLaunchKernelGGL((tpass_kernel<DT, QK>), dim3(a.nsl, a.nodes), dim3(TT), 0, s, a, r);
+  };
+  auto by_q = [&](auto dtc) {
+    if (L.q.rows == 0) go(dtc, IntC<Q_NONE>{});
+    else if (L.q.kind == GSE_Q_PROB) go(dtc, IntC<GSE_Q_PROB>{});
+    else if (L.q.kind == GSE_Q_LOGITS_BF16) go(dtc, IntC<GSE_Q_LOGITS_BF16>{});
+    else go(dtc, IntC<GSE_Q_LOGITS_F32>{});
+  };
+  if (L.s.dtype == GSE_BF16) by_q(IntC<GSE_BF16>{});
+  else by_q(IntC<GSE_F32>{});
   hipLaunchKernelGGL(walk_kernel, dim3((max(a.requests, a.nodes) + 63) / 64), dim3(64), 0, s, a);
   return hipGetLastError();
 }
