@@ -608,7 +608,7 @@ __device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShare
   }
 }
 
-constexpr int XGRID = 64;  // workgroups of the exact pass (unless every row is forced through it)
+constexpr int XGRID = 256;  // workgroups of the exact pass, at most (one per CU; every row when all are forced)
 
 // The exact pass: with GSE_BATCH_EXACT one workgroup per row; otherwise a small grid, workgroup g owning the rows
 // r = g (mod grid): it finds its hard ones (those the main pass and the split-row finish left: one scan of their flags,

@@ -46,7 +46,7 @@ static_assert(NOALLOC_ROWS == GSE_NOALLOC_ROWS && NOALLOC_VOCAB == GSE_NOALLOC_V
 constexpr int CAPW = 512;   // candidates listed per wave per part
 constexpr int PWAVES = 4;   // waves per part workgroup
 constexpr int MAXP = 64;    // parts per row
-constexpr int PTOK = 40960; // tokens per part, at most
+constexpr int PTOK = 65536; // tokens per part, at most
 constexpr int PCHUNK = 1024;  // part lengths are multiples of this (one wave chunk)
 constexpr int PMIN = 8192;    // tokens per part, at least, when a small batch is split to fill the device: every part
                               // lists its own candidates, so more parts make a longer row resolve

@@ -1,4 +1,4 @@
-// The fused selection pass. One 256-thread workgroup per (row, part), a part being a contiguous run of at most 40960
+// The fused selection pass. One 256-thread workgroup per (row, part), a part being a contiguous run of at most 65536
 // tokens of the row. Its four waves stream the part in 512-token chunks (64 lanes x 8 tokens), each wave on its own:
 // wave w takes chunks w, w + 4, w + 8, ..., the next chunks' loads are in flight while the current one is processed,
 // and no barrier separates two chunks. One HBM read of the logits, the packed mask words and the row's history ids; the
