@@ -20,7 +20,10 @@
   grow_dynamic        spec.py:183-204  EAGLE-2 expand + rerank of a proposal tree from pick()
 
 The walk is pinned in tests/test_oracle_walk.py by the joint law of its emitted tokens (chi-square against the product
-of the target's dist(), with power controls) and by known answers that fix which uniform index each depth uses.
+of the target's dist(), with power controls) and by known answers that fix which uniform index each depth uses. pick and
+grow_dynamic are pinned in tests/test_oracle_drafter.py against the reference's own TreeDrafter outputs on a toy model
+(tests/golden/drafter_golden.npz) and by the stable order, the SALT_DRAFT streams and log q in closed form. mss is
+pinned by the golden vectors of tests/test_oracle.py.
 """
 import numpy as np
 
