@@ -224,7 +224,7 @@ GSE_API int gse_sample(gse_handle *h, const gse_batch *in, const gse_out *out);
 
 /* No counterpart in the reference. gse_sample for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc): no handle, and no hipMalloc / hipFree / allocating
- * library call. Its workspace is a static device array of about 22 MB that each GPU holds from the library's load until
+ * library call. Its workspace is a static device array of about 21 MB that each GPU holds from the library's load until
  * the process ends, for batches of at most GSE_NOALLOC_ROWS rows of at most GSE_NOALLOC_VOCAB tokens (more:
  * GSE_E_CAPACITY). It runs on the current HIP device; the first call on a device sets that device's workspace up and
  * should not be captured. Every call on one GPU shares its workspace: calls that overlap on one GPU (two streams, two
