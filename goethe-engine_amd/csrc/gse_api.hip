@@ -141,7 +141,36 @@ void parts(const gse_handle *h, uint32_t rows, uint32_t vocab, int *nparts, int 
   *nparts = (int)((vocab + len - 1) / len);
 }
 
-// Workgroups of the split-row finish launches: one resident round (the kernels slice the deep rows to fit it).
+// Part boundaries of the main pass. By default the parts of a row are equal and its workgroups consecutive. When the
+// batch is one resident round of three or four part workgroups per CU, the workgroups go part-major instead (L streams
+// part L / rows8 of row L % rows8: every row has one part in each quarter of the dispatch order, and all parts of a row
+// still share an XCD) and a part's length follows its quarter: the workgroups that reach a CU later stream slower, as
+// the oldest wave wins issue and memory arbitration, at measured rates (C3, MI355X) of 1 : 0.89 : 0.73 : 0.63 by
+// quarter, so parts in that proportion end a row's streams together instead of leaving the last quarter's rows behind.
+void part_layout(const gse_handle *h, gse::ScanArgs &a) {
+  const int np = a.nparts, V = a.V;
+  for (int p = 0; p <= np; ++p) a.pstart[p] = p < np ? p * a.plen : V;
+  a.pmajor = 0;
+  const int rows8 = a.xcd_map ? (a.rows + 7) / 8 * 8 : a.rows;
+  const int64_t wgs = (int64_t)rows8 * np;
+  if (!a.xcd_map || np < 4 || np % 4 || wgs > (int64_t)h->target || 4 * wgs < 3 * (int64_t)h->target) return;
+  static const double RATE[4] = {1.0, 0.89, 0.73, 0.63};
+  double tot = 0.0;
+  for (int p = 0; p < np; ++p) tot += RATE[(4 * p) / np];
+  int32_t b[gse::MAXP + 1];
+  double c = 0.0;
+  b[0] = 0;
+  for (int p = 1; p < np; ++p) {
+    c += RATE[(4 * (p - 1)) / np];
+    b[p] = (int32_t)((int64_t)(c / tot * V + gse::PCHUNK / 2) / gse::PCHUNK * gse::PCHUNK);
+  }
+  b[np] = V;
+  for (int p = 0; p < np; ++p)  // (every part non-empty and within the part capacity, else the equal layout stays)
+    if (b[p + 1] <= b[p] || b[p + 1] - b[p] > gse::PTOK) return;
+  for (int p = 0; p <= np; ++p) a.pstart[p] = b[p];
+  a.pmajor = 1;
+}
+
 void deep_grid(const gse_handle *h, uint32_t rows, int *nsl, int *grid) {
   const uint32_t slots = rows < h->dslots ? rows : h->dslots;
   const uint32_t items = slots * (uint32_t)gse::DSMAX;
@@ -177,6 +206,7 @@ gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   a.dlist = h->dlist;
   a.dslots = (int)h->dslots;
   deep_grid(h, b.rows, &a.dslices, &a.dgrid);
+  part_layout(h, a);
   return a;
 }
 

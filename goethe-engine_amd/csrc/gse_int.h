@@ -117,6 +117,7 @@ struct ScanArgs {
   int64_t ld;
   int dtype, V, rows, nch, mode, force_exact, xcd_map;
   int nparts, plen;  // the main pass: parts per row, tokens per part (a multiple of 1024; the last part may be shorter)
+  int pmajor;        // workgroup L streams part L / rows8 of row L % rows8 (else the parts of a row are consecutive)
   const gse_row *params;
   const int32_t *mask;
   int64_t mask_ld;
@@ -141,6 +142,7 @@ struct ScanArgs {
   int dslices, dgrid;  // split-row finish enabled (slices per deep row, at most), workgroups per pass
   uint64_t plan_wait;  // wall-clock ticks (100 MHz) a split-row pick slice waits for its row's plan
   int tree;            // a verify round (gse_verify_tree): GSE_ROW_MSS rows need dist's keep boundary, not a token
+  int32_t pstart[MAXP + 1];  // part p of every row is [pstart[p], pstart[p + 1]) (multiples of 1024; pstart[nparts] = V)
 };
 
 // Verify round state of one node (gse_tree.hip), in the handle's workspace.

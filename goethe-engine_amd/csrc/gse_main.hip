@@ -855,7 +855,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
                                           Shared &sh) {
   using L = Lay<DT>;
   const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
-  const int p0 = part * a.plen, p1 = min(a.V, p0 + a.plen);
+  const int p0 = a.pstart[part], p1 = a.pstart[part + 1];
   const int pv = AL ? max(p0, p1 & ~(L::VEC - 1)) : p1;  // the stream's end; [pv, p1) go to the side pass
   const int nck = (pv - p0 + CHK - 1) / CHK;
   const bool listing = !GREEDY || nlp_of(a, P) > 0;  // candidates and the softmax sum are needed
@@ -1107,7 +1107,11 @@ __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
   __shared__ Shared sh;
   const int L = blockIdx.x;
   int row, part;
-  if (a.xcd_map) {  // the parts of a row on one XCD (workgroups go round-robin over the 8 XCDs): shared L2
+  const int rows8 = (a.rows + 7) / 8 * 8;
+  if (a.pmajor) {  // part-major: row L % rows8 (rows8 a multiple of 8: still on XCD row % 8)
+    row = L % rows8;
+    part = L / rows8;
+  } else if (a.xcd_map) {  // the parts of a row on one XCD (workgroups go round-robin over the 8 XCDs): shared L2
     const int x = L & 7, i = L >> 3;
     row = x + 8 * (i / a.nparts);
     part = i % a.nparts;
