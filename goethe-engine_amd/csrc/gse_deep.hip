@@ -163,51 +163,30 @@ __device__ __forceinline__ DGeom deep_geom(const ScanArgs &a, int nd) {
 // Pass 1: histogram and plan.
 
 // The plan of a row from its histogram (added by every slice of this launch), into the row's slot: {w2lo, w2hi, w1lo,
-// w1hi, status} and the element counts of the regions outside the windows. Run by wave 0 of the row's last slice:
-// lane l holds bins [8l, 8l + 8), prefixes by wave scans, "first bin with" queries by wave minima. Compact code (it
-// runs once per row, cold).
-constexpr int PBL = DNB / WAVE;  // bins per lane
-static_assert(PBL * WAVE == DNB, "");
+// w1hi, status} and the element counts of the regions outside the windows. Run by the whole workgroup of the row's
+// last count slice: thread t holds bins 2t and 2t + 1; inclusive prefixes by block scans (wave scans, then the wave
+// totals in order), "first bin with" queries by LDS minima, and lookups at the window edges from LDS tables.
+struct PlanShared {
+  uint64_t pc[DNB], ph[DNB], po[DNB];  // inclusive prefixes through each bin: counts, masses in 2^-40 and 2^-64 units
+  double pm[DNB];                      // the fp64 value of the mass prefix
+  uint64_t wt[3][NWV];                 // wave totals
+  uint32_t q[8];                       // queries: first / last bins
+};
 
-// p[j] of lane b / PBL for j = b % PBL (b wave-uniform; zero for b < 0). Every p[j] is read off that lane first and
-// the pick is a chain of scalar selects: a select over the registers by a run-time index becomes a private array in
-// scratch memory, with a memory round trip per lookup.
-template <typename T>
-__device__ __forceinline__ T bin_at(const T (&p)[PBL], int b) {
-  if (b < 0) return T(0);
-  const int jj = b % PBL, ln = b / PBL;
-  uint64_t v = 0;
-#pragma unroll
-  for (int j = 0; j < PBL; ++j) {
-    uint64_t x;
-    if constexpr (sizeof(T) == 4) {
-      x = (uint32_t)__builtin_amdgcn_readlane(__builtin_bit_cast(int, p[j]), ln);
-    } else {
-      const uint64_t y = __builtin_bit_cast(uint64_t, p[j]);
-      const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)y, ln);
-      const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(y >> 32), ln);
-      x = ((uint64_t)hi << 32) | lo;
-    }
-    v = j == jj ? x : v;
-  }
-  if constexpr (sizeof(T) == 4) return __builtin_bit_cast(T, (uint32_t)v);
-  else return __builtin_bit_cast(T, v);
-}
+enum { PQ_B0, PQ_B1, PQ_B2, PQ_B5, PQ_B6, PQ_B3, PQ_B4, PQ_N };
 
-__device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode) {
-  const int l = lane_id();
-  // the row's scalars first: their loads overlap the histogram loads (plain loads written after the ordered ones
-  // would only be issued once those had been waited for)
+__device__ __forceinline__ void plan_block(const uint64_t *gh, DeepSlot *ds, int mode, PlanShared &sh) {
+  const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
   const gse_row &P = ds->P;
   const float M = ds->M;
   const uint64_t K = P.top_k > 0 ? (uint64_t)P.top_k : ~0ull;
   const double top_p = P.top_p, min_p = P.min_p, u = ds->u;
-  uint64_t c[PBL], mh[PBL], mo[PBL];
+  uint64_t c[BPT], mh[BPT], mo[BPT];
 #pragma unroll
-  for (int j = 0; j < PBL; ++j) {
-    c[j] = ld_ag(&gh[l * PBL + j]);
-    mh[j] = ld_ag(&gh[DNB + l * PBL + j]);
-    mo[j] = ld_ag(&gh[2 * DNB + l * PBL + j]);
+  for (int j = 0; j < BPT; ++j) {
+    c[j] = ld_ag(&gh[tid * BPT + j]);
+    mh[j] = ld_ag(&gh[DNB + tid * BPT + j]);
+    mo[j] = ld_ag(&gh[2 * DNB + tid * BPT + j]);
   }
   // min-p keeps exp(z - M) >= min_p, i.e. d <= -ln(min_p): bins below bm - 1 are all kept, bins above bm + 1 all cut
   const bool mp = min_p > 0.0;
@@ -219,26 +198,47 @@ __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode
   // inclusive prefixes through each bin: counts, exact masses (2^-40 and 2^-64 parts) and their fp64 values
   uint64_t cl = 0, hl = 0, ol = 0;
 #pragma unroll
-  for (int j = 0; j < PBL; ++j) {
+  for (int j = 0; j < BPT; ++j) {
     cl += c[j];
     hl += mh[j];
     ol += mo[j];
   }
   const uint64_t ci = wave_incl_scan_u64(cl), hi = wave_incl_scan_u64(hl), oi = wave_incl_scan_u64(ol);
-  const uint64_t ctot = lane63(ci), htot = lane63(hi), otot = lane63(oi);
-  uint64_t pc[PBL], ph[PBL], po[PBL];
-  double pm[PBL];
-  {
-    uint64_t rc = ci - cl, rh = hi - hl, ro = oi - ol;
+  if (lane == WAVE - 1) {
+    sh.wt[0][w] = ci;
+    sh.wt[1][w] = hi;
+    sh.wt[2][w] = oi;
+  }
+  if (tid < PQ_N) sh.q[tid] = (tid == PQ_B5) ? 0u : (uint32_t)(DNB - 1);
+  __syncthreads();
+  uint64_t bc = 0, bh = 0, bo = 0, ctot = 0, htot = 0, otot = 0;
 #pragma unroll
-    for (int j = 0; j < PBL; ++j) {
+  for (int k = 0; k < NWV; ++k) {
+    const uint64_t x0 = sh.wt[0][k], x1 = sh.wt[1][k], x2 = sh.wt[2][k];
+    if (k < w) {
+      bc += x0;
+      bh += x1;
+      bo += x2;
+    }
+    ctot += x0;
+    htot += x1;
+    otot += x2;
+  }
+  uint64_t pc[BPT];
+  double pm[BPT];
+  {
+    uint64_t rc = bc + ci - cl, rh = bh + hi - hl, ro = bo + oi - ol;
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
       rc += c[j];
       rh += mh[j];
       ro += mo[j];
       pc[j] = rc;
-      ph[j] = rh;
-      po[j] = ro;
       pm[j] = fx_val(Fx{rh, ro});
+      sh.pc[tid * BPT + j] = rc;
+      sh.ph[tid * BPT + j] = rh;
+      sh.po[tid * BPT + j] = ro;
+      sh.pm[tid * BPT + j] = pm[j];
     }
   }
   const double S = fx_val(Fx{htot, otot});
@@ -250,53 +250,69 @@ __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode
   //   b2:     first bin with inclusive count >= K (top-k: the bin of rank K - 1)
   //   b5 - 1: last non-empty bin below bm - 1 (min-p: holds a kept element, so the last kept one is at or after it)
   //   b6:     first non-empty bin above bm + 1 (min-p: holds a cut element)
-  uint32_t b0 = DNB - 1, b1 = DNB - 1, b2 = DNB - 1, b5 = 0, b6 = DNB - 1;
+  {
+    uint32_t b0 = DNB - 1, b1 = DNB - 1, b2 = DNB - 1, b5 = 0, b6 = DNB - 1;
 #pragma unroll
-  for (int j = PBL - 1; j >= 0; --j) {
-    const uint32_t b = l * PBL + j;
-    if (pm[j] >= tS - delta) b0 = b;
-    if (pm[j] >= tS + delta) b1 = b;
-    if (pc[j] >= K) b2 = b;
-    if (mp && c[j] && b > bm + 1) b6 = b;
-  }
-  if (mp) {
+    for (int j = BPT - 1; j >= 0; --j) {
+      const uint32_t b = tid * BPT + j;
+      if (pm[j] >= tS - delta) b0 = b;
+      if (pm[j] >= tS + delta) b1 = b;
+      if (pc[j] >= K) b2 = b;
+      if (mp && c[j] && b > bm + 1) b6 = b;
+    }
+    if (mp) {
 #pragma unroll
-    for (int j = 0; j < PBL; ++j) {
-      const uint32_t b = l * PBL + j;
-      if (c[j] && b + 1 < bm) b5 = b + 1;
+      for (int j = 0; j < BPT; ++j) {
+        const uint32_t b = tid * BPT + j;
+        if (c[j] && b + 1 < bm) b5 = b + 1;
+      }
+    }
+    b0 = wave_min_u32(b0);
+    b1 = wave_min_u32(b1);
+    b2 = wave_min_u32(b2);
+    b5 = wave_max_u32(b5);
+    b6 = wave_min_u32(b6);
+    if (lane == 0) {
+      atomicMin(&sh.q[PQ_B0], b0);
+      atomicMin(&sh.q[PQ_B1], b1);
+      atomicMin(&sh.q[PQ_B2], b2);
+      atomicMax(&sh.q[PQ_B5], b5);
+      atomicMin(&sh.q[PQ_B6], b6);
     }
   }
-  b0 = wave_min_u32(b0);
-  b1 = wave_min_u32(b1);
-  b2 = wave_min_u32(b2);
-  b5 = wave_max_u32(b5);
-  b6 = wave_min_u32(b6);
-  uint32_t w1lo = b0, w1hi = b1;
+  __syncthreads();
+  uint32_t w1lo = sh.q[PQ_B0], w1hi = sh.q[PQ_B1];
   if (K < ctot) {
-    w1lo = min(w1lo, b2);
-    w1hi = min(w1hi, b2);
+    w1lo = min(w1lo, sh.q[PQ_B2]);
+    w1hi = min(w1hi, sh.q[PQ_B2]);
   }
   if (mp) {
-    const uint32_t lo = b5 ? b5 - 1u : 0u, hi = b6;
+    const uint32_t b5 = sh.q[PQ_B5], lo = b5 ? b5 - 1u : 0u, hi = sh.q[PQ_B6];
     w1lo = min(w1lo, lo);
     // when min-p may bind, the window reaches its first cut element (the finish cannot test min-p unlisted)
     w1hi = lo <= w1hi ? max(w1hi, min(hi, (uint32_t)(DNB - 1))) : min(w1hi, hi);
   }
+  auto at = [&](const auto *t, int b) { return b < 0 ? decltype(t[0])(0) : t[b]; };
   // masses before w1lo and through w1hi, then the windows of the draw
   uint32_t w2lo = w1lo, w2hi = w1hi;
   if (mode == MODE_SAMPLE) {
-    const double qd0 = bin_at(pm, (int)w1lo - 1), qd1 = bin_at(pm, (int)w1hi);
+    const double qd0 = at(sh.pm, (int)w1lo - 1), qd1 = at(sh.pm, (int)w1hi);
     const double tlo = u * (qd0 - delta) - delta, thi = u * (qd1 + delta) + delta;
     uint32_t b3 = DNB - 1, b4 = DNB - 1;
 #pragma unroll
-    for (int j = PBL - 1; j >= 0; --j) {
-      if (pm[j] >= tlo) b3 = l * PBL + j;
-      if (pm[j] >= thi) b4 = l * PBL + j;
+    for (int j = BPT - 1; j >= 0; --j) {
+      if (pm[j] >= tlo) b3 = tid * BPT + j;
+      if (pm[j] >= thi) b4 = tid * BPT + j;
     }
     b3 = wave_min_u32(b3);
     b4 = wave_min_u32(b4);
-    w2hi = min(b4, w1hi);
-    w2lo = min(b3, w2hi);
+    if (lane == 0) {
+      atomicMin(&sh.q[PQ_B3], b3);
+      atomicMin(&sh.q[PQ_B4], b4);
+    }
+    __syncthreads();
+    w2hi = min(sh.q[PQ_B4], w1hi);
+    w2lo = min(sh.q[PQ_B3], w2hi);
   }
   if (w2hi + 1 >= w1lo) {  // touching or overlapping windows: one window
     w2lo = min(w2lo, w1lo);
@@ -304,19 +320,21 @@ __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode
     w1lo = w2lo;
     w1hi = w2hi;
   }
-  // the regions outside the windows from the prefixes at their edges: before the draw window (0), between the
-  // windows (1), after the cut window (counts), and the rest of the mass (2)
-  const bool sep = w1lo > w2hi + 1;
-  const uint64_t n0 = bin_at(pc, (int)w2lo - 1);
-  const uint64_t n1 = sep ? bin_at(pc, (int)w1lo - 1) - bin_at(pc, (int)w2hi) : 0ull;
-  const uint64_t n2 = ctot - bin_at(pc, (int)w1hi);
-  const uint64_t inw = ctot - n0 - n1 - n2;
-  const uint64_t x0h = bin_at(ph, (int)w2lo - 1), x0o = bin_at(po, (int)w2lo - 1);
-  const uint64_t x1h = sep ? bin_at(ph, (int)w1lo - 1) - bin_at(ph, (int)w2hi) : 0ull;
-  const uint64_t x1o = sep ? bin_at(po, (int)w1lo - 1) - bin_at(po, (int)w2hi) : 0ull;
-  const uint64_t xm[6] = {x0h, x0o, x1h, x1o, htot - x0h - x1h, otot - x0o - x1o};
-  const uint32_t status = (inw > 0 && inw <= (uint64_t)DCAP && S > 0.0 && fabsf(M) < INFINITY) ? DS_PLANNED : DS_FAIL;
-  if (l == 0) {  // the plan, then (once it is stored) its status, which the row's pick slices wait for
+  if (tid == 0) {
+    // the regions outside the windows from the prefixes at their edges: before the draw window (0), between the
+    // windows (1), after the cut window (counts), and the rest of the mass (2)
+    const bool sep = w1lo > w2hi + 1;
+    const uint64_t n0 = at(sh.pc, (int)w2lo - 1);
+    const uint64_t n1 = sep ? at(sh.pc, (int)w1lo - 1) - at(sh.pc, (int)w2hi) : 0ull;
+    const uint64_t n2 = ctot - at(sh.pc, (int)w1hi);
+    const uint64_t inw = ctot - n0 - n1 - n2;
+    const uint64_t x0h = at(sh.ph, (int)w2lo - 1), x0o = at(sh.po, (int)w2lo - 1);
+    const uint64_t x1h = sep ? at(sh.ph, (int)w1lo - 1) - at(sh.ph, (int)w2hi) : 0ull;
+    const uint64_t x1o = sep ? at(sh.po, (int)w1lo - 1) - at(sh.po, (int)w2hi) : 0ull;
+    const uint64_t xm[6] = {x0h, x0o, x1h, x1o, htot - x0h - x1h, otot - x0o - x1o};
+    const uint32_t status =
+        (inw > 0 && inw <= (uint64_t)DCAP && S > 0.0 && fabsf(M) < INFINITY) ? DS_PLANNED : DS_FAIL;
+    // the plan, then (once it is stored) its status, which the row's pick slices wait for
     st_ag(&ds->w2lo, w2lo);
     st_ag(&ds->w2hi, w2hi);
     st_ag(&ds->w1lo, w1lo);
@@ -327,51 +345,6 @@ __device__ __noinline__ void plan_row(const uint64_t *gh, DeepSlot *ds, int mode
     for (int k = 0; k < 6; ++k) st_ag(&ds->acc[DA_X0HI + k], xm[k]);
     store_wait();
     st_ag(&ds->status, status);
-  }
-}
-
-template <int DT, bool AL>
-__device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slice, const DGeom &g, DeepShared &sh,
-                                           const double *etab) {
-  const int tid = threadIdx.x;
-  DeepSlot *ds = a.dslot + slot;
-  const int row = ds->row;
-  const gse_row P = ds->P;
-  const float M = ds->M;
-  const double Md = (double)M;
-  const RowCtx c = make_ctx(a, row, P);
-  const int p0 = slice * g.len, p1 = min(a.V, p0 + g.len);
-  __syncthreads();  // (LDS of the previous item)
-  for (int b = tid; b < DNB; b += MT) {
-    sh.c.hi[b] = 0;
-    sh.c.lo[b] = 0;
-  }
-  stream_slice<DT, AL>(a, c, row, p0, p1, sh, [] {}, [&](float z, int, bool ok) __attribute__((always_inline)) {
-    if (ok && z > -INFINITY) {
-      const uint32_t b = dbin(z, M);
-      const Fx f = fx_of(exp_nonpos((double)z - Md, etab));
-      atomicAdd((unsigned long long *)&sh.c.hi[b], (unsigned long long)f.hi);
-      atomicAdd((unsigned long long *)&sh.c.lo[b], (unsigned long long)(f.lo | (1ull << 48)));
-    }
-  });
-  uint64_t *gh = a.dhist + (size_t)slot * 3 * DNB;
-  for (int b = tid; b < DNB; b += MT) {
-    const uint64_t lo = sh.c.lo[b];
-    if (lo) {
-      atomic_add_ag(&gh[b], lo >> 48);
-      atomic_add_ag(&gh[DNB + b], sh.c.hi[b]);
-      atomic_add_ag(&gh[2 * DNB + b], lo & ((1ull << 48) - 1ull));
-    }
-  }
-  // Ticket: the row's last slice plans it.
-  store_wait();
-  __syncthreads();
-  if (tid == 0) sh.ticket = ticket_add(&ds->cdone);
-  __syncthreads();
-  if (sh.ticket == (uint32_t)(g.S - 1) && tid < WAVE) {
-    __builtin_amdgcn_s_setprio(3);  // (the row's other slices wait for the plan)
-    plan_row(gh, ds, a.mode);
-    if (tid == 0) ds->cdone = 0u;
   }
 }
 
@@ -730,8 +703,57 @@ __device__ __noinline__ void finish_row(const FinArgs a, DeepSlot *ds, FinShared
 
 union PickShared {
   DeepShared d;
+  PlanShared pl;
   FinShared f;
 };
+
+template <int DT, bool AL>
+__device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slice, const DGeom &g, PickShared &ps,
+                                           const double *etab) {
+  DeepShared &sh = ps.d;
+  const int tid = threadIdx.x;
+  DeepSlot *ds = a.dslot + slot;
+  const int row = ds->row;
+  const gse_row P = ds->P;
+  const float M = ds->M;
+  const double Md = (double)M;
+  const RowCtx c = make_ctx(a, row, P);
+  const int p0 = slice * g.len, p1 = min(a.V, p0 + g.len);
+  __syncthreads();  // (LDS of the previous item)
+  for (int b = tid; b < DNB; b += MT) {
+    sh.c.hi[b] = 0;
+    sh.c.lo[b] = 0;
+  }
+  stream_slice<DT, AL>(a, c, row, p0, p1, sh, [] {}, [&](float z, int, bool ok) __attribute__((always_inline)) {
+    if (ok && z > -INFINITY) {
+      const uint32_t b = dbin(z, M);
+      const Fx f = fx_of(exp_nonpos((double)z - Md, etab));
+      atomicAdd((unsigned long long *)&sh.c.hi[b], (unsigned long long)f.hi);
+      atomicAdd((unsigned long long *)&sh.c.lo[b], (unsigned long long)(f.lo | (1ull << 48)));
+    }
+  });
+  uint64_t *gh = a.dhist + (size_t)slot * 3 * DNB;
+  for (int b = tid; b < DNB; b += MT) {
+    const uint64_t lo = sh.c.lo[b];
+    if (lo) {
+      atomic_add_ag(&gh[b], lo >> 48);
+      atomic_add_ag(&gh[DNB + b], sh.c.hi[b]);
+      atomic_add_ag(&gh[2 * DNB + b], lo & ((1ull << 48) - 1ull));
+    }
+  }
+  // Ticket: the row's last slice plans it.
+  store_wait();
+  __syncthreads();
+  if (tid == 0) sh.ticket = ticket_add(&ds->cdone);
+  __syncthreads();
+  const bool lastc = sh.ticket == (uint32_t)(g.S - 1);
+  __syncthreads();  // (every thread has read the ticket: the plan's tables reuse the slice's LDS)
+  if (!lastc) return;
+  __builtin_amdgcn_s_setprio(3);  // (the row's other slices wait for the plan)
+  plan_block(gh, ds, a.mode, ps.pl);
+  if (tid == 0) ds->cdone = 0u;
+}
+
 
 template <int DT, bool AL>
 __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice, const DGeom &g, PickShared &ps,
@@ -832,7 +854,7 @@ __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
   if (nd == 0) return;
   if (threadIdx.x < 64) etab[threadIdx.x] = EXP2_64[threadIdx.x];  // (published by the first barrier of an item)
   const DGeom g = deep_geom(a, nd);
-  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) count_item<DT, AL>(a, i / g.S, i % g.S, g, sh.d, etab);
+  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) count_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab);
   for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) pick_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab);
 }
 
