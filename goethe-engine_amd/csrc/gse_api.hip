@@ -41,7 +41,9 @@ struct gse_handle {
   gse::Fx *ppart = nullptr;           // [max_rows][nsl]
   int32_t *plast = nullptr;           // [max_rows][nsl]
   uint64_t *ptop = nullptr;           // [max_rows][nsl][4 * GSE_MAX_KIDS]
-  uint32_t *ptick = nullptr;          // [max_rows]
+  uint32_t *ptick = nullptr;
+  uint32_t *plist = nullptr;          // [GSE_MAX_KIDS + 1][max_rows] nodes of each verify residual pass
+  uint32_t *pcnt = nullptr;           // [GSE_MAX_KIDS + 1]          // [max_rows]
   hipEvent_t (*ring)[5] = nullptr;  // kernel boundaries of up to GSE_PROFILE_CALLS profiled calls
   int nring = 0;                    // calls recorded
   int nprof = 0;                    // kernels per recorded call
@@ -239,6 +241,8 @@ void carve(gse_handle *h, void *block, const gse::Layout &L, bool tree) {
   h->plast = (int32_t *)(b + L.plast);
   h->ptop = (uint64_t *)(b + L.ptop);
   h->ptick = (uint32_t *)(b + L.ptick);
+  h->plist = (uint32_t *)(b + L.plist);
+  h->pcnt = (uint32_t *)(b + L.pcnt);
 }
 
 
@@ -462,6 +466,9 @@ GSE_API int gse_verify_tree(gse_handle *h, const gse_batch *in, const gse_tree *
   L.requests = (int)t.requests;
   L.sampled = h->ttok;
   L.st = h->tstate;
+  L.plist = h->plist;
+  L.pcnt = h->pcnt;
+  L.pgrid = (int)h->target;
   L.npart = h->npart;
   L.tseg = h->tseg;
   L.nlast = h->nlast;

@@ -170,6 +170,8 @@ struct TreeLaunch {
   Fx *npart;
   int32_t *nlast;
   uint64_t *tseg;
+  uint32_t *plist, *pcnt;  // [GSE_MAX_KIDS + 1][rows]: the nodes each residual pass r takes; [GSE_MAX_KIDS + 1]: counts
+  int pgrid;               // workgroups of a residual pass
   double *qmax;
   Fx *qpart;
   QFin *qfin;
@@ -190,7 +192,7 @@ struct PickLaunch {
 // counters and flags zero between calls). tree: with the buffers of verify rounds and drafter picks.
 struct Layout {
   size_t rec, cand, info, done, dctl, dslot, dhist, dlist;
-  size_t ttok, tstate, npart, nlast, tseg, qmax, qpart, qfin, pmax, ppart, plast, ptop, ptick;
+  size_t ttok, tstate, npart, nlast, tseg, qmax, qpart, qfin, pmax, ppart, plast, ptop, ptick, plist, pcnt;
   size_t total;
   uint32_t nrec, nsl, slots;
 };
@@ -231,6 +233,8 @@ constexpr Layout plan_layout(uint32_t R, uint32_t V, uint32_t target, bool tree)
     L.plast = put((size_t)R * S * sizeof(int32_t));
     L.ptop = put((size_t)R * S * 4 * GSE_MAX_KIDS * sizeof(uint64_t));
     L.ptick = put((size_t)R * sizeof(uint32_t));
+    L.plist = put((size_t)(GSE_MAX_KIDS + 1) * R * sizeof(uint32_t));  // the nodes of each residual pass
+    L.pcnt = put((GSE_MAX_KIDS + 1) * sizeof(uint32_t));
   }
   L.total = o;
   return L;

@@ -414,11 +414,19 @@ struct TreeArgs {
   Fx *npart;               // [nodes][GSE_MAX_KIDS + 1][nsl]
   int32_t *nlast;          // [nodes][GSE_MAX_KIDS + 1][nsl]
   uint64_t *tseg;          // [nodes][nsl][2 TSEG]: segment sums {hi, lo} of the residual the node draws from
+  uint32_t *plist;         // [GSE_MAX_KIDS + 1][nodes]: the nodes residual pass r takes (appended by the kernel before it)
+  uint32_t *pcnt;          // [GSE_MAX_KIDS + 1]: their counts (cleared by the statistics pass)
   double *qmax;            // [qrows][nsl] slice maxima of z
   Fx *qpart;               // [qrows][nsl] slice masses exp(z - slice maximum)
   QFin *qfin;              // [qrows]
   gse_tree_out out;
 };
+
+// Node u takes residual pass r (thread 0 of its workgroup).
+__device__ __forceinline__ void pass_add(const TreeArgs &a, int r, int u) {
+  const uint32_t k = __hip_atomic_fetch_add(&a.pcnt[r], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  a.plist[(size_t)r * a.nodes + k] = (uint32_t)u;  // (a node enters each list once: k < nodes)
+}
 
 // Kids of node u found by one wave: lanes read 64 rows after u at a time, the kids (parent u) before the first row of
 // another request (parent -1) are appended in row order by lane 0 of the wave.
@@ -681,6 +689,7 @@ template <int DTK, int QKK>
 __global__ __launch_bounds__(TT) void tstats_kernel(TreeArgs a) {
   __shared__ TreeShared sh;
   const int s = blockIdx.x, y = blockIdx.y, tid = threadIdx.x;
+  if (s == 0 && y == 0 && tid <= GSE_MAX_KIDS) a.pcnt[tid] = 0u;  // (the residual passes' lists of this call)
   const int V = a.s.V, s0 = s * TS, s1 = min(V, s0 + TS);
   if (y < a.nodes) {
     const int u = y;
@@ -929,21 +938,27 @@ __global__ __launch_bounds__(TT) void tkid0_kernel(TreeArgs a) {
   if ((int)nd.next != 1) return;
   load_etab(sh);
   load_node(a, u, ns);  // (its barrier publishes the table)
-  if (ns.k.n == 0) return;
+  if (ns.k.n == 0) {  // (no kids: pass 1 draws)
+    if (threadIdx.x == 0) pass_add(a, 1, u);
+    return;
+  }
   const Tgt g = tgt_of(a, u, P);
-  if (test_kid(a, P, g, ns, 0, sh) && threadIdx.x == 0) {
-    nd.token = ns.k.tok[0];
-    nd.kid = ns.k.row[0];
-    nd.next = 0;
+  const bool acc = test_kid(a, P, g, ns, 0, sh);
+  if (threadIdx.x == 0) {
+    if (acc) {
+      nd.token = ns.k.tok[0];
+      nd.kid = ns.k.row[0];
+      nd.next = 0;
+    } else {
+      pass_add(a, 1, u);
+    }
   }
 }
 
-// Pass r over slice blockIdx.x of node blockIdx.y (see the file comment).
+// Pass r over slice s of node u (see the file comment).
 template <int DTK, int QKK>
-__global__ __launch_bounds__(TT) void tpass_kernel(TreeArgs a, int r) {
-  __shared__ TreeShared sh;
-  __shared__ NodeShared ns;
-  const int s = blockIdx.x, u = blockIdx.y, tid = threadIdx.x;
+__device__ __forceinline__ void tpass_item(const TreeArgs &a, int r, int u, int s, TreeShared &sh, NodeShared &ns) {
+  const int tid = threadIdx.x;
   const gse_row P = a.s.params[u];
   if (!node_live(a, u, P)) return;
   TreeNode &nd = a.st[u];
@@ -1065,6 +1080,7 @@ __global__ __launch_bounds__(TT) void tpass_kernel(TreeArgs a, int r) {
         nd.next = 0;
       } else {
         nd.next = r + 1;
+        pass_add(a, r + 1, u);
       }
     }
     return;
@@ -1074,6 +1090,20 @@ __global__ __launch_bounds__(TT) void tpass_kernel(TreeArgs a, int r) {
     nd.token = j;
     nd.kid = -1;
     nd.next = 0;
+  }
+}
+
+// Residual pass r: the (node, slice) items of the nodes listed for it, over a grid of at most one resident round (a
+// grid over every node and slice spent most of its time dispatching workgroups of nodes the pass does not take).
+template <int DTK, int QKK>
+__global__ __launch_bounds__(TT) void tpass_kernel(TreeArgs a, int r) {
+  __shared__ TreeShared sh;
+  __shared__ NodeShared ns;
+  const int items = (int)a.pcnt[r] * a.nsl;  // (written by the kernels before this one)
+  for (int it = blockIdx.x; it < items; it += gridDim.x) {
+    const int u = (int)a.plist[(size_t)r * a.nodes + it / a.nsl];
+    __syncthreads();  // (LDS of the previous item)
+    tpass_item<DTK, QKK>(a, r, u, it % a.nsl, sh, ns);
   }
 }
 
@@ -1316,6 +1346,8 @@ hipError_t launch_tree(const TreeLaunch &L, hipStream_t s) {
   a.npart = L.npart;
   a.nlast = L.nlast;
   a.tseg = L.tseg;
+  a.plist = L.plist;
+  a.pcnt = L.pcnt;
   a.qmax = L.qmax;
   a.qpart = L.qpart;
   a.qfin = L.qfin;
@@ -1327,8 +1359,12 @@ hipError_t launch_tree(const TreeLaunch &L, hipStream_t s) {
     hipLaunchKernelGGL((tstats_kernel<DT, QK>), dim3(a.nsl, a.nodes + (qlog ? L.q.rows : 0)), dim3(TT), 0, s, a);
     hipLaunchKernelGGL(tkid0_kernel, dim3(a.nodes), dim3(TT), 0, s, a);
     // pass r: kid r - 1 rejected -> res_r; a node with k kids needs passes 1..k (one without kids draws in pass 1)
-    for (int r = 1; r <= max(L.max_kids, 1); ++r)
-      hipLaunchKernelGGL((tpass_kernel<DT, QK>), dim3(a.nsl, a.nodes), dim3(TT), 0, s, a, r);
+    // pass 1 takes most live nodes: one resident round; later passes only nodes with more kids (a quarter round,
+    // workgroups take several items if there are more)
+    for (int r = 1; r <= max(L.max_kids, 1); ++r) {
+      const int pg = max(1, min(a.nsl * a.nodes, r == 1 ? L.pgrid : max(L.pgrid / 4, a.nsl)));
+      hipLaunchKernelGGL((tpass_kernel<DT, QK>), dim3(pg), dim3(TT), 0, s, a, r);
+    }
   };
   auto by_q = [&](auto dtc) {
     if (L.q.rows == 0) go(dtc, IntC<Q_NONE>{});
