@@ -197,3 +197,34 @@ def test_tree_drafter_matches_oracle(ge, gpu, shape, t):
         wt, wp, _ = spo.grow_dynamic(lambda pt: m.dist(s, pt).cpu().numpy().astype(np.float64), s.seed, 3, 6, 3, 3, t)
         assert (toks, par) == (wt, wp)
     assert (q is None) == (t == 0)
+
+
+def test_verify_passes_with_more_items_than_workgroups(ge, gpu):
+    """Residual passes that take more (node, slice) items than their grid (later passes run a quarter of a resident
+    round): 96 strict requests whose root has four kids the drafter favours but the target finds unlikely, so most
+    roots are rejected kid after kid and draw from their fourth residual, over a 131072-token vocabulary (16 slices a
+    row)."""
+    rng = np.random.default_rng(31)
+    v = 131072
+    P = ge.sampling.SamplingParams
+    parents = [0, 0, 0, 0]
+    calls, reqs = [], []
+    for a in range(96):
+        target = rng.normal(0, 1.5, size=(5, v)).astype(np.float32)
+        draft = (target + rng.normal(0, 0.6, size=target.shape)).astype(np.float32)
+        order = np.argsort(target[0], kind="stable")  # ascending: the first ids are the least likely
+        toks = [int(order[int(rng.integers(0, 1000))]) for _ in parents]
+        draft[0, toks] = draft[0].max() + 4.0  # the drafter favours them: p/q is tiny, the kids are rejected
+        p = P(temperature=1.0, accept="rejection")
+        seed = int(rng.integers(0, 1 << 62))
+        reqs.append((target, draft, toks, p, seed))
+        calls.append(dict(target=torch.from_numpy(target).to(gpu), tokens=toks, parents=parents, params=p, seed=seed,
+                          draft=torch.from_numpy(draft).to(gpu), draft_t=1.0))
+    print(f"[verify] 96 requests x 5 rows, V={v}", flush=True)
+    got = ge.spec.verify_tree(calls)
+    rejected = 0
+    for a, (target, draft, toks, p, seed) in enumerate(reqs):
+        want = spo.verify_tree(target, _q_of_draft(draft, parents), toks, parents, p, seed)
+        assert got[a] == want, (a, got[a], want)
+        rejected += len(want[1]) == 1
+    assert rejected > 48, rejected  # most roots went through all four residual passes
