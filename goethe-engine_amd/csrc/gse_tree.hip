@@ -305,14 +305,27 @@ __device__ __forceinline__ QGrp<QL> ld_qgrp(__amdgpu_buffer_rsrc_t qb, int t0) {
   return r;
 }
 
-// f(t0, group) for the thread's groups of slice s0 (token t0 + e TT is element e). Four groups are in registers: the
-// loop is unrolled by four so that each one is reloaded in place after its use (a copy of a register whose load is
-// still in flight would wait for the load), so every group is loaded three groups ahead of its use.
-template <typename Ld, typename F>
+// f(t0, group) for the thread's groups of slice s0 (token t0 + e TT is element e). RING groups are in registers: the
+// loop is unrolled by RING so that each one is reloaded in place after its use (a copy of a register whose load is
+// still in flight would wait for the load), so every group is loaded RING - 1 groups ahead of its use. Four suits the
+// kernels that keep four waves per SIMD; two frees the registers a heavier per-token body needs for a third wave.
+template <int RING = 4, typename Ld, typename F>
 __device__ __forceinline__ void slice_groups(int s0, Ld ld, F f) {
-  static_assert(NG % 4 == 0, "");
+  static_assert(NG % 4 == 0 && (RING == 2 || RING == 4), "");
   const int tid = threadIdx.x;
   auto t0_of = [&](int g) { return s0 + min(g, NG - 1) * 4 * TT + tid; };  // (past the end: the last group again)
+  if constexpr (RING == 2) {
+    auto b0 = ld(t0_of(0));
+    auto b1 = ld(t0_of(1));
+#pragma unroll 1
+    for (int g = 0; g < NG; g += 2) {
+      f(t0_of(g), b0);
+      b0 = ld(t0_of(g + 2));
+      f(t0_of(g + 1), b1);
+      b1 = ld(t0_of(g + 3));
+    }
+    return;
+  }
   auto b0 = ld(t0_of(0));
   auto b1 = ld(t0_of(1));
   auto b2 = ld(t0_of(2));
@@ -1002,7 +1015,7 @@ __device__ __forceinline__ void tpass_item(const TreeArgs &a, int r, int u, int 
       const int wv = tid >> 6;
       with_qv<QKK>(ns.k.nq > 0, q.t1, [&](auto qvc) {
         constexpr int QL = ql_of(decltype(qvc)::value), QK = qk_of(decltype(qvc)::value);
-        slice_groups(s0, [&](int t0) { return ld_grp<DT, QL>(tb, qb, t0); }, [&](int t0, const Grp<DT, QL> &gr) {
+        slice_groups<2>(s0, [&](int t0) { return ld_grp<DT, QL>(tb, qb, t0); }, [&](int t0, const Grp<DT, QL> &gr) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int i = t0 + e * TT;
@@ -1029,8 +1042,8 @@ __device__ __forceinline__ void tpass_item(const TreeArgs &a, int r, int u, int 
       });
     } else {
       // deeper chains or kids with several q rows: the q values read token by token
-      slice_groups(s0, [&](int t0) { return ld_grp<DT, Q_NONE>(tb, tb.x, t0); },
-                   [&](int t0, const Grp<DT, Q_NONE> &gr) {
+      slice_groups<2>(s0, [&](int t0) { return ld_grp<DT, Q_NONE>(tb, tb.x, t0); },
+                      [&](int t0, const Grp<DT, Q_NONE> &gr) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = t0 + e * TT;
@@ -1094,9 +1107,12 @@ __device__ __forceinline__ void tpass_item(const TreeArgs &a, int r, int u, int 
 }
 
 // Residual pass r: the (node, slice) items of the nodes listed for it, over a grid of at most one resident round (a
-// grid over every node and slice spent most of its time dispatching workgroups of nodes the pass does not take).
+// grid over every node and slice spent most of its time dispatching workgroups of nodes the pass does not take). Three
+// waves per SIMD where the f32 target's body fits them without spilling (the pass's items then take one round more
+// often).
 template <int DTK, int QKK>
-__global__ __launch_bounds__(TT) void tpass_kernel(TreeArgs a, int r) {
+__global__ __launch_bounds__(TT) __attribute__((amdgpu_waves_per_eu(DTK == GSE_F32 ? 3 : 2, 8))) void tpass_kernel(
+    TreeArgs a, int r) {
   __shared__ TreeShared sh;
   __shared__ NodeShared ns;
   const int items = (int)a.pcnt[r] * a.nsl;  // (written by the kernels before this one)
