@@ -46,9 +46,14 @@ constexpr int NSL = MAXP * PWAVES;     // wave lists of a row, at most (one per 
 static_assert(NWV == PWAVES, "");
 static_assert(NSL <= MT, "one wave list per resolve thread");
 
+constexpr int KHP = 4;                // history tokens per thread whose logits are loaded ahead (ranks below KHP MT)
+
 struct Shared {
   union {
-    HistTab h;                 // history of the part's tokens
+    struct {
+      HistTab h;               // history of the part's tokens
+      float hx[KHP * MT];      // logits of its first KHP MT ranks, loaded ahead of the side pass
+    };
     struct {
       uint64_t head[NH];       // listed elements at or above the certified key; then sorted (descending)
       uint64_t tmp[NH];        // the head grouped by bucket
@@ -806,20 +811,13 @@ __device__ __forceinline__ void chunk_sum(const ScanArgs &a, int row, int wl, fl
   rn.b += (double)s * (2.4e-7 + LV * 6.0e-8 + 5e-8) - (double)mom * 1.25e-7 + 1e-36;
 }
 
-// Tokens outside the stream (history tokens with their counts, ragged tokens with count 0; tok < 0: empty slot): logit,
-// penalties, NaN test, mask, z, then the same running state as the stream (tokens out of order: ties go to the lower id).
-// Every thread of the wave takes part, with empty slots where it has no token.
+// Tokens outside the stream (history tokens with their counts, ragged tokens with count 0; tok < 0: empty slot), with
+// their logits x0 and mask bits al: penalties, NaN test, mask, z, then the same running state as the stream (tokens out
+// of order: ties go to the lower id). Every thread of the wave takes part, with empty slots where it has no token.
 template <int N, bool GREEDY, bool DIV>
 __device__ __forceinline__ void side_tokens(const ScanArgs &a, const RowCtx &c, int row, int wl,
-                                            bool listing, const int (&tk)[N], const uint32_t (&cnt)[N], Run &rn,
-                                            float *proc) {
-  float x0[N];
-  bool al[N];
-#pragma unroll
-  for (int k = 0; k < N; ++k) {  // the loads first
-    x0[k] = tk[k] >= 0 ? load_one(c, tk[k]) : 0.0f;
-    al[k] = tk[k] >= 0 && mask_bit(c, tk[k]);
-  }
+                                            bool listing, const int (&tk)[N], const uint32_t (&cnt)[N],
+                                            const float (&x0)[N], const bool (&al)[N], Run &rn, float *proc) {
   float xr[N];
   float cmax = -INFINITY;
   bool hnan = false;
@@ -911,6 +909,21 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   } else {
     apc = tid == 0 ? (uint32_t)(pv - p0) : 0u;
   }
+  // The logits and mask words of the part's first KHP MT history tokens (by rank), loaded now so that the loads overlap
+  // the first chunks; they wait in LDS for the side pass (the logit in hx, the mask bit in bit 31 of the count). Every
+  // slot loads (an empty one from the part's first token), so no branch waits for the loads.
+  float hx0[KHP];
+  uint32_t hmw[KHP];
+  if (c.pen) {
+    const uint32_t nd = sh.h.nd;
+#pragma unroll
+    for (int k = 0; k < KHP; ++k) {
+      const uint32_t r = (uint32_t)(tid + k * MT);
+      const int t = p0 + (r < nd ? (int)sh.h.off[r] : 0);
+      hx0[k] = load_one(c, t);
+      hmw[k] = c.mw ? c.mw[t >> 5] >> (t & 31) : 1u;
+    }
+  }
 
   if (c.pen) {  // (the first two chunks were loaded before the history tables existed)
     hist_words<DT>(sh.h, cst(c0), p0, p1, ha);
@@ -982,7 +995,18 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   }
   int c2 = grab();
   load_u<DT, AL, MASKED>(c, rbuf, cst(c2), pv, p1, xc, mcw);
-  if (c.pen) hist_words<DT>(sh.h, cst(c2), p0, p1, hc);
+  if (c.pen) {
+    hist_words<DT>(sh.h, cst(c2), p0, p1, hc);
+    const uint32_t nd = sh.h.nd;
+#pragma unroll
+    for (int k = 0; k < KHP; ++k) {  // (rank r is this thread's in the side pass too: no barrier)
+      const uint32_t r = (uint32_t)(tid + k * MT);
+      if (r < nd) {
+        sh.hx[r] = hx0[k];
+        sh.h.cnt[r] |= (hmw[k] & 1u) << 31;
+      }
+    }
+  }
   if (c0 < nck) {
     if (listing) chunk_sum<EPL>(a, row, wl, cmax, xa, rn, tok_of(p0 + c0 * CHK));
     else rn.m = fmaxf(rn.m, cmax);
@@ -1023,13 +1047,24 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     const uint32_t nd = sh.h.nd;
     int tk[KH];
     uint32_t cn[KH];
+    float x0[KH];
+    bool al[KH];
 #pragma unroll
     for (int k = 0; k < KH; ++k) {
       const uint32_t r = (uint32_t)(tid + k * MT);
       tk[k] = r < nd ? p0 + (int)sh.h.off[r] : -1;
-      cn[k] = r < nd ? sh.h.cnt[r] : 0u;
+      const uint32_t cw = r < nd ? sh.h.cnt[r] : 0u;
+      if (k < KHP) {  // loaded ahead
+        cn[k] = cw & 0x7FFFFFFFu;
+        x0[k] = r < nd ? sh.hx[r] : 0.0f;
+        al[k] = r < nd && (cw >> 31) != 0u;
+      } else {
+        cn[k] = cw;
+        x0[k] = tk[k] >= 0 ? load_one(c, tk[k]) : 0.0f;
+        al[k] = tk[k] >= 0 && mask_bit(c, tk[k]);
+      }
     }
-    side_tokens<KH, GREEDY, DIV>(a, c, row, wl, listing, tk, cn, rn, proc);
+    side_tokens<KH, GREEDY, DIV>(a, c, row, wl, listing, tk, cn, x0, al, rn, proc);
   }
   if (AL && pv < p1 && w == 0) {  // (uniform: at most VEC - 1 tokens, wave 0)
     const int t = pv + lane;
@@ -1039,7 +1074,9 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
       const int o = t - p0;
       if (!(c.pen && ((sh.h.bits[o >> 5] >> (o & 31)) & 1u))) tk[0] = t;
     }
-    side_tokens<1, GREEDY, DIV>(a, c, row, wl, listing, tk, cn, rn, proc);
+    const float x0[1] = {tk[0] >= 0 ? load_one(c, tk[0]) : 0.0f};
+    const bool al[1] = {tk[0] >= 0 && mask_bit(c, tk[0])};
+    side_tokens<1, GREEDY, DIV>(a, c, row, wl, listing, tk, cn, x0, al, rn, proc);
   }
 
   // Part record: the part maximum, then every lane's sum rescaled to it (fp64, fixed order).
