@@ -66,17 +66,19 @@ __device__ __forceinline__ void atomic_add_ag(uint64_t *p, uint64_t v) {
 // double-buffered loop whose loads are the same for every chunk (a chunk past the end reads the row's first one), so
 // one chunk stays in flight while the wave works on another; the history ids and each wave's first chunks are loaded
 // before the history tables are built. A partial last chunk is taken by wave 0 afterwards, with bounds checks.
-// pre() runs (every thread) once the history tables are built, before the first chunk is used. f(z, token, valid) is
+// With keep, the history tables in LDS are already the slice's (built by the count item of the same slice) and are not
+// built again. pre() runs (every thread) once the history tables are built, before the first chunk is used. f(z, token, valid) is
 // called for every element slot of each chunk by every lane of the wave (valid false past the slice end), so f may use
 // ballots. Ends with a barrier.
 template <int DT, bool AL, typename Pre, typename F>
 __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c, int row, int p0, int p1,
-                                             DeepShared &sh, Pre pre, F f) {
+                                             DeepShared &sh, bool keep, Pre pre, F f) {
   using L = Lay<DT>;
   const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
   const int nfull = (p1 - p0) / CHK;
+  const bool build = c.pen && !keep;
   int hid[HPT];
-  if (c.pen) {
+  if (build) {
 #pragma unroll
     for (int k = 0; k < HPT; ++k) {
       const int j = c.hb + k * MT + tid;
@@ -88,9 +90,12 @@ __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c,
   const int wu = __builtin_amdgcn_readfirstlane(w);  // (the wave index as a scalar: the chunk loop stays uniform)
   int ck = wu;
   if (nfull > 0) load_full<DT, AL>(c, p0 + ck * CHK, ck < nfull, xa, ma);
-  if (tid == 0) sh.hover = 0;
-  if (c.pen) build_history(c, a.hist, hid, p0, p1, sh.h, sh.wsum, sh.hover);
-  else __syncthreads();
+  if (build) {
+    if (tid == 0) sh.hover = 0;
+    build_history(c, a.hist, hid, p0, p1, sh.h, sh.wsum, sh.hover);
+  } else {
+    __syncthreads();
+  }
   pre();
   Lane ln;
   ln.m = -INFINITY;
@@ -167,8 +172,8 @@ __device__ __forceinline__ DGeom deep_geom(const ScanArgs &a, int nd) {
 // last count slice: thread t holds bins 2t and 2t + 1; inclusive prefixes by block scans (wave scans, then the wave
 // totals in order), "first bin with" queries by LDS minima, and lookups at the window edges from LDS tables.
 struct PlanShared {
-  uint64_t pc[DNB], ph[DNB], po[DNB];  // inclusive prefixes through each bin: counts, masses in 2^-40 and 2^-64 units
-  double pm[DNB];                      // the fp64 value of the mass prefix
+  uint64_t ph[DNB], po[DNB];  // inclusive prefixes through each bin: masses in 2^-40 and 2^-64 units
+  uint32_t pc[DNB];           // and element counts (a row has fewer than 2^32 elements)
   uint64_t wt[3][NWV];                 // wave totals
   uint32_t q[8];                       // queries: first / last bins
 };
@@ -235,10 +240,9 @@ __device__ __forceinline__ void plan_block(const uint64_t *gh, DeepSlot *ds, int
       ro += mo[j];
       pc[j] = rc;
       pm[j] = fx_val(Fx{rh, ro});
-      sh.pc[tid * BPT + j] = rc;
+      sh.pc[tid * BPT + j] = (uint32_t)rc;
       sh.ph[tid * BPT + j] = rh;
       sh.po[tid * BPT + j] = ro;
-      sh.pm[tid * BPT + j] = pm[j];
     }
   }
   const double S = fx_val(Fx{htot, otot});
@@ -296,7 +300,8 @@ __device__ __forceinline__ void plan_block(const uint64_t *gh, DeepSlot *ds, int
   // masses before w1lo and through w1hi, then the windows of the draw
   uint32_t w2lo = w1lo, w2hi = w1hi;
   if (mode == MODE_SAMPLE) {
-    const double qd0 = at(sh.pm, (int)w1lo - 1), qd1 = at(sh.pm, (int)w1hi);
+    const double qd0 = fx_val(Fx{at(sh.ph, (int)w1lo - 1), at(sh.po, (int)w1lo - 1)});  // (pm of those bins)
+    const double qd1 = fx_val(Fx{at(sh.ph, (int)w1hi), at(sh.po, (int)w1hi)});
     const double tlo = u * (qd0 - delta) - delta, thi = u * (qd1 + delta) + delta;
     uint32_t b3 = DNB - 1, b4 = DNB - 1;
 #pragma unroll
@@ -325,7 +330,7 @@ __device__ __forceinline__ void plan_block(const uint64_t *gh, DeepSlot *ds, int
     // windows (1), after the cut window (counts), and the rest of the mass (2)
     const bool sep = w1lo > w2hi + 1;
     const uint64_t n0 = at(sh.pc, (int)w2lo - 1);
-    const uint64_t n1 = sep ? at(sh.pc, (int)w1lo - 1) - at(sh.pc, (int)w2hi) : 0ull;
+    const uint64_t n1 = sep ? (uint64_t)(at(sh.pc, (int)w1lo - 1) - at(sh.pc, (int)w2hi)) : 0ull;
     const uint64_t n2 = ctot - at(sh.pc, (int)w1hi);
     const uint64_t inw = ctot - n0 - n1 - n2;
     const uint64_t x0h = at(sh.ph, (int)w2lo - 1), x0o = at(sh.po, (int)w2lo - 1);
@@ -701,9 +706,14 @@ __device__ __noinline__ void finish_row(const FinArgs a, DeepSlot *ds, FinShared
   }
 }
 
+// The plan's tables lie past the history tables, so that the planning workgroup's pick item (the same slice) keeps
+// them.
 union PickShared {
   DeepShared d;
-  PlanShared pl;
+  struct {
+    HistTab h;
+    PlanShared pl;
+  } p;
   FinShared f;
 };
 
@@ -724,7 +734,7 @@ __device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slic
     sh.c.hi[b] = 0;
     sh.c.lo[b] = 0;
   }
-  stream_slice<DT, AL>(a, c, row, p0, p1, sh, [] {}, [&](float z, int, bool ok) __attribute__((always_inline)) {
+  stream_slice<DT, AL>(a, c, row, p0, p1, sh, false, [] {}, [&](float z, int, bool ok) __attribute__((always_inline)) {
     if (ok && z > -INFINITY) {
       const uint32_t b = dbin(z, M);
       const Fx f = fx_of(exp_nonpos((double)z - Md, etab));
@@ -750,14 +760,14 @@ __device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slic
   __syncthreads();  // (every thread has read the ticket: the plan's tables reuse the slice's LDS)
   if (!lastc) return;
   __builtin_amdgcn_s_setprio(3);  // (the row's other slices wait for the plan)
-  plan_block(gh, ds, a.mode, ps.pl);
+  plan_block(gh, ds, a.mode, ps.p.pl);
   if (tid == 0) ds->cdone = 0u;
 }
 
 
 template <int DT, bool AL>
 __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice, const DGeom &g, PickShared &ps,
-                                          const double *etab) {
+                                          const double *etab, bool keep) {
   DeepShared &sh = ps.d;
   const int tid = threadIdx.x;
   DeepSlot *ds = a.dslot + slot;
@@ -799,7 +809,7 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
       w1hi = ld_ag(&ds->w1hi);
     }
   };
-  stream_slice<DT, AL>(a, c, row, p0, p1, sh, wait_plan, [&](float z, int t, bool ok) __attribute__((always_inline)) {
+  stream_slice<DT, AL>(a, c, row, p0, p1, sh, keep, wait_plan, [&](float z, int t, bool ok) __attribute__((always_inline)) {
     if (planned && ok && z > -INFINITY) {
       const uint32_t b = dbin(z, Mf);
       if ((b >= w2lo && b <= w2hi) || (b >= w1lo && b <= w1hi)) {
@@ -855,7 +865,9 @@ __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
   if (threadIdx.x < 64) etab[threadIdx.x] = EXP2_64[threadIdx.x];  // (published by the first barrier of an item)
   const DGeom g = deep_geom(a, nd);
   for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) count_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab);
-  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) pick_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab);
+  // one item per workgroup in each pass: the pick item is the count item's slice, whose history tables are still in LDS
+  const bool keep = nd * g.S <= (int)gridDim.x;
+  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) pick_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab, keep);
 }
 
 template <int DT, bool AL>
