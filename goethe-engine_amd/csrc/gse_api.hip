@@ -44,6 +44,8 @@ struct gse_handle {
   uint32_t *ptick = nullptr;
   uint32_t *plist = nullptr;          // [GSE_MAX_KIDS + 1][max_rows] nodes of each verify residual pass
   uint32_t *pcnt = nullptr;           // [GSE_MAX_KIDS + 1]          // [max_rows]
+  hipStream_t side = nullptr;       // verify rounds: the q rows' statistics run here, beside the selection pass
+  hipEvent_t fork = nullptr, join = nullptr;
   hipEvent_t (*ring)[5] = nullptr;  // kernel boundaries of up to GSE_PROFILE_CALLS profiled calls
   int nring = 0;                    // calls recorded
   int nprof = 0;                    // kernels per recorded call
@@ -452,9 +454,6 @@ GSE_API int gse_verify_tree(gse_handle *h, const gse_batch *in, const gse_tree *
   a.tokens = h->ttok;
   hipStream_t s = (hipStream_t)b.stream;
   hipError_t e;
-  if ((e = gse::launch_main(a, s)) != hipSuccess) return hip_fail(h, e, "main launch");
-  if (a.dgrid > 0 && (e = gse::launch_deep(a, s)) != hipSuccess) return hip_fail(h, e, "deep launch");
-  if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
   gse::TreeLaunch L = {};
   L.s = a;
   L.parent = t.parent;
@@ -476,7 +475,34 @@ GSE_API int gse_verify_tree(gse_handle *h, const gse_batch *in, const gse_tree *
   L.qpart = h->qpart;
   L.qfin = h->qfin;
   L.out = o;
-  if ((e = gse::launch_tree(L, s)) != hipSuccess) return hip_fail(h, e, "verify launch");
+  // The drafter rows' statistics need only the inputs: they run on the handle's side stream (forked from the caller's
+  // stream after its earlier work, joined before the kid tests), so that their workgroups fill the slots the selection
+  // pass leaves idle. They are queued after the main pass, whose workgroups then take the device first. Streams keep
+  // the default priority.
+  hipEvent_t qdone = nullptr;
+  const bool side = gse::tree_has_qstats(L);
+  if (side) {
+    if (!h->side) {
+      if ((e = hipStreamCreateWithFlags(&h->side, hipStreamNonBlocking)) != hipSuccess) {
+        h->side = nullptr;
+        return hip_fail(h, e, "side stream");
+      }
+      if ((e = hipEventCreateWithFlags(&h->fork, hipEventDisableTiming)) != hipSuccess ||
+          (e = hipEventCreateWithFlags(&h->join, hipEventDisableTiming)) != hipSuccess)
+        return hip_fail(h, e, "side stream events");
+    }
+    if ((e = hipEventRecord(h->fork, s)) != hipSuccess) return hip_fail(h, e, "side stream fork");
+  }
+  if ((e = gse::launch_main(a, s)) != hipSuccess) return hip_fail(h, e, "main launch");
+  if (side) {
+    if ((e = hipStreamWaitEvent(h->side, h->fork, 0)) != hipSuccess) return hip_fail(h, e, "side stream fork");
+    if ((e = gse::launch_qstats(L, h->side)) != hipSuccess) return hip_fail(h, e, "q statistics launch");
+    if ((e = hipEventRecord(h->join, h->side)) != hipSuccess) return hip_fail(h, e, "side stream join");
+    qdone = h->join;
+  }
+  if (a.dgrid > 0 && (e = gse::launch_deep(a, s)) != hipSuccess) return hip_fail(h, e, "deep launch");
+  if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
+  if ((e = gse::launch_tree(L, s, qdone)) != hipSuccess) return hip_fail(h, e, "verify launch");
   return GSE_OK;
 }
 
@@ -587,6 +613,9 @@ GSE_API void gse_close(gse_handle *h) {
     DeviceGuard g(h->device);
     (void)hipDeviceSynchronize();
     if (h->owned && h->block) (void)hipFree(h->block);
+    if (h->fork) (void)hipEventDestroy(h->fork);
+    if (h->join) (void)hipEventDestroy(h->join);
+    if (h->side) (void)hipStreamDestroy(h->side);
     if (h->ring) {
       for (int c = 0; c < GSE_PROFILE_CALLS; ++c)
         for (int i = 0; i < 5; ++i)

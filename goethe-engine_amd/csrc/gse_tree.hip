@@ -697,11 +697,12 @@ __device__ __forceinline__ Tgt tgt_of(const TreeArgs &a, int u, const gse_row &P
 
 // Per MSS node: the exact kept mass per slice (the last slice forms C). Per logits q row: the slice maximum m of z and
 // the slice mass exp(z - m) (the last slice forms M = max m and E = sum over slices of mass * exp(m - M), in slice
-// order: within a few ulp of the sum of exp(z - M) over the row).
+// order: within a few ulp of the sum of exp(z - M) over the row). Row y = blockIdx.y + ybase: node y, or q row
+// y - nodes (the q rows depend on the inputs only, so they may run in a launch of their own).
 template <int DTK, int QKK>
-__global__ __launch_bounds__(TT) void tstats_kernel(TreeArgs a) {
+__global__ __launch_bounds__(TT) void tstats_kernel(TreeArgs a, int ybase) {
   __shared__ TreeShared sh;
-  const int s = blockIdx.x, y = blockIdx.y, tid = threadIdx.x;
+  const int s = blockIdx.x, y = (int)blockIdx.y + ybase, tid = threadIdx.x;
   if (s == 0 && y == 0 && tid <= GSE_MAX_KIDS) a.pcnt[tid] = 0u;  // (the residual passes' lists of this call)
   const int V = a.s.V, s0 = s * TS, s1 = min(V, s0 + TS);
   if (y < a.nodes) {
@@ -1345,7 +1346,9 @@ __global__ __launch_bounds__(TT) void pick3_kernel(PickArgs a) {
 
 }  // namespace
 
-hipError_t launch_tree(const TreeLaunch &L, hipStream_t s) {
+namespace {
+
+TreeArgs tree_args(const TreeLaunch &L) {
   TreeArgs a;
   a.s = L.s;
   a.parent = L.parent;
@@ -1368,11 +1371,45 @@ hipError_t launch_tree(const TreeLaunch &L, hipStream_t s) {
   a.qpart = L.qpart;
   a.qfin = L.qfin;
   a.out = L.out;
-  const bool qlog = L.q.rows > 0 && L.q.kind != GSE_Q_PROB;
+  return a;
+}
+
+// f(IntC<logits type>, IntC<q kind>) for the call's instance
+template <typename F>
+void by_instance(const TreeLaunch &L, F f) {
+  auto by_q = [&](auto dtc) {
+    if (L.q.rows == 0) f(dtc, IntC<Q_NONE>{});
+    else if (L.q.kind == GSE_Q_PROB) f(dtc, IntC<GSE_Q_PROB>{});
+    else if (L.q.kind == GSE_Q_LOGITS_BF16) f(dtc, IntC<GSE_Q_LOGITS_BF16>{});
+    else f(dtc, IntC<GSE_Q_LOGITS_F32>{});
+  };
+  if (L.s.dtype == GSE_BF16) by_q(IntC<GSE_BF16>{});
+  else by_q(IntC<GSE_F32>{});
+}
+
+}  // namespace
+
+bool tree_has_qstats(const TreeLaunch &L) { return L.q.rows > 0 && L.q.kind != GSE_Q_PROB; }
+
+hipError_t launch_qstats(const TreeLaunch &L, hipStream_t s) {
+  const TreeArgs a = tree_args(L);
+  if (!tree_has_qstats(L)) return hipSuccess;
+  by_instance(L, [&](auto dtc, auto qkc) {
+    constexpr int DT = decltype(dtc)::value, QK = decltype(qkc)::value;
+    hipLaunchKernelGGL((tstats_kernel<DT, QK>), dim3(a.nsl, L.q.rows), dim3(TT), 0, s, a, a.nodes);
+  });
+  return hipGetLastError();
+}
+
+hipError_t launch_tree(const TreeLaunch &L, hipStream_t s, hipEvent_t qdone) {
+  const TreeArgs a = tree_args(L);
+  // the q rows' statistics in this launch too, unless they ran on their own (qdone: their launch's end)
+  const int yq = tree_has_qstats(L) && !qdone ? (int)L.q.rows : 0;
   // the instances for the call's logits type and q kind
   auto go = [&](auto dtc, auto qkc) {
     constexpr int DT = decltype(dtc)::value, QK = decltype(qkc)::value;
-    hipLaunchKernelGGL((tstats_kernel<DT, QK>), dim3(a.nsl, a.nodes + (qlog ? L.q.rows : 0)), dim3(TT), 0, s, a);
+    hipLaunchKernelGGL((tstats_kernel<DT, QK>), dim3(a.nsl, a.nodes + yq), dim3(TT), 0, s, a, 0);
+    if (qdone) (void)hipStreamWaitEvent(s, qdone, 0);
     hipLaunchKernelGGL(tkid0_kernel, dim3(a.nodes), dim3(TT), 0, s, a);
     // pass r: kid r - 1 rejected -> res_r; a node with k kids needs passes 1..k (one without kids draws in pass 1)
     // pass 1 takes most live nodes: one resident round; later passes only nodes with more kids (a quarter round,
@@ -1382,14 +1419,7 @@ hipError_t launch_tree(const TreeLaunch &L, hipStream_t s) {
       hipLaunchKernelGGL((tpass_kernel<DT, QK>), dim3(pg), dim3(TT), 0, s, a, r);
     }
   };
-  auto by_q = [&](auto dtc) {
-    if (L.q.rows == 0) go(dtc, IntC<Q_NONE>{});
-    else if (L.q.kind == GSE_Q_PROB) go(dtc, IntC<GSE_Q_PROB>{});
-    else if (L.q.kind == GSE_Q_LOGITS_BF16) go(dtc, IntC<GSE_Q_LOGITS_BF16>{});
-    else go(dtc, IntC<GSE_Q_LOGITS_F32>{});
-  };
-  if (L.s.dtype == GSE_BF16) by_q(IntC<GSE_BF16>{});
-  else by_q(IntC<GSE_F32>{});
+  by_instance(L, go);
   hipLaunchKernelGGL(walk_kernel, dim3((max(a.requests, a.nodes) + 63) / 64), dim3(64), 0, s, a);
   return hipGetLastError();
 }

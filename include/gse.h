@@ -240,7 +240,9 @@ GSE_API int gse_dist(gse_handle *h, const gse_batch *in, double *probs, int64_t 
 /* Replaces: the acceptance walk of goethe_engine/engine.py:262-298 (one sample() call per tree level, dist + mss per
  * strict node, spec.py:88-103) with one call that runs every node of every request on the device and walks the trees
  * there: no host round trip per level. Stop rules (engine.py:218-229) stay with the caller, which ends each emitted
- * sequence at its first stop reason; the tokens before it do not depend on what follows. in->rows are the tree nodes. */
+ * sequence at its first stop reason; the tokens before it do not depend on what follows. in->rows are the tree nodes.
+ * With drafter logits, the q rows' statistics run on a stream of the handle, forked from in->stream at the call's start
+ * and joined back before they are used: the call stays ordered on in->stream like every other. */
 GSE_API int gse_verify_tree(gse_handle *h, const gse_batch *in, const gse_tree *tree, const gse_tree_out *out);
 
 /* Replaces: goethe_engine/spec.py:151-159 TreeDrafter._pick (torch.sort / softmax / draw on the host) for a batch of

@@ -228,3 +228,41 @@ def test_verify_passes_with_more_items_than_workgroups(ge, gpu):
         assert got[a] == want, (a, got[a], want)
         rejected += len(want[1]) == 1
     assert rejected > 48, rejected  # most roots went through all four residual passes
+
+
+def test_verify_rounds_back_to_back_on_a_stream(ge, gpu):
+    """Two verify rounds with drafter logits (their q-row statistics run on the library's side stream, forked from and
+    joined to the caller's stream), launched alternately four times each on a non-default stream without any
+    synchronisation: every launch's output equals a synchronised launch's, which equals the oracle walk's."""
+    reqs = ge.workloads.c4()
+    other = [dict(r, seed=(r["seed"] * 7 + 3) % (1 << 62)) for r in reqs[:12]]
+
+    def call_of(rs):
+        return ge.spec.VerifyCall([dict(target=torch.from_numpy(r["target"]).to(gpu), tokens=r["tokens"],
+                                        parents=r["parents"], params=r["params"], seed=r["seed"],
+                                        draft=torch.from_numpy(r["draft"]).to(gpu), draft_t=1.0) for r in rs])
+
+    def snap(c):
+        return torch.cat([c.e_len[:, None], c.e_st[:, None], c.e_tok, c.e_node], 1).clone()
+
+    calls, refs = [call_of(reqs), call_of(other)], []
+    for c, rs in zip(calls, [reqs, other]):
+        c.launch()
+        torch.cuda.synchronize()
+        got = c.result()
+        for a, r in enumerate(rs):
+            want = spo.verify_tree(r["target"], _q_of_draft(r["draft"], r["parents"]), r["tokens"], r["parents"],
+                                   r["params"], r["seed"])
+            assert got[a] == want, (a, got[a], want)
+        refs.append(snap(c))
+    print("[verify] back-to-back rounds on a side stream", flush=True)
+    st = torch.cuda.Stream(gpu)  # (default priority)
+    snaps = []
+    with torch.cuda.stream(st):
+        for _ in range(4):
+            for c in calls:
+                c.launch()
+                snaps.append(snap(c))
+    torch.cuda.synchronize()
+    for k, sn in enumerate(snaps):
+        assert torch.equal(sn, refs[k % 2]), k
