@@ -368,6 +368,15 @@ GSE_API int gse_open(const gse_open_params *p, gse_handle **out) {
   }
   h->owned = true;
   carve(h, block, L, true);
+  // the verify rounds' side stream (default priority) and its fork / join events, made here so that no call creates
+  // them (a call may be under graph capture)
+  if ((e = hipStreamCreateWithFlags(&h->side, hipStreamNonBlocking)) != hipSuccess ||
+      (e = hipEventCreateWithFlags(&h->fork, hipEventDisableTiming)) != hipSuccess ||
+      (e = hipEventCreateWithFlags(&h->join, hipEventDisableTiming)) != hipSuccess) {
+    fail(nullptr, GSE_E_DEVICE, "side stream: %s", hipGetErrorString(e));
+    gse_close(h);
+    return GSE_E_DEVICE;
+  }
   *out = h;
   return GSE_OK;
 }
@@ -481,18 +490,8 @@ GSE_API int gse_verify_tree(gse_handle *h, const gse_batch *in, const gse_tree *
   // the default priority.
   hipEvent_t qdone = nullptr;
   const bool side = gse::tree_has_qstats(L);
-  if (side) {
-    if (!h->side) {
-      if ((e = hipStreamCreateWithFlags(&h->side, hipStreamNonBlocking)) != hipSuccess) {
-        h->side = nullptr;
-        return hip_fail(h, e, "side stream");
-      }
-      if ((e = hipEventCreateWithFlags(&h->fork, hipEventDisableTiming)) != hipSuccess ||
-          (e = hipEventCreateWithFlags(&h->join, hipEventDisableTiming)) != hipSuccess)
-        return hip_fail(h, e, "side stream events");
-    }
-    if ((e = hipEventRecord(h->fork, s)) != hipSuccess) return hip_fail(h, e, "side stream fork");
-  }
+  if (side && !h->side) return fail(h, GSE_E_DEVICE, "the handle has no side stream");
+  if (side && (e = hipEventRecord(h->fork, s)) != hipSuccess) return hip_fail(h, e, "side stream fork");
   if ((e = gse::launch_main(a, s)) != hipSuccess) return hip_fail(h, e, "main launch");
   if (side) {
     if ((e = hipStreamWaitEvent(h->side, h->fork, 0)) != hipSuccess) return hip_fail(h, e, "side stream fork");
