@@ -887,7 +887,10 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   constexpr int APW = (PTOK / 32 + MT - 1) / MT;  // mask words per thread
   const int nmw = (pv - p0 + 31) >> 5;
   uint32_t mwd[APW];
-  if constexpr (MASKED) {
+  // (only the listing threshold uses the count: a greedy row without logprobs skips it; for sampled rows listing is
+  // true at compile time and the loads are unconditional)
+  const bool count_allowed = MASKED && listing;
+  if (count_allowed) {
 #pragma unroll
     for (int k = 0; k < APW; ++k) mwd[k] = c.mw[(p0 >> 5) + max(min(tid + k * MT, nmw - 1), 0)];
   }
@@ -897,7 +900,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   uint32_t apc = 0;
   if constexpr (MASKED) {
 #pragma unroll
-    for (int k = 0; k < APW; ++k) {
+    for (int k = 0; k < (count_allowed ? APW : 0); ++k) {
       const int i = tid + k * MT;
       if (i < nmw) {
         uint32_t word = mwd[k];
@@ -1105,8 +1108,10 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     s = rn.s * f;
     b = rn.b * f;
   }
-  s = block_sum_f64(s, sh.wred);
-  b = block_sum_f64(b, sh.wred);
+  if (listing) {  // (without a listing the sums are zero)
+    s = block_sum_f64(s, sh.wred);
+    b = block_sum_f64(b, sh.wred);
+  }
   if (tid == 0) {
     // flags: a finite value exists if the maximum of z over the allowed tokens is finite; a maximum of +inf (x = +inf,
     // or x / T overflowing) leaves the row to the exact path
