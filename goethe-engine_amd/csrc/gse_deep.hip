@@ -31,7 +31,7 @@ using namespace strm;
 
 constexpr float BSC = 32.0f;    // bins per unit of d
 constexpr int BPT = DNB / MT;   // planner: bins per thread (contiguous)
-constexpr int WLC = 512;        // window elements a slice gathers in LDS before one global reservation
+constexpr int WLC = 1024;       // window elements a slice gathers in LDS before one global reservation (the histogram's space)
 static_assert(BPT * MT == DNB, "");
 
 struct DeepShared {
