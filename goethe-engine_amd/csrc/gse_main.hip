@@ -320,6 +320,13 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
   return EV_DONE;
 }
 
+// A verify node that takes dist + mss and keeps every token (sampling.py:80 with top_k off and top_p 1, no min-p):
+// dist needs only the maximum of z, and the verify round's statistics pass forms the exact kept mass itself, so its
+// parts list nothing and sum nothing.
+__device__ __forceinline__ bool keeps_all_mss(const ScanArgs &a, const gse_row &P) {
+  return a.tree && (P.flags & GSE_ROW_MSS) && (P.top_k <= 0 || P.top_k >= a.V) && P.top_p >= 1.0 && !(P.min_p > 0.0);
+}
+
 __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gse_row &P, Shared &sh) {
   const int tid = threadIdx.x;
   const SliceRec *rb = a.rec + (size_t)row * a.nparts;
@@ -425,11 +432,13 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   // Gather the listed elements: masses for S, the certified head, the packed maximum.
   const bool finite_max = mk < KEY_POSINF;
   const double M = finite_max ? (double)fkey_inv(mk) : 0.0;
-  if (a.tree && (P.flags & GSE_ROW_MSS) && finite_max && !(flags & F_HOVER) &&
-      (P.top_k <= 0 || P.top_k >= a.V) && P.top_p >= 1.0 && !(P.min_p > 0.0)) {
-    // a verify node that takes dist + mss and keeps every token (sampling.py:80 with top_k off, top_p 1): dist needs
-    // only the maximum of z; the verify round's stats pass forms the exact kept mass itself
-    if (tid == 0) set_info(ri, pack(mk, 0u), 0ull, 0.0, 0.0, R_DONE, -1);
+  if (keeps_all_mss(a, P) && nlp == 0) {
+    // its parts listed nothing: done with the maximum, or (more distinct history ids than a part can count, or a
+    // maximum that is not finite) the exact path redoes the row
+    if (tid == 0) {
+      if (finite_max && !(flags & F_HOVER)) set_info(ri, pack(mk, 0u), 0ull, 0.0, 0.0, R_DONE, -1);
+      else set_info(ri, gtop, 0, 0.0, 0.0, R_HARD | R_FULL, -1);
+    }
     return;
   }
   const uint32_t kappa = max(sh.rkappa, KEY_NEGINF + 1u);
@@ -856,7 +865,9 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   const int p0 = a.pstart[part], p1 = a.pstart[part + 1];
   const int pv = AL ? max(p0, p1 & ~(L::VEC - 1)) : p1;  // the stream's end; [pv, p1) go to the side pass
   const int nck = (pv - p0 + CHK - 1) / CHK;
-  const bool listing = !GREEDY || nlp_of(a, P) > 0;  // candidates and the softmax sum are needed
+  // candidates and the softmax sum are needed (not for greedy rows without logprobs, nor for verify nodes that keep
+  // every token)
+  const bool listing = (!GREEDY || nlp_of(a, P) > 0) && !(keeps_all_mss(a, P) && nlp_of(a, P) == 0);
   const int wl = part * PWAVES + w;                  // this wave's list
   float *proc = a.processed ? a.processed + (int64_t)row * a.processed_ld : nullptr;
 
