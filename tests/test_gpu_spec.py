@@ -266,3 +266,31 @@ def test_verify_rounds_back_to_back_on_a_stream(ge, gpu):
     torch.cuda.synchronize()
     for k, sn in enumerate(snaps):
         assert torch.equal(sn, refs[k % 2]), k
+
+
+def test_verify_keep_all_node_with_history_overflow(ge, gpu):
+    """Strict nodes that keep every token list nothing in the selection pass (the round needs only their maximum); one
+    whose part holds more distinct penalty-history ids than a part can count (3000 of 8192 tokens) cannot finish on its
+    maximum and takes the exact path. Every request's walk still equals the oracle's."""
+    rng = np.random.default_rng(41)
+    v = 8192
+    P = ge.sampling.SamplingParams
+    parents = [0, 1, 0]
+    reqs = []
+    for a in range(6):
+        target = rng.normal(0, 1.5, size=(4, v)).astype(np.float32)
+        draft = (target + rng.normal(0, 0.6, size=target.shape)).astype(np.float32)
+        q = _q_of_draft(draft, parents)
+        toks = [int(rng.choice(v, p=q[par])) for par in parents]
+        big = a % 2 == 0  # (the overflowing history on every other request)
+        hist = [rng.permutation(v)[:3000] if big else rng.integers(0, v, size=40) for _ in range(4)]
+        p = P(temperature=1.0, frequency_penalty=0.2, presence_penalty=0.1, accept="rejection")
+        reqs.append(dict(target=target, tokens=toks, parents=parents, params=p, seed=500 + a, q=q, history=hist))
+    print(f"[verify] keep-all strict nodes, V={v}, histories of 3000 distinct ids", flush=True)
+    got = ge.spec.verify_tree(reqs)
+    paths = ge._lib.handle(gpu.index, 4 * len(reqs), v).row_paths(4 * len(reqs))
+    assert (paths == ge._lib.PATH_EXACT).sum() >= 3, paths  # (the strict nodes of the overflowing requests)
+    for a, r in enumerate(reqs):
+        want = spo.verify_tree(r["target"], r["q"], r["tokens"], r["parents"], r["params"], r["seed"],
+                               history=r["history"])
+        assert got[a] == want, (a, got[a], want)
