@@ -294,3 +294,54 @@ def test_verify_keep_all_node_with_history_overflow(ge, gpu):
         want = spo.verify_tree(r["target"], r["q"], r["tokens"], r["parents"], r["params"], r["seed"],
                                history=r["history"])
         assert got[a] == want, (a, got[a], want)
+
+
+def _bf16(x, gpu):
+    """A bf16 device copy of x and the fp32 values it holds (bf16 widens to fp32 exactly)."""
+    d = torch.from_numpy(x).to(gpu).to(torch.bfloat16)
+    return d, d.float().cpu().numpy()
+
+
+def test_verify_bf16_target_and_drafter_logits(ge, gpu):
+    """A verify round over bf16 target rows with bf16 drafter logits (the bf16 instances of the statistics and residual
+    passes, and q = softmax(float64(x) / t) from bf16 x): strict, exact-acceptance and greedy requests, a ragged
+    vocabulary (40000 tokens). The oracle walks the same values widened to fp32."""
+    rng = np.random.default_rng(77)
+    v = 40000
+    P = ge.sampling.SamplingParams
+    calls, want = [], []
+    for a in range(12):
+        parents = [0, 1, 2, 0, 4][:int(rng.integers(2, 6))]
+        n = len(parents)
+        tgt, tgt32 = _bf16(rng.normal(0, 1.5, size=(n + 1, v)).astype(np.float32), gpu)
+        drf, drf32 = _bf16((tgt32 + rng.normal(0, 0.6, size=tgt32.shape)).astype(np.float32), gpu)
+        t = float(rng.choice([0.8, 1.0, 1.3]))
+        q = _q_of_draft(drf32, parents, t)
+        toks = [int(rng.choice(v, p=q[par])) for par in parents]
+        kind = a % 3
+        p = (P(temperature=1.0, top_p=float(rng.choice([1.0, 0.9])), accept="rejection") if kind == 0 else
+             P(temperature=0.9, top_k=40) if kind == 1 else P())
+        seed = int(rng.integers(0, 1 << 62))
+        calls.append(dict(target=tgt, tokens=toks, parents=parents, params=p, seed=seed, draft=drf, draft_t=t))
+        want.append(spo.verify_tree(tgt32, q, toks, parents, p, seed))
+    print(f"[verify] 12 requests, bf16 target and drafter logits, V={v}", flush=True)
+    got = ge.spec.verify_tree(calls)
+    for a in range(len(calls)):
+        assert got[a] == want[a], (a, got[a], want[a])
+
+
+@pytest.mark.parametrize("t", [0.0, 1.0])
+def test_draft_pick_bf16_matches_oracle(ge, gpu, t):
+    """The drafter's selection over bf16 logits (the bf16 pick instances) against the oracle on the widened values."""
+    rng = np.random.default_rng(int(t * 10) + 9)
+    rows, v = 12, 50000
+    x, x32 = _bf16(rng.normal(0, 2, size=(rows, v)).astype(np.float32), gpu)
+    n = [int(k) for k in rng.integers(1, 9, size=rows)]
+    seeds = [int(s) for s in rng.integers(0, 1 << 62, size=rows)]
+    ats = [int(s) for s in rng.integers(0, 4000, size=rows)]
+    toks, vals = ge.spec.pick_batch(x, n, t, seeds, ats)
+    toks, vals = toks.cpu().numpy(), vals.cpu().numpy()
+    for r in range(rows):
+        w = spo.pick(x32[r].astype(np.float64), n[r], t, seeds[r], ats[r])
+        assert list(toks[r, :n[r]]) == [e[0] for e in w], r
+        np.testing.assert_allclose(vals[r, :n[r]], [e[2] for e in w], rtol=1e-12, atol=1e-12)
