@@ -210,6 +210,26 @@ def test_deep_rows_sample_and_dist(ge, gpu):
         np.testing.assert_allclose(d[r], ora.dist(x[r], params[r]), rtol=DIST_RTOL, atol=1e-300)
 
 
+def test_deep_rows_odd_vocab_masks_history(ge, gpu):
+    """The split-row finish over an odd vocabulary (rows unaligned for 16-byte loads: the finish's scalar-load
+    instance) with grammar masks and penalty histories in its count and pick streams: tokens against the oracle."""
+    n, v = 16, 100003
+    x, params = _flat_rows(ge, n, v, 13)
+    rng = np.random.default_rng(13)
+    P = ge.sampling.SamplingParams
+    params = [P(temperature=p.temperature, top_p=p.top_p, top_k=p.top_k, min_p=p.min_p, repetition_penalty=1.1,
+                frequency_penalty=0.2, presence_penalty=0.1) for p in params]
+    masks = [rng.random(v) < 0.7 for _ in range(n)]
+    hist = [rng.integers(0, v, size=300) for _ in range(n)]
+    u = np.array([ora.uniform(3000 + r, 7) for r in range(n)], np.float64)
+    xt = torch.from_numpy(x).to(gpu)
+    got = ge.sampling.sample_ex(xt, params, None, None, [torch.from_numpy(m) for m in masks], history=hist,
+                                uniforms=u).tolist()
+    paths = ge._lib.handle(gpu.index, n, v).row_paths(n)
+    assert got == ora.sample(x, params, None, None, masks, history=hist, uniforms=u)
+    assert (paths == ge._lib.PATH_DEEP).sum() >= n // 2, paths
+
+
 @pytest.mark.gpu
 def test_deep_rows_plan_wait_off(ge, gpu):
     """The split-row finish's bounded wait: with GSE_BATCH_NO_PLAN_WAIT a pick slice that finds its row's plan not yet
