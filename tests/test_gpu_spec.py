@@ -345,3 +345,34 @@ def test_draft_pick_bf16_matches_oracle(ge, gpu, t):
         w = spo.pick(x32[r].astype(np.float64), n[r], t, seeds[r], ats[r])
         assert list(toks[r, :n[r]]) == [e[0] for e in w], r
         np.testing.assert_allclose(vals[r, :n[r]], [e[2] for e in w], rtol=1e-12, atol=1e-12)
+
+
+def test_verify_round_in_a_captured_graph(ge, gpu):
+    """A verify round with drafter logits (its fork to the handle's side stream and the join back) captured in a graph
+    on the stream it ran on before (so its handle exists: opening one allocates), replayed three times with eager work
+    between the replays; every replay's walks equal the eager round's, which equal the oracle's."""
+    reqs = ge.workloads.c4()[:8]
+    call = ge.spec.VerifyCall([dict(target=torch.from_numpy(r["target"]).to(gpu), tokens=r["tokens"],
+                                    parents=r["parents"], params=r["params"], seed=r["seed"],
+                                    draft=torch.from_numpy(r["draft"]).to(gpu), draft_t=1.0) for r in reqs])
+    st = torch.cuda.Stream(gpu)  # (default priority)
+    with torch.cuda.stream(st):
+        call.launch()
+    torch.cuda.synchronize()
+    ref = call.result()
+    for a, r in enumerate(reqs):
+        want = spo.verify_tree(r["target"], _q_of_draft(r["draft"], r["parents"]), r["tokens"], r["parents"],
+                               r["params"], r["seed"])
+        assert ref[a] == want, (a, ref[a], want)
+    print("[verify] capturing one round in a graph", flush=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        call.launch()
+    torch.cuda.synchronize()
+    for k in range(3):
+        for t in (call.e_len, call.e_st, call.e_tok, call.e_node):
+            t.fill_(-7)  # (eager work between the replays: the outputs cleared)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert call.result() == ref, k
