@@ -314,3 +314,43 @@ def test_logits_borrowed_not_copied(ge, gpu, monkeypatch):
     params = [_P(ge, temperature=1.0, top_p=0.95) for _ in range(4)]
     toks = ge.sampling.sample(x, params, [1, 2, 3, 4], [0, 0, 0, 0], None)
     assert toks == ora.sample(x.cpu().numpy(), params, [1, 2, 3, 4], [0, 0, 0, 0], None)
+
+
+def test_sample_in_a_captured_graph(ge, gpu):
+    """One gse_sample call over the whole full-stack batch (256 rows, 23 of them settled by the split-row finish, the
+    exact pass launched too) captured in a graph on the stream whose handle it used before, replayed three times with
+    an eager call of the same handle and cleared outputs between the replays: every replay's tokens equal the eager
+    call's, which equal the Python path's."""
+    import ctypes as C
+    lib = ge._lib
+    b = ge.workloads.c3()
+    x0 = torch.from_numpy(b.logits).to(gpu)
+    masks = [torch.from_numpy(m) for m in b.masks]
+    st = torch.cuda.Stream(gpu)  # (default priority)
+    with torch.cuda.stream(st):
+        h, x, code, _, b0, keep = ge.sampling._prepare(x0, b.params, None, None, masks, b.history, b.uniforms)
+        bb = ge.sampling._batch(x, code, keep[1], keep[2], b0.mask_ld, keep[3], keep[4], gpu)
+        toks = torch.empty(b.rows, dtype=torch.int32, device=gpu)
+        o = lib.Out()
+        o.size = C.sizeof(lib.Out)
+        o.tokens = toks.data_ptr()
+        h.ck(h.L.gse_sample(h.h, C.byref(bb), C.byref(o)), "gse_sample")
+    torch.cuda.synchronize()
+    ref = toks.cpu().tolist()
+    want = ge.sampling.sample_ex(x0.clone(), b.params, None, None, masks, history=b.history,
+                                 uniforms=b.uniforms).tolist()
+    assert ref == want
+    print("[sample] capturing one full-stack call in a graph", flush=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        h.ck(h.L.gse_sample(h.h, C.byref(bb), C.byref(o)), "gse_sample")
+    torch.cuda.synchronize()
+    for k in range(3):
+        with torch.cuda.stream(st):
+            h.ck(h.L.gse_sample(h.h, C.byref(bb), C.byref(o)), "gse_sample")  # (eager, the same workspace)
+        torch.cuda.synchronize()
+        toks.fill_(-5)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert toks.cpu().tolist() == ref, k
