@@ -302,9 +302,11 @@ def run_sample(args, ge, torch, batch):
     torch.cuda.synchronize()
     log(f"[bench] {copies} input copies resident ({copies * batch.logits.nbytes / 2**20:.0f} MiB of logits)")
 
+    base_flags = ge.sampling._sample_flags(batch.params)  # (what the drop-in adds: sample_ex)
+
     def step(k, profile=False):
         s = sets[k % copies]
-        s["b"].flags = lib.BATCH_PROFILE if profile else 0
+        s["b"].flags = base_flags | (lib.BATCH_PROFILE if profile else 0)
         rc = h.L.gse_sample(h.h, C.byref(s["b"]), C.byref(s["o"]))
         if rc:
             h.ck(rc, "gse_sample")

@@ -11,7 +11,7 @@ import threading
 import numpy as np
 import torch
 
-ABI_MAJOR, ABI_MINOR = 1, 2
+ABI_MAJOR, ABI_MINOR = 1, 3
 PATH_MAIN, PATH_DEEP, PATH_EXACT = 0, 1, 2  # gse_row_paths codes
 OK, E_ARG, E_DEVICE, E_UNSUPPORTED, E_CAPACITY = 0, -1, -4, -5, -7
 F32, BF16 = 0, 1
@@ -24,6 +24,7 @@ NOALLOC_ROWS, NOALLOC_VOCAB = 32, 163840
 BATCH_EXACT = 1
 BATCH_PROFILE = 2
 BATCH_NO_PLAN_WAIT = 4
+BATCH_NO_SPLIT = 8  # (ABI 1.3)
 MAX_LOGPROBS = 64
 P_ = C.POINTER
 

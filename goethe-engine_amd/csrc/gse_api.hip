@@ -210,6 +210,10 @@ gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   a.dlist = h->dlist;
   a.dslots = (int)h->dslots;
   deep_grid(h, b.rows, &a.dslices, &a.dgrid);
+  if (b.flags & GSE_BATCH_NO_SPLIT) {  // (no slots: the resolve sends such rows to the exact path)
+    a.dslices = 0;
+    a.dgrid = 0;
+  }
   part_layout(h, a);
   return a;
 }

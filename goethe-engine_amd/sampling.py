@@ -255,6 +255,12 @@ def _prepare(logits, params, seeds, idxs, masks, history, uniforms):
     return h, x, code, dev, _batch(x, code, rows_dev, mask_dev, mask_ld, hist_dev, uni_dev, dev), keep
 
 
+def _sample_flags(params):
+    """GSE_BATCH_* bits the drop-in adds to a gse_sample call: NO_SPLIT when every row is greedy (temperature 0 as
+    float32, as the device decides), since greedy rows never take the split-row finish and its launch is saved."""
+    return _lib.BATCH_NO_SPLIT if params and all(float(p.temperature) == 0.0 for p in params) else 0
+
+
 def sample_ex(logits, params, seeds, idxs, masks, history=None, uniforms=None, exact=False, processed=False,
               flags=0):
     """gse_sample on the current stream, asynchronously: a Selection of device tensors. flags adds GSE_BATCH_* bits
@@ -267,7 +273,7 @@ def sample_ex(logits, params, seeds, idxs, masks, history=None, uniforms=None, e
     h, x, code, dev, b, keep = _prepare(x, params, seeds, idxs, masks, history, uniforms)
     if exact:
         b.flags |= _lib.BATCH_EXACT
-    b.flags |= int(flags)
+    b.flags |= int(flags) | _sample_flags(params)
     nlp = max([int(_get(p, "logprobs", 0)) for p in params] + [0])
     toks = torch.empty(n, dtype=torch.int32, device=dev)
     o = _lib.Out()

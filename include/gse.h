@@ -24,7 +24,7 @@ extern "C" {
 #endif
 
 #define GSE_ABI_MAJOR 1
-#define GSE_ABI_MINOR 2
+#define GSE_ABI_MINOR 3
 #define GSE_ABI_VERSION ((GSE_ABI_MAJOR << 16) | GSE_ABI_MINOR)
 
 #if defined(__GNUC__)
@@ -103,8 +103,11 @@ typedef struct gse_batch {
 enum {
   GSE_BATCH_EXACT = 1u,   /* finish every sampled row on the exact radix-select path (same results, slower) */
   GSE_BATCH_PROFILE = 2u, /* record HIP events around each kernel of this call on its stream (read with gse_profile) */
-  GSE_BATCH_NO_PLAN_WAIT = 4u /* testing: a split-row finish slice whose row's plan is not out when it first looks
-                               * does not wait; the row takes the exact path (same results, slower) */
+  GSE_BATCH_NO_PLAN_WAIT = 4u, /* testing: a split-row finish slice whose row's plan is not out when it first looks
+                                * does not wait; the row takes the exact path (same results, slower) */
+  GSE_BATCH_NO_SPLIT = 8u /* the split-row finish is not launched: a row that would take it takes the exact path
+                           * (same results). For batches that cannot use it, to save its launch: greedy rows of
+                           * gse_sample never do (the Python layer sets it when every row is greedy). Since ABI 1.3. */
 };
 
 typedef struct gse_out {

@@ -91,3 +91,26 @@ def test_row_record_round_trip(ge):
     assert raw.shape == (2 * 72,)
     assert np.frombuffer(raw[:4].tobytes(), np.float32)[0] == np.float32(0.5)
     assert np.frombuffer(raw[40:48].tobytes(), np.uint64)[0] == 2 ** 64 - 1
+
+
+ENUMS = r"""
+#include <stdio.h>
+#include "gse.h"
+int main(void) {
+  printf("%u %u %u %u\n", (unsigned)GSE_BATCH_EXACT, (unsigned)GSE_BATCH_PROFILE, (unsigned)GSE_BATCH_NO_PLAN_WAIT,
+         (unsigned)GSE_BATCH_NO_SPLIT);
+  return 0;
+}
+"""
+
+
+def test_batch_flags_match_the_header(ge, tmp_path):
+    """The GSE_BATCH_* bits the binding uses are the header's."""
+    src = tmp_path / "enums.c"
+    src.write_text(ENUMS)
+    exe = tmp_path / "enums"
+    inc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+    subprocess.run(["gcc", "-I", inc, str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    lib = ge._lib
+    assert got == [lib.BATCH_EXACT, lib.BATCH_PROFILE, lib.BATCH_NO_PLAN_WAIT, lib.BATCH_NO_SPLIT]

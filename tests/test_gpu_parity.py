@@ -230,6 +230,21 @@ def test_deep_rows_odd_vocab_masks_history(ge, gpu):
     assert (paths == ge._lib.PATH_DEEP).sum() >= n // 2, paths
 
 
+def test_no_split_flag_sends_deep_rows_to_exact(ge, gpu):
+    """GSE_BATCH_NO_SPLIT on rows that need the split-row finish: it is not launched, those rows take the exact path,
+    and every token still equals the oracle's. (The drop-in sets the flag only when every row is greedy.)"""
+    n, v = 8, 151936
+    x, params = _flat_rows(ge, n, v, 7)
+    u = np.array([ora.uniform(1000 + r, 3) for r in range(n)], np.float64)
+    xt = torch.from_numpy(x).to(gpu)
+    got = ge.sampling.sample_ex(xt, params, None, None, None, uniforms=u, flags=ge._lib.BATCH_NO_SPLIT).tolist()
+    paths = ge._lib.handle(gpu.index, n, v).row_paths(n)
+    assert got == ora.sample(x, params, None, None, None, uniforms=u)
+    assert (paths == ge._lib.PATH_DEEP).sum() == 0 and (paths == ge._lib.PATH_EXACT).sum() >= 1, paths
+    assert ge.sampling._sample_flags(params) == 0
+    assert ge.sampling._sample_flags([ge.sampling.SamplingParams()] * 3) == ge._lib.BATCH_NO_SPLIT
+
+
 @pytest.mark.gpu
 def test_deep_rows_plan_wait_off(ge, gpu):
     """The split-row finish's bounded wait: with GSE_BATCH_NO_PLAN_WAIT a pick slice that finds its row's plan not yet
