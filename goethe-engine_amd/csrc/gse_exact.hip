@@ -50,28 +50,116 @@ struct XCtx {
   double M, S;
 };
 
+// The logits of tokens t0 .. t0+PER-1 (a thread's run inside a chunk), loaded together so that the PER loads are in
+// flight at once; indexes past the row end read its last element (the callers skip those tokens). The mask word of
+// the run (its PER tokens share one: PER divides 32), all ones without a mask.
+__device__ __forceinline__ uint32_t load_run(const RowCtx &c, int t0, float (&v)[PER]) {
+  static_assert(32 % PER == 0, "a run shares one mask word");
+  if (c.dtype == GSE_BF16) {
+    const uint16_t *p = (const uint16_t *)c.base;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) v[i] = bf16_to_f32(p[min(t0 + i, c.V - 1)]);
+  } else {
+    const float *p = (const float *)c.base;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) v[i] = p[min(t0 + i, c.V - 1)];
+  }
+  return c.mw ? (t0 < c.V ? c.mw[t0 >> 5] : 0u) : 0xFFFFFFFFu;
+}
+
 // Calls f(t, key) for every token of the row, thread-contiguous inside each chunk (ids increase with (tid, i)).
 template <typename F>
-__device__ __forceinline__ void for_each_key(const XCtx &x, ExactShared &sh, F f) {
+__device__ __forceinline__ void for_each_key(const RowCtx &c, const int32_t *hist, int nch, ExactShared &sh, F f) {
   const int tid = threadIdx.x;
-  for (int ch = 0; ch < x.nch; ++ch) {
+  for (int ch = 0; ch < nch; ++ch) {
     const int c0 = ch * CH;
-    if (x.c.pen) build_counts(x.c, x.hist, c0, sh.cnt);
+    if (c.pen) build_counts(c, hist, c0, sh.cnt);
     const int t0 = c0 + tid * PER;
-    const uint32_t mword = x.c.mw ? (t0 < x.c.V ? x.c.mw[t0 >> 5] : 0u) : 0xFFFFFFFFu;
+    float v[PER];
+    const uint32_t mword = load_run(c, t0, v);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int t = t0 + i;
-      if (t < x.c.V) {
-        const uint32_t ct = x.c.pen ? sh.cnt[t - c0] : 0u;
+      if (t < c.V) {
+        const uint32_t ct = c.pen ? sh.cnt[t - c0] : 0u;
         bool fn = false, ff = false;
         float xm;
-        const uint32_t k = elem_key(x.c, load_one(x.c, t), ct, (mword >> (t & 31)) & 1u, fn, ff, xm);
+        const uint32_t k = elem_key(c, v[i], ct, (mword >> (t & 31)) & 1u, fn, ff, xm);
         f(t, k);
       }
     }
-    if (x.c.pen) __syncthreads();
+    if (c.pen) __syncthreads();
   }
+}
+
+// The workgroup's LDS, at file scope so that the pass functions below address it as LDS without taking it as an
+// argument (a pointer argument would be a generic one).
+__shared__ ExactShared xsh;
+
+// ---- whole-row passes -----------------------------------------------------------------------------------------------
+// Each pass over the row is a function of its own, not inlined, taking the row context by value: its element loop is
+// then register-allocated apart from the finishing code around it. Inlined, the loop reloaded values of that code
+// from private memory (spill slots) inside every element, each reload waited for, at 150-700 us per pass over a
+// 128k-token row.
+
+enum { P_MAX = 0, P_SUM, P_COUNT, P_HIST, P_COLLECT, P_TOP };
+
+struct PassIn {
+  double M;         // row maximum of z (P_SUM, P_HIST)
+  uint32_t lo, hi;  // key window (P_HIST, P_COLLECT); lo alone: the smallest key counted (P_COUNT)
+  int shift;        // bin width 2^shift keys (P_HIST)
+  uint64_t pk;      // smallest packed key collected (P_TOP)
+};
+
+struct PassOut {
+  uint64_t u;  // P_MAX: the thread's largest packed key; P_COUNT: its count
+  double d;    // P_SUM: the thread's sum of exp(z - M), in token order
+};
+
+// Every thread of the workgroup calls it. P_HIST adds counts and fixed-point masses to the histogram bins, P_COLLECT
+// and P_TOP append packed keys at xsh.n (the callers clear the bins and the count first and synchronise afterwards).
+template <int OP>
+__device__ __noinline__ PassOut row_pass(const RowCtx c, const int32_t *hist, int nch, const PassIn in) {
+  ExactShared &sh = xsh;
+  uint64_t u = 0;
+  double d = 0.0;
+  for_each_key(c, hist, nch, sh, [&](int t, uint32_t k) {
+    if constexpr (OP == P_MAX) {
+      const uint64_t p = pack(k, (uint32_t)t);
+      u = p > u ? p : u;
+    } else if constexpr (OP == P_SUM) {
+      d += k > KEY_NEGINF ? exp((double)fkey_inv(k) - in.M) : 0.0;
+    } else if constexpr (OP == P_COUNT) {
+      u += k >= in.lo ? 1u : 0u;
+    } else if constexpr (OP == P_HIST) {
+      if (k >= in.lo && k <= in.hi) {
+        const int b = (int)((k - in.lo) >> in.shift);
+        atomicAdd(&sh.u.h.c[b], 1u);
+        if (k > KEY_NEGINF) {
+          const Fx f = fx_of(exp((double)fkey_inv(k) - in.M));
+          if (f.hi) atomicAdd((unsigned long long *)&sh.u.h.hi[b], (unsigned long long)f.hi);
+          if (f.lo) atomicAdd((unsigned long long *)&sh.u.h.lo[b], (unsigned long long)f.lo);
+        }
+      }
+    } else if constexpr (OP == P_COLLECT) {
+      if (k >= in.lo && k <= in.hi) {
+        const uint32_t pos = atomicAdd(&sh.n, 1u);
+        if (pos < (uint32_t)CAPS) sh.u.col.k[pos] = pack(k, (uint32_t)t);
+      }
+    } else {
+      const uint64_t p = pack(k, (uint32_t)t);
+      if (p >= in.pk) {
+        const uint32_t pos = atomicAdd(&sh.n, 1u);
+        if (pos < (uint32_t)CAPS) sh.u.col.k[pos] = p;
+      }
+    }
+  });
+  return PassOut{u, d};
+}
+
+template <int OP>
+__device__ __forceinline__ PassOut pass(const XCtx &x, const PassIn &in) {
+  return row_pass<OP>(x.c, x.hist, x.nch, in);
 }
 
 // ---- block reductions / scans (1024 threads) ------------------------------------------------------------------------
@@ -149,18 +237,7 @@ __device__ void build_hist(const XCtx &x, ExactShared &sh, const Win &w) {
     sh.u.h.lo[b] = 0;
   }
   __syncthreads();
-  const double M = x.M;
-  for_each_key(x, sh, [&](int, uint32_t k) {
-    if (k >= w.lo && k <= w.hi) {
-      const int b = (int)((k - w.lo) >> w.shift);
-      atomicAdd(&sh.u.h.c[b], 1u);
-      if (k > KEY_NEGINF) {
-        const Fx f = fx_of(exp((double)fkey_inv(k) - M));
-        if (f.hi) atomicAdd((unsigned long long *)&sh.u.h.hi[b], (unsigned long long)f.hi);
-        if (f.lo) atomicAdd((unsigned long long *)&sh.u.h.lo[b], (unsigned long long)f.lo);
-      }
-    }
-  });
+  pass<P_HIST>(x, PassIn{x.M, w.lo, w.hi, w.shift, 0});
   __syncthreads();
 }
 
@@ -247,12 +324,7 @@ __device__ int find_bin(ExactShared &sh, const Win &w, int kind, uint64_t r, dou
 __device__ uint32_t collect(const XCtx &x, ExactShared &sh, uint32_t klo, uint32_t khi) {
   if (threadIdx.x == 0) sh.n = 0;
   __syncthreads();
-  for_each_key(x, sh, [&](int t, uint32_t k) {
-    if (k >= klo && k <= khi) {
-      const uint32_t pos = atomicAdd(&sh.n, 1u);
-      if (pos < (uint32_t)CAPS) sh.u.col.k[pos] = pack(k, (uint32_t)t);
-    }
-  });
+  pass<P_COLLECT>(x, PassIn{0.0, klo, khi, 0, 0});
   __syncthreads();
   const uint32_t n = sh.n;
   if (n <= (uint32_t)CAPS) {
@@ -271,13 +343,14 @@ __device__ int walk_list(const XCtx &x, ExactShared &sh, int n, int kind, uint64
   const int tid = threadIdx.x;
   constexpr int PT = CAPS / XT;  // 8 elements per thread, consecutive
   Fx ef[PT];
+  const double M = x.M;
   uint64_t sh_hi = 0, sh_lo = 0;
   for (int i = 0; i < PT; ++i) {
     const int idx = tid * PT + i;
     ef[i] = Fx{0, 0};
     if (idx < n) {
       const uint32_t k = pk_key(sh.u.col.k[idx]);
-      if (k > KEY_NEGINF) ef[i] = fx_of(exp((double)fkey_inv(k) - x.M));
+      if (k > KEY_NEGINF) ef[i] = fx_of(exp((double)fkey_inv(k) - M));
     }
     sh_hi += ef[i].hi;
     sh_lo += ef[i].lo;
@@ -321,20 +394,24 @@ __device__ uint32_t nth_with_key(const XCtx &x, ExactShared &sh, uint32_t key, u
   uint64_t base = 0;
   if (tid == 0) sh.found = 0xFFFFFFFFu;
   __syncthreads();
-  for (int ch = 0; ch < x.nch; ++ch) {
+  const RowCtx c = x.c;
+  const int32_t *hist = x.hist;
+  const int nch = x.nch;
+  for (int ch = 0; ch < nch; ++ch) {
     const int c0 = ch * CH;
-    if (x.c.pen) build_counts(x.c, x.hist, c0, sh.cnt);
+    if (c.pen) build_counts(c, hist, c0, sh.cnt);
     const int t0 = c0 + tid * PER;
-    const uint32_t mword = x.c.mw ? (t0 < x.c.V ? x.c.mw[t0 >> 5] : 0u) : 0xFFFFFFFFu;
+    float v[PER];
+    const uint32_t mword = load_run(c, t0, v);
     uint32_t match = 0;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int t = t0 + i;
-      if (t < x.c.V) {
-        const uint32_t ct = x.c.pen ? sh.cnt[t - c0] : 0u;
+      if (t < c.V) {
+        const uint32_t ct = c.pen ? sh.cnt[t - c0] : 0u;
         bool fn = false, ff = false;
         float xm;
-        if (elem_key(x.c, load_one(x.c, t), ct, (mword >> (t & 31)) & 1u, fn, ff, xm) == key) match |= 1u << i;
+        if (elem_key(c, v[i], ct, (mword >> (t & 31)) & 1u, fn, ff, xm) == key) match |= 1u << i;
       }
     }
     uint64_t cntm = (uint64_t)__popc(match), d = 0;
@@ -429,22 +506,14 @@ __device__ Hit query(const XCtx &x, ExactShared &sh, int kind, uint64_t r, doubl
 }
 
 __device__ uint64_t count_ge(const XCtx &x, ExactShared &sh, uint32_t kmin) {
-  uint64_t n = 0;
-  for_each_key(x, sh, [&](int, uint32_t k) { n += (k >= kmin) ? 1u : 0u; });
-  return block_sum_u64(n, sh);
+  return block_sum_u64(pass<P_COUNT>(x, PassIn{0.0, kmin, 0, 0, 0}).u, sh);
 }
 
 // Collects the elements with packed key >= pk (the top ranks) and sorts them.
 __device__ uint32_t collect_top(const XCtx &x, ExactShared &sh, uint64_t pk) {
   if (threadIdx.x == 0) sh.n = 0;
   __syncthreads();
-  for_each_key(x, sh, [&](int t, uint32_t k) {
-    const uint64_t p = pack(k, (uint32_t)t);
-    if (p >= pk) {
-      const uint32_t pos = atomicAdd(&sh.n, 1u);
-      if (pos < (uint32_t)CAPS) sh.u.col.k[pos] = p;
-    }
-  });
+  pass<P_TOP>(x, PassIn{0.0, 0, 0, 0, pk});
   __syncthreads();
   const uint32_t n = min(sh.n, (uint32_t)CAPS);
   const int np2 = pow2_ceil(max((int)n, 2));
@@ -476,18 +545,19 @@ __device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShare
     RowCtx gc = make_ctx(a, row, P);
     bool fnan = false, ffin = false;
     uint64_t gb = 0;
-    for (int ch = 0; ch < x.nch; ++ch) {
+    const int nch = a.nch;
+    for (int ch = 0; ch < nch; ++ch) {
       const int c0 = ch * CH;
-      if (gc.pen) build_counts(gc, x.hist, c0, sh.cnt);
+      if (gc.pen) build_counts(gc, a.hist, c0, sh.cnt);
       const int t0 = c0 + tid * PER;
-      const uint32_t mword = gc.mw ? (t0 < gc.V ? gc.mw[t0 >> 5] : 0u) : 0xFFFFFFFFu;
+      float v[PER];
+      const uint32_t mword = load_run(gc, t0, v);
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int t = t0 + i;
         if (t < gc.V) {
           float xm;
-          const uint32_t k = elem_key(gc, load_one(gc, t), gc.pen ? sh.cnt[t - c0] : 0u, (mword >> (t & 31)) & 1u, fnan,
-                                      ffin, xm);
+          const uint32_t k = elem_key(gc, v[i], gc.pen ? sh.cnt[t - c0] : 0u, (mword >> (t & 31)) & 1u, fnan, ffin, xm);
           const uint64_t p = pack(k, (uint32_t)t);
           gb = p > gb ? p : gb;
         }
@@ -515,12 +585,7 @@ __device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShare
     }
   }
   // pass 0: the row maximum of z
-  uint64_t best = 0;
-  for_each_key(x, sh, [&](int t, uint32_t k) {
-    const uint64_t p = pack(k, (uint32_t)t);
-    best = p > best ? p : best;
-  });
-  best = block_max_u64(best, sh);
+  uint64_t best = block_max_u64(pass<P_MAX>(x, PassIn{}).u, sh);
   const uint32_t mk = pk_key(best);
   if (mk >= KEY_POSINF || mk <= KEY_NEGINF) {
     for (int i = tid; i < nlp; i += XT) {
@@ -537,9 +602,7 @@ __device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShare
   }
   x.M = (double)fkey_inv(mk);
   // pass A: S (fixed thread order, deterministic)
-  double s = 0.0;
-  for_each_key(x, sh, [&](int, uint32_t k) { s += k > KEY_NEGINF ? exp((double)fkey_inv(k) - x.M) : 0.0; });
-  x.S = block_sum_f64(s, sh);
+  x.S = block_sum_f64(pass<P_SUM>(x, PassIn{x.M, 0, 0, 0, 0}).d, sh);
   const double S = x.S;
   const int64_t V = a.V;
 
@@ -614,7 +677,7 @@ constexpr int XGRID = 256;  // workgroups of the exact pass, at most (one per CU
 // r = g (mod grid): it finds its hard ones (those the main pass and the split-row finish left: one scan of their flags,
 // compacted in row order) and finishes them, so that a call with no hard row costs a launch and one round of loads.
 __global__ __launch_bounds__(XT) void exact_kernel(ScanArgs a) {
-  __shared__ ExactShared sh;
+  ExactShared &sh = xsh;
   __shared__ uint32_t wn[XT / WAVE];
   __shared__ int hrow[XT];
   if (blockIdx.x == 0 && threadIdx.x == 0) a.dctl[0] = 0u;  // the deep rows of this call are finished
