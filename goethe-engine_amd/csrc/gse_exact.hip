@@ -50,33 +50,46 @@ struct XCtx {
   double M, S;
 };
 
-// The logits of tokens t0 .. t0+PER-1 (a thread's run inside a chunk), loaded together so that the PER loads are in
-// flight at once; indexes past the row end read its last element (the callers skip those tokens). The mask word of
-// the run (its PER tokens share one: PER divides 32), all ones without a mask.
-__device__ __forceinline__ uint32_t load_run(const RowCtx &c, int t0, float (&v)[PER]) {
+// The logits of tokens t0 .. t0+PER-1 (a thread's run inside a chunk) as raw bits (bf16 zero-extended), loaded
+// together so that the PER loads are in flight at once, and converted only where used (raw_logit), so that a
+// prefetched run is not waited for early; indexes past the row end read its last element (the callers skip those
+// tokens). Returns the mask word of the run (its PER tokens share one: PER divides 32), all ones without a mask.
+// The pointers are global ones: loads through generic pointers would be flat loads, whose completion the compiler
+// cannot count, so that every later use waited for all loads in flight, the next run's included.
+__device__ __forceinline__ uint32_t load_run(const RowCtx &c, int t0, uint32_t (&v)[PER]) {
   static_assert(32 % PER == 0, "a run shares one mask word");
+  typedef const __attribute__((address_space(1))) uint16_t g16;
+  typedef const __attribute__((address_space(1))) uint32_t g32;
   if (c.dtype == GSE_BF16) {
-    const uint16_t *p = (const uint16_t *)c.base;
+    g16 *p = (g16 *)c.base;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) v[i] = bf16_to_f32(p[min(t0 + i, c.V - 1)]);
+    for (int i = 0; i < PER; ++i) v[i] = p[min(t0 + i, c.V - 1)];
   } else {
-    const float *p = (const float *)c.base;
+    g32 *p = (g32 *)c.base;
 #pragma unroll
     for (int i = 0; i < PER; ++i) v[i] = p[min(t0 + i, c.V - 1)];
   }
-  return c.mw ? (t0 < c.V ? c.mw[t0 >> 5] : 0u) : 0xFFFFFFFFu;
+  return c.mw ? (t0 < c.V ? ((g32 *)c.mw)[t0 >> 5] : 0u) : 0xFFFFFFFFu;
+}
+
+__device__ __forceinline__ float raw_logit(const RowCtx &c, uint32_t r) {
+  return __uint_as_float(c.dtype == GSE_BF16 ? r << 16 : r);
 }
 
 // Calls f(t, key) for every token of the row, thread-contiguous inside each chunk (ids increase with (tid, i)).
+// The next chunk's run is loaded while the current one is processed (issued after the history counts, whose loads
+// are waited for).
 template <typename F>
 __device__ __forceinline__ void for_each_key(const RowCtx &c, const int32_t *hist, int nch, ExactShared &sh, F f) {
   const int tid = threadIdx.x;
+  uint32_t v[PER];
+  uint32_t mword = load_run(c, tid * PER, v);
   for (int ch = 0; ch < nch; ++ch) {
     const int c0 = ch * CH;
-    if (c.pen) build_counts(c, hist, c0, sh.cnt);
     const int t0 = c0 + tid * PER;
-    float v[PER];
-    const uint32_t mword = load_run(c, t0, v);
+    if (c.pen) build_counts(c, hist, c0, sh.cnt);
+    uint32_t vn[PER];
+    const uint32_t mn = load_run(c, ch + 1 < nch ? t0 + CH : t0, vn);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int t = t0 + i;
@@ -84,11 +97,14 @@ __device__ __forceinline__ void for_each_key(const RowCtx &c, const int32_t *his
         const uint32_t ct = c.pen ? sh.cnt[t - c0] : 0u;
         bool fn = false, ff = false;
         float xm;
-        const uint32_t k = elem_key(c, v[i], ct, (mword >> (t & 31)) & 1u, fn, ff, xm);
+        const uint32_t k = elem_key(c, raw_logit(c, v[i]), ct, (mword >> (t & 31)) & 1u, fn, ff, xm);
         f(t, k);
       }
     }
     if (c.pen) __syncthreads();
+#pragma unroll
+    for (int i = 0; i < PER; ++i) v[i] = vn[i];
+    mword = mn;
   }
 }
 
@@ -401,7 +417,7 @@ __device__ uint32_t nth_with_key(const XCtx &x, ExactShared &sh, uint32_t key, u
     const int c0 = ch * CH;
     if (c.pen) build_counts(c, hist, c0, sh.cnt);
     const int t0 = c0 + tid * PER;
-    float v[PER];
+    uint32_t v[PER];
     const uint32_t mword = load_run(c, t0, v);
     uint32_t match = 0;
 #pragma unroll
@@ -411,7 +427,7 @@ __device__ uint32_t nth_with_key(const XCtx &x, ExactShared &sh, uint32_t key, u
         const uint32_t ct = c.pen ? sh.cnt[t - c0] : 0u;
         bool fn = false, ff = false;
         float xm;
-        if (elem_key(c, v[i], ct, (mword >> (t & 31)) & 1u, fn, ff, xm) == key) match |= 1u << i;
+        if (elem_key(c, raw_logit(c, v[i]), ct, (mword >> (t & 31)) & 1u, fn, ff, xm) == key) match |= 1u << i;
       }
     }
     uint64_t cntm = (uint64_t)__popc(match), d = 0;
@@ -550,14 +566,15 @@ __device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShare
       const int c0 = ch * CH;
       if (gc.pen) build_counts(gc, a.hist, c0, sh.cnt);
       const int t0 = c0 + tid * PER;
-      float v[PER];
+      uint32_t v[PER];
       const uint32_t mword = load_run(gc, t0, v);
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int t = t0 + i;
         if (t < gc.V) {
           float xm;
-          const uint32_t k = elem_key(gc, v[i], gc.pen ? sh.cnt[t - c0] : 0u, (mword >> (t & 31)) & 1u, fnan, ffin, xm);
+          const uint32_t k =
+              elem_key(gc, raw_logit(gc, v[i]), gc.pen ? sh.cnt[t - c0] : 0u, (mword >> (t & 31)) & 1u, fnan, ffin, xm);
           const uint64_t p = pack(k, (uint32_t)t);
           gb = p > gb ? p : gb;
         }
