@@ -521,6 +521,37 @@ __device__ Hit query(const XCtx &x, ExactShared &sh, int kind, uint64_t r, doubl
   return out;
 }
 
+// The head of the row: every element above the level-0 histogram bin that holds rank CAPS (every element when the row
+// has at most CAPS), collected and sorted descending in the list area; kcut receives the smallest key it covers
+// completely (every element with a key >= kcut is in the head). Returns its length, 0 when the top bin alone holds
+// more than CAPS elements. A query answered inside the head is a walk of the list; query() reuses the LDS, after
+// which the head is gone.
+__device__ uint32_t collect_head(const XCtx &x, ExactShared &sh, uint32_t &kcut) {
+  const Win w{0u, 0xFFFFFFFFu, 20, 0, Fx{0, 0}};
+  build_hist(x, sh, w);
+  uint64_t nb = 0;
+  Fx mb{0, 0};
+  const int b = find_bin(sh, w, Q_RANK, (uint64_t)CAPS, x.S, 0.0, nb, mb);
+  if (b == NB - 1) return 0;
+  kcut = b < 0 ? 0u : (uint32_t)(b + 1) << w.shift;
+  __syncthreads();
+  return collect(x, sh, kcut, 0xFFFFFFFFu);
+}
+
+// A query answered from the head of n elements: false when no element of the head satisfies it (the answer, if any,
+// ranks at n or below).
+__device__ bool head_query(const XCtx &x, ExactShared &sh, uint32_t n, int kind, uint64_t r, double tgt, Hit &h) {
+  Fx above, self;
+  const int i = walk_list(x, sh, (int)n, kind, r, 0, Fx{0, 0}, tgt, above, self);
+  if (i >= (int)n) return false;
+  h.rank = i;
+  h.pk = sh.u.col.k[i];
+  h.above = above;
+  h.self = self;
+  __syncthreads();
+  return true;
+}
+
 __device__ uint64_t count_ge(const XCtx &x, ExactShared &sh, uint32_t kmin) {
   return block_sum_u64(pass<P_COUNT>(x, PassIn{0.0, kmin, 0, 0, 0}).u, sh);
 }
@@ -623,6 +654,9 @@ __device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShare
   const double S = x.S;
   const int64_t V = a.V;
 
+  // The head serves the queries below whose answers rank inside it; nh = 0 once a query has run its own levels.
+  uint32_t kcut = 0, nh = 0;
+  if (!greedy || nlp > 0) nh = collect_head(x, sh, kcut);
   if (!greedy) {
     const double q0 = 1.0 / S;
     int64_t m = V;
@@ -636,21 +670,43 @@ __device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShare
         if (exp((double)fkey_inv(mid) - x.M) / S >= thr) hi = mid;
         else lo = mid + 1;
       }
-      const int64_t mm = (int64_t)count_ge(x, sh, lo);
+      int64_t mm;
+      if (nh > 0 && lo >= kcut) {  // every key >= lo is in the head
+        uint64_t c = 0;
+        for (int i = tid; i < (int)nh; i += XT) c += pk_key(sh.u.col.k[i]) >= lo ? 1u : 0u;
+        mm = (int64_t)block_sum_u64(c, sh);
+      } else {
+        mm = (int64_t)count_ge(x, sh, lo);
+      }
       if (mm < m) m = mm;
     }
     {
-      const Hit hp = query(x, sh, Q_EXCL, 0, P.top_p);
-      if (hp.rank >= 0 && hp.rank < m) m = hp.rank;
+      // An answer at rank m or below leaves m as it is: with m <= nh, one not in the head needs no search.
+      Hit hp;
+      if (nh > 0 && head_query(x, sh, nh, Q_EXCL, 0, P.top_p, hp)) {
+        if (hp.rank < m) m = hp.rank;
+      } else if (!(nh > 0 && m <= (int64_t)nh)) {
+        nh = 0;
+        hp = query(x, sh, Q_EXCL, 0, P.top_p);
+        if (hp.rank >= 0 && hp.rank < m) m = hp.rank;
+      }
     }
     if (m < 1) m = 1;
-    const Hit hl = query(x, sh, Q_RANK, (uint64_t)(m - 1), 0.0);
+    Hit hl;
+    if (!(m <= (int64_t)nh && head_query(x, sh, nh, Q_RANK, (uint64_t)(m - 1), 0.0, hl))) {
+      nh = 0;
+      hl = query(x, sh, Q_RANK, (uint64_t)(m - 1), 0.0);
+    }
     const double clast = fx_val(fx_add(hl.above, hl.self)) / S;
     int32_t tok = -1;
     if (a.mode == MODE_SAMPLE) {
       const double u = a.uni ? a.uni[row] : uniform64(P.seed, P.idx);
       const double thr = u * clast;
-      Hit hj = query(x, sh, Q_INCL, 0, thr);
+      Hit hj;
+      if (!(nh > 0 && head_query(x, sh, nh, Q_INCL, 0, thr, hj))) {
+        nh = 0;
+        hj = query(x, sh, Q_INCL, 0, thr);
+      }
       if (hj.rank < 0 || hj.rank > m - 1) hj = hl;  // j = min(count, keep.sum() - 1)
       tok = (int32_t)pk_id(hj.pk);
     }
@@ -670,8 +726,11 @@ __device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShare
   }
   if (nlp > 0) {
     const int n_top = (int)min((int64_t)nlp, V);
-    const Hit hn = query(x, sh, Q_RANK, (uint64_t)(n_top - 1), 0.0);
-    const uint32_t n = collect_top(x, sh, hn.pk);
+    uint32_t n = (uint32_t)n_top;  // the first n_top elements of the head, when it holds them
+    if (n_top > (int)nh) {
+      const Hit hn = query(x, sh, Q_RANK, (uint64_t)(n_top - 1), 0.0);
+      n = collect_top(x, sh, hn.pk);
+    }
     const double lS = log(S);
     for (int i = tid; i < nlp; i += XT) {
       int32_t id = -1;
