@@ -118,12 +118,12 @@ __shared__ ExactShared xsh;
 // from private memory (spill slots) inside every element, each reload waited for, at 150-700 us per pass over a
 // 128k-token row.
 
-enum { P_MAX = 0, P_SUM, P_COUNT, P_HIST, P_COLLECT, P_TOP };
+enum { P_MAX = 0, P_SUM, P_COUNT, P_HIST, P_COLLECT, P_TOP, P_MAXH };
 
 struct PassIn {
   double M;         // row maximum of z (P_SUM, P_HIST)
   uint32_t lo, hi;  // key window (P_HIST, P_COLLECT); lo alone: the smallest key counted (P_COUNT)
-  int shift;        // bin width 2^shift keys (P_HIST)
+  int shift;        // bin width 2^shift keys (P_HIST, P_MAXH)
   uint64_t pk;      // smallest packed key collected (P_TOP)
 };
 
@@ -132,7 +132,8 @@ struct PassOut {
   double d;    // P_SUM: the thread's sum of exp(z - M), in token order
 };
 
-// Every thread of the workgroup calls it. P_HIST adds counts and fixed-point masses to the histogram bins, P_COLLECT
+// Every thread of the workgroup calls it. P_HIST adds counts and fixed-point masses to the histogram bins (P_MAXH:
+// P_MAX that also counts every key into the bins, masses left alone), P_COLLECT
 // and P_TOP append packed keys at xsh.n (the callers clear the bins and the count first and synchronise afterwards).
 template <int OP>
 __device__ __noinline__ PassOut row_pass(const RowCtx c, const int32_t *hist, int nch, const PassIn in) {
@@ -140,9 +141,10 @@ __device__ __noinline__ PassOut row_pass(const RowCtx c, const int32_t *hist, in
   uint64_t u = 0;
   double d = 0.0;
   for_each_key(c, hist, nch, sh, [&](int t, uint32_t k) {
-    if constexpr (OP == P_MAX) {
+    if constexpr (OP == P_MAX || OP == P_MAXH) {
       const uint64_t p = pack(k, (uint32_t)t);
       u = p > u ? p : u;
+      if constexpr (OP == P_MAXH) atomicAdd(&sh.u.h.c[k >> in.shift], 1u);
     } else if constexpr (OP == P_SUM) {
       d += k > KEY_NEGINF ? exp((double)fkey_inv(k) - in.M) : 0.0;
     } else if constexpr (OP == P_COUNT) {
@@ -521,14 +523,18 @@ __device__ Hit query(const XCtx &x, ExactShared &sh, int kind, uint64_t r, doubl
   return out;
 }
 
+// Level-0 bins (2^HS keys each) of the head's histogram, which the max pass counts.
+constexpr int HS = 20;
+static_assert((0xFFFFFFFFu >> HS) < (uint32_t)NB, "the level-0 bins cover every key");
+
 // The head of the row: every element above the level-0 histogram bin that holds rank CAPS (every element when the row
 // has at most CAPS), collected and sorted descending in the list area; kcut receives the smallest key it covers
 // completely (every element with a key >= kcut is in the head). Returns its length, 0 when the top bin alone holds
-// more than CAPS elements. A query answered inside the head is a walk of the list; query() reuses the LDS, after
+// more than CAPS elements. Expects the level-0 counts of every key in the histogram (the max pass, P_MAXH), masses
+// zero: the cut is a rank. A query answered inside the head is a walk of the list; query() reuses the LDS, after
 // which the head is gone.
 __device__ uint32_t collect_head(const XCtx &x, ExactShared &sh, uint32_t &kcut) {
-  const Win w{0u, 0xFFFFFFFFu, 20, 0, Fx{0, 0}};
-  build_hist(x, sh, w);
+  const Win w{0u, 0xFFFFFFFFu, HS, 0, Fx{0, 0}};
   uint64_t nb = 0;
   Fx mb{0, 0};
   const int b = find_bin(sh, w, Q_RANK, (uint64_t)CAPS, x.S, 0.0, nb, mb);
@@ -633,7 +639,18 @@ __device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShare
     }
   }
   // pass 0: the row maximum of z
-  uint64_t best = block_max_u64(pass<P_MAX>(x, PassIn{}).u, sh);
+  // (with the level-0 counts of the head when a query will need it)
+  const bool want_head = !greedy || nlp > 0;
+  if (want_head) {
+    for (int b = tid; b < NB; b += XT) {
+      sh.u.h.c[b] = 0;
+      sh.u.h.hi[b] = 0;
+      sh.u.h.lo[b] = 0;
+    }
+    __syncthreads();
+  }
+  const PassIn pin{0.0, 0u, 0xFFFFFFFFu, HS, 0};
+  uint64_t best = block_max_u64((want_head ? pass<P_MAXH>(x, pin) : pass<P_MAX>(x, pin)).u, sh);
   const uint32_t mk = pk_key(best);
   if (mk >= KEY_POSINF || mk <= KEY_NEGINF) {
     for (int i = tid; i < nlp; i += XT) {
@@ -656,7 +673,7 @@ __device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShare
 
   // The head serves the queries below whose answers rank inside it; nh = 0 once a query has run its own levels.
   uint32_t kcut = 0, nh = 0;
-  if (!greedy || nlp > 0) nh = collect_head(x, sh, kcut);
+  if (want_head) nh = collect_head(x, sh, kcut);
   if (!greedy) {
     const double q0 = 1.0 / S;
     int64_t m = V;
