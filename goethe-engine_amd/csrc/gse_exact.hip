@@ -4,9 +4,11 @@
 //   m   = min(top_k, #{q_i >= min_p * q_0}, first rank with cumsum(q)_i - q_i >= top_p)    (sampling.py:80)
 //   j   = first rank with cumsum(q)_i >= u * c_last, c_last = cumsum(q)_{m-1}             (sampling.py:81-83)
 //
-// Every rank / mass query walks a 4096-bin histogram of the 32-bit key (count and mass per bin), then collects the one
-// bin that holds the answer into LDS and sorts it; a bin too large to collect is refined with a histogram of its own
-// key range (12 bits per level), and a single key with more elements than fit is ordered by token id (the stable order).
+// The head of the row (at most HEADN top elements, cut at a bin of the key histogram that the max pass counts) is
+// collected into LDS and sorted once; a rank / mass query whose answer lies in it is a walk of that list. Any other
+// query walks a 4096-bin histogram of the 32-bit key (count and mass per bin), then collects the one bin that holds
+// the answer into LDS and sorts it; a bin too large to collect is refined with a histogram of its own key range
+// (12 bits per level), and a single key with more elements than fit is ordered by token id (the stable order).
 // Masses are exact sums of per-element fixed-point values (2^-64 resolution), so every prefix is deterministic and
 // the same whichever order the atomics land in.
 #include "gse_rowctx.h"
