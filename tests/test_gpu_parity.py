@@ -121,6 +121,39 @@ def test_c5_bf16_nucleus_logprobs(ge, gpu):
     _check(ge, ge.workloads.c5(rows=list(range(8))), gpu, check_processed=False)
 
 
+def test_exact_head_branches(ge, gpu):
+    """Rows chosen for each branch of the exact path's sorted head: keep sets that run below the head (top-p near 1,
+    top-k 3000), a min-p threshold below the head's cut, a row whose one key fills every bin the head could cut at (no
+    head: every query runs its own histogram levels, logprobs included), logprobs served from the head, a greedy row
+    with logprobs. Fast and exact paths against the oracle, tokens and logprobs."""
+    v = 151936
+    rng = np.random.default_rng(11)
+    x = rng.normal(0.0, 1.0, size=(8, v)).astype(np.float32)
+    x[2] = 0.5
+    x[3, :40] += 6.0
+    P = ge.sampling.SamplingParams
+    params = [P(temperature=1.0, top_p=0.999),
+              P(temperature=1.2, top_k=3000, top_p=1.0),
+              P(temperature=1.0, top_p=0.9, logprobs=5),
+              P(temperature=0.8, top_p=0.95, min_p=0.05, logprobs=8),
+              P(temperature=1.0, top_p=1.0, min_p=1e-6),
+              P(temperature=0.0, logprobs=6),
+              P(temperature=0.7, top_k=50, top_p=0.9),
+              P(temperature=1.5, top_p=0.5, min_p=0.2)]
+    u = np.array([ora.uniform(2000 + r, 1) for r in range(8)], np.float64)
+    batch = ge.workloads.Batch("head", x, params, u)
+    want = _oracle(batch)
+    for exact in (False, True):
+        sel = _run(ge, batch, gpu, exact=exact)
+        assert sel.tolist() == [w["token"] for w in want], exact
+        ids, lps = sel.logprob_ids.cpu().numpy(), sel.logprobs.cpu().numpy()
+        for r, w in enumerate(want):
+            if "logprob_ids" in w:
+                n = len(w["logprob_ids"])
+                assert list(ids[r, :n]) == list(w["logprob_ids"]), (exact, r)
+                np.testing.assert_allclose(lps[r, :n], w["logprobs"], rtol=LOGPROB_RTOL)
+
+
 def test_c4_tree_verify(ge, gpu):
     reqs = ge.workloads.c4(requests=range(4), v=128256)
     qrows = []
