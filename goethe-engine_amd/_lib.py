@@ -7,18 +7,19 @@ carry the soname libamdhip64.so.7): one runtime, so torch's streams and device p
 import ctypes as C
 import os
 import threading
+from collections import OrderedDict
 
 import numpy as np
 import torch
 
-ABI_MAJOR, ABI_MINOR = 1, 3
+ABI_MAJOR, ABI_MINOR = 1, 4
 PATH_MAIN, PATH_DEEP, PATH_EXACT = 0, 1, 2  # gse_row_paths codes
 OK, E_ARG, E_DEVICE, E_UNSUPPORTED, E_CAPACITY = 0, -1, -4, -5, -7
 F32, BF16 = 0, 1
 ROW_TEMP_UNDERFLOW = 1
 ROW_MSS = 2
 Q_PROB, Q_LOGITS_F32, Q_LOGITS_BF16 = 0, 1, 2
-WALK_OK, WALK_ERROR, WALK_TRUNCATED = 0, 1, 2
+WALK_OK, WALK_ERROR, WALK_TRUNCATED, WALK_KIDS = 0, 1, 2, 3
 MAX_KIDS = 16
 NOALLOC_ROWS, NOALLOC_VOCAB = 32, 163840
 BATCH_EXACT = 1
@@ -95,6 +96,7 @@ SIGNATURES = dict(
     gse_dist=(C.c_int, [C.c_void_p, P_(Batch), C.c_void_p, C.c_int64]),
     gse_draw=(C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p,
                         C.c_void_p]),
+    gse_qprob=(C.c_int, [C.c_void_p, P_(QRows), C.c_uint32, C.c_void_p, C.c_int64, C.c_void_p]),
     gse_mss=(C.c_int, [C.c_void_p, P_(MssBatch)]),
     gse_sample_noalloc=(C.c_int, [P_(Batch), P_(Out)]),
     gse_verify_tree=(C.c_int, [C.c_void_p, P_(Batch), P_(Tree), P_(TreeOut)]),
@@ -124,7 +126,11 @@ def bind(path=PATH):
 
 _lock = threading.Lock()
 _L = None
-_handles = {}
+# Open handles, least recently used first, keyed by (device, stream). Each holds a device workspace (plan_layout in
+# gse_int.h: about 47 MB for 256 rows x 151936 tokens, 278 MB for 1024 x 262144), so the cache is bounded: past
+# MAX_HANDLES the least recently used one leaves it and is closed once nothing references it any more.
+MAX_HANDLES = 8
+_handles = OrderedDict()
 
 
 def lib():
@@ -135,11 +141,15 @@ def lib():
 
 
 class Handle:
-    """One gse handle on one device, reopened larger when a call needs more rows or a larger vocabulary."""
+    """One gse handle on one device, for the calls of one stream. A handle is not thread safe (abi/gc.h:16-19): every
+    library call goes through call(), which holds the handle's lock while the call is enqueued; the calls of two threads
+    on one stream then run one after the other on the device, so they may share the workspace."""
 
     def __init__(self, device, rows, vocab):
         self.L = lib()
         self.device, self.rows, self.vocab = device, rows, vocab
+        self.lock = threading.Lock()
+        self.h = None
         h = C.c_void_p()
         p = OpenParams(C.sizeof(OpenParams), device, rows, vocab)
         rc = self.L.gse_open(C.byref(p), C.byref(h))
@@ -151,12 +161,21 @@ class Handle:
         if rc < 0:
             why = (self.L.gse_last_error(self.h) or b"").decode()
             raise RuntimeError(f"{what} failed ({rc}): {why}")
+        return rc
+
+    def call(self, name, *args):
+        """gse_<name>(handle, *args) under the handle's lock; a negative code raises RuntimeError with the library's
+        last error (gc_c.py:222-227)."""
+        with self.lock:
+            if not self.h:
+                raise RuntimeError(f"{name}: the handle is closed")
+            return self.ck(getattr(self.L, name)(self.h, *args), name)
 
     def row_paths(self, rows):
         """uint8 [rows]: which path finished each row of the last sample / dist call (PATH_MAIN, PATH_DEEP,
         PATH_EXACT). Waits for the device."""
         out = np.zeros(rows, np.uint8)
-        self.ck(self.L.gse_row_paths(self.h, rows, out.ctypes.data), "gse_row_paths")
+        self.call("gse_row_paths", rows, out.ctypes.data)
         return out
 
     def profile(self):
@@ -164,31 +183,38 @@ class Handle:
         since the last read; clears the record."""
         ms = (C.c_float * 4)()
         calls = C.c_uint32()
-        n = self.L.gse_profile(self.h, ms, 4, C.byref(calls))
-        self.ck(n, "gse_profile")
+        n = self.call("gse_profile", ms, 4, C.byref(calls))
         return calls.value, [float(ms[i]) for i in range(n)]
 
     def close(self):
-        if self.h:
-            self.L.gse_close(self.h)
-            self.h = None
+        """Waits for the device (gse_close synchronizes) and frees the workspace."""
+        with self.lock:
+            if self.h:
+                self.L.gse_close(self.h)
+                self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # (interpreter shutdown)
+            pass
 
 
 def handle(device, rows, vocab):
-    """A handle on device that fits rows x vocab, grown on demand. There is one per (device, current stream, thread):
-    a handle's workspace must not serve two calls that can overlap, on the device (two streams) or on the host (two
-    threads: a handle is not thread safe), so each stream a thread launches on gets its own."""
+    """The handle of (device, current stream) that fits rows x vocab, reopened larger on demand. Calls on two streams
+    may overlap on the device, so each stream gets its own workspace; at most MAX_HANDLES stay cached."""
     if not torch.cuda.is_available():
         raise RuntimeError("goethe-engine_amd needs a HIP device (torch.cuda.is_available() is False)")
-    key = (device, torch.cuda.current_stream(device).cuda_stream, threading.get_ident())
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
     with _lock:
         h = _handles.get(key)
         if h is None or h.rows < rows or h.vocab < vocab:
-            if h is not None:
-                torch.cuda.synchronize(device)
-                h.close()
+            # (a handle that is replaced or evicted is closed when its last user lets it go)
             h = Handle(device, max(rows, h.rows if h else 0, 64), max(vocab, h.vocab if h else 0))
             _handles[key] = h
+            while len(_handles) > MAX_HANDLES:
+                _handles.popitem(last=False)
+        _handles.move_to_end(key)
         return h
 
 

@@ -49,6 +49,8 @@ struct gse_handle {
   hipEvent_t (*ring)[5] = nullptr;  // kernel boundaries of up to GSE_PROFILE_CALLS profiled calls
   int nring = 0;                    // calls recorded
   int nprof = 0;                    // kernels per recorded call
+  bool is_static = false;           // gse_sample_noalloc's per-device handle: its errors go to the thread's fixed
+                                    // buffer (no host allocation on that path)
   std::string err;
 };
 
@@ -63,7 +65,7 @@ int fail(gse_handle *h, int rc, const char *fmt, ...) {
   va_start(ap, fmt);
   vsnprintf(buf, sizeof buf, fmt, ap);
   va_end(ap);
-  if (h) h->err = buf;
+  if (h && !h->is_static) h->err = buf;
   else memcpy(g_open_err, buf, sizeof buf);
   return rc;
 }
@@ -288,6 +290,7 @@ int static_handle(gse_handle **out, hipStream_t s) {
     if ((e = gse::launch_zero(ptr, NOALLOC_LAYOUT.total, s)) != hipSuccess)
       return fail(nullptr, GSE_E_DEVICE, "static workspace clear: %s", hipGetErrorString(e));
     h->device = dev;
+    h->is_static = true;
     h->max_rows = gse::NOALLOC_ROWS;
     h->max_vocab = gse::NOALLOC_VOCAB;
     h->nchmax = (gse::NOALLOC_VOCAB + gse::CH - 1) / gse::CH;
@@ -398,6 +401,8 @@ GSE_API int gse_sample_noalloc(const gse_batch *in, const gse_out *out) {
   gse_batch b;
   gse_out o;
   if (!take(in, b) || !take(out, o)) return fail(nullptr, GSE_E_ARG, "null or short gse_batch / gse_out");
+  if (b.flags & GSE_BATCH_PROFILE)
+    return fail(nullptr, GSE_E_UNSUPPORTED, "gse_sample_noalloc: GSE_BATCH_PROFILE allocates events; use gse_sample");
   if (b.rows > gse::NOALLOC_ROWS || b.vocab > gse::NOALLOC_VOCAB)
     return fail(nullptr, GSE_E_CAPACITY,
                 "gse_sample_noalloc: %u rows of %u tokens; its static workspace holds at most %u rows of at most %u "
@@ -405,9 +410,7 @@ GSE_API int gse_sample_noalloc(const gse_batch *in, const gse_out *out) {
   gse_handle *h = nullptr;
   int rc = static_handle(&h, (hipStream_t)b.stream);
   if (rc) return rc;
-  rc = sample_impl(h, b, o);
-  if (rc) fail(nullptr, rc, "%s", h->err.c_str());
-  return rc;
+  return sample_impl(h, b, o);  // (its errors land in the thread's fixed buffer: gse_last_error(NULL))
 }
 
 GSE_API int gse_dist(gse_handle *h, const gse_batch *in, double *probs, int64_t probs_ld) {
@@ -532,6 +535,22 @@ GSE_API int gse_draft_pick(gse_handle *h, const gse_pick_batch *in) {
   L.tick = h->ptick;
   hipError_t e = gse::launch_pick(L, (hipStream_t)b.stream);
   return e == hipSuccess ? GSE_OK : hip_fail(h, e, "pick launch");
+}
+
+GSE_API int gse_qprob(gse_handle *h, const gse_qrows *qrows, uint32_t vocab, double *out, int64_t out_ld,
+                      void *stream) {
+  if (!h) return fail(nullptr, GSE_E_ARG, "null handle");
+  gse_qrows q;
+  if (!take(qrows, q)) return fail(h, GSE_E_ARG, "null or short gse_qrows");
+  if (q.kind != GSE_Q_LOGITS_F32 && q.kind != GSE_Q_LOGITS_BF16)
+    return fail(h, GSE_E_ARG, "q kind %u: gse_qprob takes drafter logits (GSE_Q_LOGITS_F32 / _BF16)", q.kind);
+  if (q.rows == 0) return GSE_OK;
+  if (!q.q || !q.temperature || !out) return fail(h, GSE_E_ARG, "q, temperature and out are required");
+  if (vocab == 0 || q.ld < (int64_t)vocab || out_ld < (int64_t)vocab)
+    return fail(h, GSE_E_ARG, "vocab 0, q ld < vocab or out_ld < vocab");
+  DeviceGuard g(h->device);
+  hipError_t e = gse::launch_qprob(q, (int)vocab, out, out_ld, (hipStream_t)stream);
+  return e == hipSuccess ? GSE_OK : hip_fail(h, e, "qprob launch");
 }
 
 GSE_API int gse_draw(gse_handle *h, const double *q, int64_t q_ld, uint32_t rows, uint32_t vocab, const double *u,

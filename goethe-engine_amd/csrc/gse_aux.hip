@@ -164,6 +164,61 @@ __global__ __launch_bounds__(DT) void mss_kernel(gse_mss_batch b) {
   }
 }
 
+// ---- q of a drafter row: spec.py:157 (q = softmax(float64(x) / t)) -------------------------------------------------------
+// One workgroup per row: the maximum of x (z = x / t is monotone in x and rounds once, so max z = (max x) / t), the mass
+// E = sum exp(z - M) in fixed point (the same sum in any order, exp_nonpos within 1.5 ulp), then q = exp(z - M) / E. A
+// row holding NaN, +inf, or no value above -inf gives NaN everywhere, as torch.softmax does.
+__global__ __launch_bounds__(DT) void qprob_kernel(gse_qrows q, int V, double *out, int64_t ld) {
+  __shared__ double etab[64];
+  __shared__ double redd[DT / WAVE];
+  __shared__ uint64_t redh[DT / WAVE], redl[DT / WAVE];
+  const int row = blockIdx.x, tid = threadIdx.x, w = tid >> 6;
+  const bool bf = q.kind == GSE_Q_LOGITS_BF16;
+  const char *base = (const char *)q.q + (size_t)row * (size_t)q.ld * (bf ? 2 : 4);
+  const double t = q.temperature[row];
+  double *o = out + (int64_t)row * ld;
+  auto xat = [&](int i) -> double {
+    return bf ? (double)bf16_to_f32(((const uint16_t *)base)[i]) : (double)((const float *)base)[i];
+  };
+  if (tid < 64) etab[tid] = EXP2_64[tid];
+  double m = -INFINITY;
+  bool nan = false;
+  for (int i = tid; i < V; i += DT) {
+    const double x = xat(i);
+    nan |= x != x;
+    m = fmax(m, x);
+  }
+  m = lane63(wave_scan(m, (double)-INFINITY, [](double a, double b) { return fmax(a, b); }));
+  const bool wnan = ballot64(nan) != 0ull;
+  if (lane_id() == 0) redd[w] = wnan ? __builtin_nan("") : m;
+  __syncthreads();
+  double M = -INFINITY;
+  bool bad = false;
+  for (int k = 0; k < DT / WAVE; ++k) {
+    bad |= redd[k] != redd[k];
+    M = fmax(M, redd[k]);
+  }
+  M = M / t;
+  bad = bad || !(fabs(M) < INFINITY);
+  if (bad) {
+    for (int i = tid; i < V; i += DT) o[i] = __builtin_nan("");
+    return;
+  }
+  Fx f = {0, 0};
+  for (int i = tid; i < V; i += DT) f = fx_add(f, fx_of(exp_nonpos(xat(i) / t - M, etab)));
+  f.hi = wave_sum_u64(f.hi);
+  f.lo = wave_sum_u64(f.lo);
+  if (lane_id() == 0) {
+    redh[w] = f.hi;
+    redl[w] = f.lo;
+  }
+  __syncthreads();
+  Fx tot = {0, 0};
+  for (int k = 0; k < DT / WAVE; ++k) tot = fx_add(tot, Fx{redh[k], redl[k]});
+  const double E = fx_val(tot);
+  for (int i = tid; i < V; i += DT) o[i] = exp_nonpos(xat(i) / t - M, etab) / E;
+}
+
 // ---- bool rows -> packed words (grammar.py:44-45 inverted) ---------------------------------------------------------------
 __global__ __launch_bounds__(AT) void pack_kernel(const uint8_t *bools, int64_t bld, int V, int32_t *words, int64_t wld) {
   const int row = blockIdx.y;
@@ -205,6 +260,11 @@ hipError_t launch_draw(const double *q, int64_t ld, int rows, int V, const doubl
 
 hipError_t launch_mss(const gse_mss_batch &b, hipStream_t s) {
   hipLaunchKernelGGL(mss_kernel, dim3(b.nodes), dim3(DT), 0, s, b);
+  return hipGetLastError();
+}
+
+hipError_t launch_qprob(const gse_qrows &q, int V, double *out, int64_t ld, hipStream_t s) {
+  hipLaunchKernelGGL(qprob_kernel, dim3(q.rows), dim3(DT), 0, s, q, V, out, ld);
   return hipGetLastError();
 }
 

@@ -254,6 +254,7 @@ hipError_t launch_qstats(const TreeLaunch &L, hipStream_t s);
 hipError_t launch_tree(const TreeLaunch &L, hipStream_t s, hipEvent_t qdone);
 hipError_t launch_pick(const PickLaunch &L, hipStream_t s);
 hipError_t launch_zero(void *p, size_t bytes, hipStream_t s);
+hipError_t launch_qprob(const gse_qrows &q, int V, double *out, int64_t ld, hipStream_t s);
 hipError_t launch_pack(const uint8_t *bools, int64_t bld, int rows, int V, int32_t *words, int64_t wld, hipStream_t s);
 
 }  // namespace gse

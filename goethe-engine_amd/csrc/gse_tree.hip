@@ -1126,6 +1126,14 @@ __global__ __launch_bounds__(TT) __attribute__((amdgpu_waves_per_eu(DTK == GSE_F
 
 // ---- verify: the walk ------------------------------------------------------------------------------------------------
 
+// More kids than the round was given room for (max_kids, GSE_MAX_KIDS): find_kids dropped the later ones, so a strict
+// node's decision would not be the reference's (spec.py:91 walks every kid). rows (u, end) hold the node's request.
+__device__ __forceinline__ bool kids_over(const TreeArgs &a, int u, int end) {
+  int n = 0;
+  for (int j = u + 1; j < end && a.parent[j] >= 0; ++j) n += a.parent[j] == u ? 1 : 0;
+  return n > a.max_kids || n > GSE_MAX_KIDS;
+}
+
 __global__ __launch_bounds__(64) void walk_kernel(TreeArgs a) {
   const int q = blockIdx.x * 64 + threadIdx.x;
   // node_token / node_kid of every node
@@ -1133,7 +1141,7 @@ __global__ __launch_bounds__(64) void walk_kernel(TreeArgs a) {
     const gse_row &P = a.s.params[u];
     int tok, kid;
     if (P.flags & GSE_ROW_MSS) {
-      const bool live = node_live(a, u, P);
+      const bool live = node_live(a, u, P) && !kids_over(a, u, a.nodes);
       tok = live ? a.st[u].token : -1;
       kid = live ? a.st[u].kid : -1;
     } else {
@@ -1158,6 +1166,11 @@ __global__ __launch_bounds__(64) void walk_kernel(TreeArgs a) {
     const gse_row &P = a.s.params[u];
     int tok, kid = -1;
     if (P.flags & GSE_ROW_MSS) {
+      if (kids_over(a, u, end)) {  // (the node's decision is not the reference's: the walk stops before it)
+        status = GSE_WALK_KIDS;
+        if (n < a.out.emit_ld) a.out.emit_nodes[(int64_t)q * a.out.emit_ld + n] = u;
+        break;
+      }
       const bool live = node_live(a, u, P);
       tok = live ? a.st[u].token : -1;
       kid = live ? a.st[u].kid : -1;

@@ -24,7 +24,7 @@ extern "C" {
 #endif
 
 #define GSE_ABI_MAJOR 1
-#define GSE_ABI_MINOR 3
+#define GSE_ABI_MINOR 4
 #define GSE_ABI_VERSION ((GSE_ABI_MAJOR << 16) | GSE_ABI_MINOR)
 
 #if defined(__GNUC__)
@@ -177,7 +177,10 @@ typedef struct gse_tree {
   uint32_t reserved;
 } gse_tree;
 
-enum { GSE_WALK_OK = 0, GSE_WALK_ERROR = 1, GSE_WALK_TRUNCATED = 2 };
+/* GSE_WALK_KIDS (since ABI 1.4): the walk reached a GSE_ROW_MSS node with more kids than gse_tree.max_kids (or
+ * GSE_MAX_KIDS); its decision would have ignored the later kids, so the walk stops before it (emit_nodes[emit_len]
+ * holds the node) instead of emitting a token the reference would not. */
+enum { GSE_WALK_OK = 0, GSE_WALK_ERROR = 1, GSE_WALK_TRUNCATED = 2, GSE_WALK_KIDS = 3 };
 
 typedef struct gse_tree_out {
   uint32_t size;
@@ -231,7 +234,8 @@ GSE_API int gse_sample(gse_handle *h, const gse_batch *in, const gse_out *out);
  * the process ends, for batches of at most GSE_NOALLOC_ROWS rows of at most GSE_NOALLOC_VOCAB tokens (more:
  * GSE_E_CAPACITY). It runs on the current HIP device; the first call on a device sets that device's workspace up and
  * should not be captured. Every call on one GPU shares its workspace: calls that overlap on one GPU (two streams, two
- * threads) race. Errors: gse_last_error(NULL). Results are gse_sample's. */
+ * threads) race. Errors: gse_last_error(NULL). Results are gse_sample's. GSE_BATCH_PROFILE is refused
+ * (GSE_E_UNSUPPORTED): its events are host allocations, and without a handle nobody could read them. */
 #define GSE_NOALLOC_ROWS 32
 #define GSE_NOALLOC_VOCAB 163840
 GSE_API int gse_sample_noalloc(const gse_batch *in, const gse_out *out);
@@ -251,6 +255,12 @@ GSE_API int gse_verify_tree(gse_handle *h, const gse_batch *in, const gse_tree *
 /* Replaces: goethe_engine/spec.py:151-159 TreeDrafter._pick (torch.sort / softmax / draw on the host) for a batch of
  * nodes. */
 GSE_API int gse_draft_pick(gse_handle *h, const gse_pick_batch *in);
+
+/* Replaces: the q of goethe_engine/spec.py:157 (TreeDrafter._pick: torch.softmax(lp.double() / t, 0), the distribution
+ * a sampled child carries in Tree.q and that engine.py:282 hands to mss): fp64 rows q = softmax(float64(x) / t) of
+ * drafter logits or log-probabilities (kind GSE_Q_LOGITS_F32 / _BF16, qrows->temperature[r] > 0), written to
+ * out[r][0, vocab) (out_ld >= vocab). Since ABI 1.4. */
+GSE_API int gse_qprob(gse_handle *h, const gse_qrows *qrows, uint32_t vocab, double *out, int64_t out_ld, void *stream);
 
 /* Replaces: goethe_engine/sampling.py:100-104 draw(): inverse CDF in vocabulary order of each fp64 row q at u[r]:
  * min(count(cumsum(q) < u * sum(q)), last index with q > 0). */

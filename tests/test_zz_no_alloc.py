@@ -67,3 +67,18 @@ def test_noalloc_rejects_batches_past_its_limit(ge):
     assert b"at most 32 rows of at most 163840 tokens" in L.gse_last_error(None)
     b.rows, b.vocab, b.ld = 4, lib.NOALLOC_VOCAB + 1, lib.NOALLOC_VOCAB + 1
     assert L.gse_sample_noalloc(C.byref(b), C.byref(o)) == lib.E_CAPACITY
+
+
+def test_noalloc_refuses_the_profile_flag(ge):
+    """GSE_BATCH_PROFILE records host-allocated events on a handle; the entry point that allocates nothing refuses it
+    (before it touches a device)."""
+    lib = ge._lib
+    L = lib.bind()
+    b = lib.Batch()
+    b.size = C.sizeof(lib.Batch)
+    b.rows, b.vocab, b.ld = 4, 1000, 1000
+    b.flags = lib.BATCH_PROFILE
+    o = lib.Out()
+    o.size = C.sizeof(lib.Out)
+    assert L.gse_sample_noalloc(C.byref(b), C.byref(o)) == lib.E_UNSUPPORTED
+    assert b"GSE_BATCH_PROFILE" in L.gse_last_error(None)
