@@ -8,8 +8,13 @@
   verify_tree(reqs, ...)           one verify round of many requests' draft trees in one call (gse_verify_tree): every
                                    node decided on the device, the walk done there, one copy of the results back
   pick_batch(x, n, t, seeds, ats)  the drafter's children of many nodes in one call (gse_draft_pick)
-  TreeDrafter                      spec.py:125-216 with its selection on the device (chain / static / dynamic shapes)
+  qprob(x, t)                      q = softmax(float64(x) / t) of drafter rows on the device (gse_qprob)
+  Tree / as_tree                   spec.py:22-67: the proposal tree the scheduler fits and the engine walks
+  TreeDrafter                      spec.py:125-216 with its selection on the device (chain / static / dynamic shapes);
+                                   propose() returns Tree objects whose q entries (sampled children) are QRefs, which
+                                   mss(), mss_batch() and numpy read
 """
+from dataclasses import dataclass
 import ctypes as C
 
 import numpy as np
@@ -24,7 +29,10 @@ SALT_ACC, SALT_RES, SALT_DRAFT = 1 << 40, 1 << 41, 1 << 42  # uniform streams: a
 def _f64_rows(rows, dev):
     out = []
     for r in rows:
-        t = r if isinstance(r, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(np.asarray(r, np.float64)))
+        if isinstance(r, QRef):
+            t = r.prob()
+        else:
+            t = r if isinstance(r, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(np.asarray(r, np.float64)))
         out.append(t.to(dev, torch.float64).reshape(-1))
     return torch.stack(out).contiguous() if out else None
 
@@ -68,7 +76,7 @@ def mss_batch(p, kids, seeds, idxs):
     b.seed, b.idx = seed_d.data_ptr(), idx_d.data_ptr()
     b.out_token, b.out_kid = otok.data_ptr(), okid.data_ptr()
     b.stream = torch.cuda.current_stream(dev).cuda_stream
-    h.ck(h.L.gse_mss(h.h, C.byref(b)), "gse_mss")
+    h.call("gse_mss", C.byref(b))
     toks = otok.cpu().tolist()
     kid = [None if k < 0 else int(k) for k in okid.cpu().tolist()]
     return [int(t) for t in toks], kid
@@ -94,14 +102,106 @@ def strict(p):
     return getattr(p, "accept", "exact") == "rejection" and p.temperature > 0
 
 
-class QRef:
-    """A draft distribution held as the drafter's logits row on the device: q = softmax(float64(x) / t) (spec.py:157),
-    never materialised. pick_batch returns these as the q of the children it draws."""
+def qprob(x, t):
+    """q = softmax(float64(x) / t) (spec.py:157) of drafter rows x [rows, V] (device tensor, fp32 or bf16, or anything
+    torch / numpy) at per-row temperatures t > 0 (a list, or one value): an fp64 [rows, V] device tensor (gse_qprob)."""
+    xt, code = _logits(x)
+    rows, v = xt.shape
+    dev = xt.device
+    ts = [float(k) for k in (t if isinstance(t, (list, tuple, np.ndarray)) else [t] * rows)]
+    if len(ts) != rows or not all(k > 0 for k in ts):
+        raise ValueError("qprob needs one temperature > 0 per row")
+    tt = torch.tensor(ts, dtype=torch.float64, device=dev)
+    out = torch.empty((rows, v), dtype=torch.float64, device=dev)
+    q = _lib.QRows()
+    q.size = C.sizeof(_lib.QRows)
+    q.kind = _lib.Q_LOGITS_BF16 if code == _lib.BF16 else _lib.Q_LOGITS_F32
+    q.rows, q.q, q.ld, q.temperature = rows, xt.data_ptr(), xt.stride(0), tt.data_ptr()
+    h = _lib.handle(dev.index, 1, v)
+    h.call("gse_qprob", C.byref(q), v, out.data_ptr(), out.stride(0), _lib.stream_of(dev.index))
+    return out
 
-    __slots__ = ("x", "t")
+
+class QRef:
+    """A draft distribution held as the drafter's logits row on the device: q = softmax(float64(x) / t) (spec.py:157).
+    verify_tree reads it without materialising it; mss / mss_batch, q[i] and numpy (np.asarray(q), so the reference's
+    mss and host() too) read the fp64 row, computed on the device once (gse_qprob). pick_batch's callers make these the
+    q of the children they draw."""
+
+    __slots__ = ("x", "t", "_q")
 
     def __init__(self, x, t):
-        self.x, self.t = x, float(t)
+        self.x, self.t, self._q = x, float(t), None
+
+    def prob(self):
+        """q as an fp64 [V] device tensor."""
+        if self._q is None:
+            self._q = qprob(self.x.reshape(1, -1), [self.t])[0]
+        return self._q
+
+    def __len__(self):
+        return int(self.x.numel())
+
+    def __getitem__(self, i):
+        return float(self.prob()[i])
+
+    def __array__(self, dtype=None, copy=None):
+        a = self.prob().cpu().numpy()
+        return a if dtype is None else a.astype(dtype)
+
+
+@dataclass
+class Tree:
+    """The proposal tree of spec.py:22-67, with the same fields and methods, so that the reference's scheduler
+    (scheduler.py:128-133: as_tree, ok, fit; cut at :152) and engine (engine.py:248-282: kids, tokens, q) take it: node 0
+    is the anchor, tokens[j] is node j + 1 with parent node parents[j] < j + 1; q[j] is the distribution tokens[j] was
+    drawn from (fp64 [V] or a QRef), None for a deterministic drafter."""
+
+    tokens: list
+    parents: list
+    q: list | None = None
+
+    @staticmethod
+    def chain(tokens, q=None):
+        return Tree(list(tokens), list(range(len(tokens))), q)
+
+    def __len__(self):
+        return len(self.tokens)
+
+    def cut(self, n):
+        """The first n drafted nodes (parents come before children, so it is still a tree)."""
+        return type(self)(self.tokens[:n], self.parents[:n], self.q[:n] if self.q else None)
+
+    def fit(self, n, depth):
+        """At most n nodes no deeper than depth, in draft order, renumbered; a node is kept only with its parent."""
+        depth_of, new_id = [0], {0: 0}
+        toks, par, qs = [], [], []
+        for j, (t, p) in enumerate(zip(self.tokens, self.parents)):
+            depth_of.append(depth_of[p] + 1)
+            if len(toks) < n and p in new_id and depth_of[-1] <= depth:
+                new_id[j + 1] = len(toks) + 1
+                toks.append(t)
+                par.append(new_id[p])
+                qs.append(self.q[j] if self.q else None)
+        return type(self)(toks, par, qs if self.q else None)
+
+    @property
+    def is_chain(self):
+        return list(self.parents) == list(range(len(self.parents)))
+
+    def kids(self):
+        """Children of every node (node 0 the anchor) in draft order."""
+        return kids_of(self.parents)
+
+    def ok(self, vocab):
+        """Well formed over a vocabulary: one parent per token, each an earlier node, tokens in range, q per token."""
+        return (len(self.parents) == len(self.tokens) and all(0 <= p <= j for j, p in enumerate(self.parents))
+                and all(0 <= t < vocab for t in self.tokens) and (self.q is None or len(self.q) == len(self.tokens)))
+
+
+def as_tree(x):
+    """A Tree as is; a token list as a chain (spec.py:66-67)."""
+    return x if isinstance(x, Tree) else Tree.chain(x)
 
 
 def _per_node(v, n):
@@ -160,7 +260,7 @@ class VerifyCall:
     def launch(self):
         self.b.stream = torch.cuda.current_stream(self.dev).cuda_stream
         h = _lib.handle(self.dev.index, self.nodes, self.vocab)  # (this stream's handle, grown by other calls or not)
-        h.ck(h.L.gse_verify_tree(h.h, C.byref(self.b), C.byref(self.t), C.byref(self.o)), "gse_verify_tree")
+        h.call("gse_verify_tree", C.byref(self.b), C.byref(self.t), C.byref(self.o))
 
     def result(self, stop=None):
         out = torch.cat([self.e_len[:, None], self.e_st[:, None], self.e_tok, self.e_node], 1).cpu().numpy()
@@ -171,6 +271,8 @@ class VerifyCall:
             tk = [int(v) for v in out[a, 2:2 + min(n, ld)]]
             nd = [int(v) - int(anchors[a]) for v in out[a, 2 + ld:2 + ld + min(n, ld)]]
             why = None
+            if stt == _lib.WALK_KIDS:
+                raise RuntimeError(f"gse_verify_tree: request {a} reached a node with more kids than max_kids")
             if stt == _lib.WALK_ERROR:  # the path also holds the node whose row had no valid token
                 why = "error"
                 if n < ld:
@@ -358,68 +460,82 @@ def pick_batch(x, n, t, seeds, ats):
     b.temperature, b.n, b.seed, b.at = t_d.data_ptr(), n_d.data_ptr(), s_d.data_ptr(), a_d.data_ptr()
     b.out_tokens, b.out_logq, b.out_ld = out_t.data_ptr(), out_v.data_ptr(), nmax
     b.stream = torch.cuda.current_stream(dev).cuda_stream
-    h.ck(h.L.gse_draft_pick(h.h, C.byref(b)), "gse_draft_pick")
+    h.call("gse_draft_pick", C.byref(b))
     out_t._keep = (xt, n_d, t_d, s_d, a_d)
     return out_t, out_v
 
 
 class TreeDrafter:
     """spec.py:125-216 TreeDrafter over a next-token model m: m.dist(seq, path) -> log-probabilities (a device tensor
-    [V]) of the token after seq.tokens + path. Shapes: chain; static rank paths (Medusa, EAGLE-1); dynamic (EAGLE-2:
-    expand the topk best of each level by cumulative log-probability, rerank every candidate, keep the k best).
-    temperature > 0: children are drawn from the model at that temperature and carry q (a QRef) for rejection
-    acceptance. The selection of every node of one level runs in one gse_draft_pick call."""
+    [V]) of the token after seq.tokens + path; m.feed / m.release optional (passed through, as spec.py:146-152 does).
+    Shapes: chain; static rank paths (Medusa, EAGLE-1); dynamic (EAGLE-2: expand the topk best of each level by
+    cumulative log-probability, rerank every candidate, keep the k best). temperature > 0: chain and dynamic children are
+    drawn from the model at that temperature and carry their q (a QRef) for rejection acceptance; static paths always
+    take ranks. The selection of every node of one level runs in one gse_draft_pick call. propose() returns tree_cls
+    objects (default: this module's Tree; the reference's Tree class may be passed instead, it takes the same
+    arguments)."""
 
-    def __init__(self, m, shape="chain", topk=4, depth=6, choices=None, temperature=0.0):
+    def __init__(self, m, shape="chain", topk=4, depth=6, choices=None, temperature=0.0, tree_cls=None):
         assert shape in ("chain", "static", "dynamic") and (shape != "static" or choices)
         self.m, self.shape, self.topk, self.depth, self.t = m, shape, topk, depth, temperature
         self.choices = sorted({tuple(c) for c in choices or ()}, key=lambda c: (len(c), c))
         self.needs = dict(tree=shape != "chain", taps=tuple(getattr(m, "taps", ())))
+        self.tree_cls = tree_cls or Tree
 
     def propose(self, seqs, k):
-        return [self.grow(s, k) if k > 0 else (list(), list(), None) for s in seqs]
+        return [self.grow(s, k) if k > 0 else self.tree_cls([], []) for s in seqs]
 
-    def _pick_level(self, s, lps, n, ats):
-        """n children of each of a level's nodes (log-prob rows lps, absolute indices ats): [(token, q, log-prob)]."""
+    def feed(self, seq, pos, rows):
+        if hasattr(self.m, "feed"):
+            self.m.feed(seq, pos, rows)
+
+    def release(self, sid):
+        if hasattr(self.m, "release"):
+            self.m.release(sid)
+
+    def _pick_level(self, s, lps, n, ats, t):
+        """n children of each of a level's nodes (log-prob rows lps, absolute indices ats) at temperature t:
+        [(token, q, log-prob)] per node."""
         x = torch.stack([lp.reshape(-1) for lp in lps]).float()  # (the drafter's row as fp32)
-        toks, vals = pick_batch(x, n, self.t, s.seed, ats)
+        toks, vals = pick_batch(x, n, t, s.seed, ats)
         toks, vals = toks.cpu().tolist(), vals.cpu().tolist()
         out = []
         for r in range(len(lps)):
-            q = QRef(x[r], self.t) if self.t else None
-            out.append([(int(toks[r][k]), q, float(lps[r][toks[r][k]]) if self.t == 0 else float(vals[r][k]))
+            q = QRef(x[r], t) if t else None
+            out.append([(int(toks[r][k]), q, float(lps[r][toks[r][k]]) if t == 0 else float(vals[r][k]))
                         for k in range(n)])
         return out
 
     def grow(self, s, k):
-        """(tokens, parents, q list or None) of the proposal tree after s (spec.py:161-204)."""
-        m, at = self.m, len(s.tokens)
+        """The proposal tree after s (spec.py:161-204), a tree_cls object."""
+        m, at, T = self.m, len(s.tokens), self.tree_cls
         if self.shape == "chain":
             toks, qs = [], []
             for d in range(k):
-                x, q, _ = self._pick_level(s, [m.dist(s, toks)], 1, [at + d])[0][0]
+                x, q, _ = self._pick_level(s, [m.dist(s, toks)], 1, [at + d], self.t)[0][0]
                 toks.append(x)
                 qs.append(q)
-            return toks, list(range(len(toks))), (qs if self.t else None)
+            return T(toks, list(range(len(toks))), qs if self.t else None)
         if self.shape == "static":
             node, toks, par, order = {(): 0}, [], [], {}
             for c in self.choices:
                 if len(toks) == k or c[:-1] not in node:
                     continue
                 p = node[c[:-1]]
-                if p not in order:
+                if p not in order:  # the node's tokens by rank (spec.py:176: a stable descending sort)
                     lp = m.dist(s, self._path(toks, par, p))
-                    got = self._pick_level(s, [lp], min(lp.numel(), max(cc[-1] for cc in self.choices) + 1), [at])
-                    order[p] = [x for x, _, _ in got[0]]
+                    n = min(lp.numel(), max(cc[-1] for cc in self.choices) + 1)
+                    order[p] = [x for x, _, _ in self._pick_level(s, [lp], n, [at], 0.0)[0]]
                 toks.append(int(order[p][c[-1]]))
                 par.append(p)
                 node[c] = len(toks)
-            return toks, par, None
+            return T(toks, par)
         cand = []  # (score, token, parent candidate index or -1, q)
         beam = [-1]
         for _ in range(self.depth):
             paths = [self._cpath(cand, b) for b in beam]
-            got = self._pick_level(s, [m.dist(s, pt) for pt in paths], self.topk, [at + len(pt) for pt in paths])
+            got = self._pick_level(s, [m.dist(s, pt) for pt in paths], self.topk, [at + len(pt) for pt in paths],
+                                   self.t)
             new = []
             for b, kids in zip(beam, got):
                 for x, q, lp in kids:
@@ -436,8 +552,8 @@ class TreeDrafter:
                 sel.append(i)
         sel.sort()
         idx = {i: j + 1 for j, i in enumerate(sel)}
-        return ([cand[i][1] for i in sel], [idx.get(cand[i][2], 0) for i in sel],
-                [cand[i][3] for i in sel] if self.t else None)
+        return T([cand[i][1] for i in sel], [idx.get(cand[i][2], 0) for i in sel],
+                 [cand[i][3] for i in sel] if self.t else None)
 
     @staticmethod
     def _path(toks, par, n):

@@ -18,13 +18,18 @@
                                        t) in fp64 and n draws draw(q, uniform(mix(seed, SALT_DRAFT + r), at)), each with
                                        log q[x]
   grow_dynamic        spec.py:183-204  EAGLE-2 expand + rerank of a proposal tree from pick()
+  Tree / as_tree      spec.py:22-67    the proposal tree as the scheduler consumes it (scheduler.py:128-133: as_tree,
+                                       ok, fit; cut at :152) and the engine walks it (kids, tokens, q)
 
 The walk is pinned in tests/test_oracle_walk.py by the joint law of its emitted tokens (chi-square against the product
 of the target's dist(), with power controls) and by known answers that fix which uniform index each depth uses. pick and
 grow_dynamic are pinned in tests/test_oracle_drafter.py against the reference's own TreeDrafter outputs on a toy model
 (tests/golden/drafter_golden.npz) and by the stable order, the SALT_DRAFT streams and log q in closed form. mss is
-pinned by the golden vectors of tests/test_oracle.py.
+pinned by the golden vectors of tests/test_oracle.py. Tree is pinned by the known answers of the reference's
+tests/test_spec.py:21-27 (kids, fit, ok) in tests/test_spec_tree.py.
 """
+from dataclasses import dataclass
+
 import numpy as np
 
 from .sampling_ref import dist, draw, mix, sample, uniform
@@ -163,3 +168,49 @@ def _cpath(cand, b):
         out.append(cand[b][1])
         b = cand[b][2]
     return out[::-1]
+
+
+@dataclass
+class Tree:
+    """spec.py:22-63: drafted tokens (node j + 1) with their parent nodes (0 the anchor) and the distribution each was
+    drawn from (None: deterministic)."""
+    tokens: list
+    parents: list
+    q: list | None = None
+
+    @staticmethod
+    def chain(tokens, q=None):
+        return Tree(list(tokens), list(range(len(tokens))), q)
+
+    def __len__(self):
+        return len(self.tokens)
+
+    def cut(self, n):
+        return Tree(self.tokens[:n], self.parents[:n], self.q[:n] if self.q else None)
+
+    def fit(self, n, depth):
+        d, idx, toks, par, qs = [0], {0: 0}, [], [], []
+        for i, (t, p) in enumerate(zip(self.tokens, self.parents)):
+            d.append(d[p] + 1)
+            if len(toks) < n and p in idx and d[-1] <= depth:
+                idx[i + 1] = len(toks) + 1
+                toks.append(t)
+                par.append(idx[p])
+                qs.append(self.q[i] if self.q else None)
+        return Tree(toks, par, qs if self.q else None)
+
+    @property
+    def is_chain(self):
+        return self.parents == list(range(len(self.parents)))
+
+    def kids(self):
+        return kids_of(self.parents)
+
+    def ok(self, vocab):
+        return (len(self.parents) == len(self.tokens) and all(0 <= p <= i for i, p in enumerate(self.parents))
+                and all(0 <= t < vocab for t in self.tokens) and (self.q is None or len(self.q) == len(self.tokens)))
+
+
+def as_tree(x):
+    """spec.py:66-67: a Tree as is (any object with the Tree methods), a token list as a chain."""
+    return x if hasattr(x, "fit") else Tree.chain(x)

@@ -186,7 +186,8 @@ def test_tree_drafter_matches_oracle(ge, gpu, shape, t):
     m = _LM(v, gpu)
     d = ge.spec.TreeDrafter(m, shape, topk=3, depth=3, temperature=t)
     s = NS(tokens=[5, 9, 2], seed=4242)
-    toks, par, q = d.grow(s, 6)
+    tr = d.grow(s, 6)
+    toks, par, q = tr.tokens, tr.parents, tr.q
     if shape == "chain":
         want_t, want_q = [], []
         for k in range(6):
@@ -376,3 +377,100 @@ def test_verify_round_in_a_captured_graph(ge, gpu):
         g.replay()
         torch.cuda.synchronize()
         assert call.result() == ref, k
+
+
+@pytest.mark.parametrize("shape,t", [("chain", 0.0), ("chain", 1.0), ("dynamic", 0.0), ("dynamic", 0.8)])
+def test_drafter_proposals_through_scheduler_and_mss(ge, gpu, shape, t):
+    """The drafter as the reference's scheduler and engine use it: propose() (selection on the device) -> as_tree ->
+    ok -> fit (scheduler.py:128-133, the oracle's Tree injected as the tree class), then at every node with kids the
+    drop-in mss over (token, tree.q[c - 1]) (engine.py:280-283; the q of a sampled child is a QRef, read on the device)
+    against the oracle's mss over the oracle's own drafted q: same tokens, same accepted kid. The materialised q equals
+    the oracle's softmax within 1e-12."""
+    from types import SimpleNamespace as NS
+    v, k = 4000, 6
+    m = _LM(v, gpu)
+    seqs = [NS(tokens=[5, 9, 2], seed=4242), NS(tokens=[7, 1], seed=99)]
+    d = ge.spec.TreeDrafter(m, shape, topk=3, depth=3, temperature=t, tree_cls=spo.Tree)
+    rng = np.random.default_rng(5)
+    P = ge.sampling.SamplingParams
+    nodes = 0
+    for s, tr in zip(seqs, d.propose(seqs, k)):
+        tr = spo.as_tree(tr)
+        assert isinstance(tr, spo.Tree) and tr.ok(v)
+        tr = tr.fit(k, 4)
+        at = len(s.tokens)
+        lp = lambda pt: m.dist(s, pt).cpu().numpy().astype(np.float64)
+        if shape == "chain":
+            wt, wq = [], []
+            for j in range(k):
+                x, q, _ = spo.pick(lp(wt), 1, t, s.seed, at + j)[0]
+                wt.append(x)
+                wq.append(q)
+            want = spo.Tree.chain(wt, wq if t else None).fit(k, 4)
+        else:
+            want = spo.Tree(*spo.grow_dynamic(lp, s.seed, at, k, 3, 3, t)).fit(k, 4)
+        assert (tr.tokens, tr.parents) == (want.tokens, want.parents)
+        assert (tr.q is None) == (t == 0)
+        if t:
+            for qa, qb in zip(tr.q, want.q):
+                np.testing.assert_allclose(np.asarray(qa), qb, rtol=1e-12, atol=1e-300)
+        # the engine's strict node: dist of the target row, then mss over the node's kids
+        for u, kids in enumerate(tr.kids()):
+            if not kids:
+                continue
+            x = (rng.standard_normal(v) * 2.0).astype(np.float32)
+            pp = P(temperature=1.0, accept="rejection")
+            pd = ora.dist(x, pp)
+            got = ge.spec.mss(torch.from_numpy(pd).to(gpu), [(tr.tokens[c - 1], tr.q[c - 1] if tr.q else None)
+                                                             for c in kids], s.seed, 7 + u)
+            exp = spo.mss(pd, [(want.tokens[c - 1], want.q[c - 1] if want.q else None) for c in kids], s.seed, 7 + u)
+            assert got == exp, (shape, t, u, got, exp)
+            nodes += 1
+    assert nodes > 0
+
+
+def test_qprob_matches_softmax(ge, gpu):
+    """gse_qprob: q = softmax(float64(x) / t) of fp32 and bf16 drafter rows (spec.py:157) against numpy in fp64."""
+    rng = np.random.default_rng(8)
+    x = (rng.standard_normal((5, 30011)) * 3.0).astype(np.float32)
+    t = [1.0, 0.5, 1.7, 2.0, 0.9]
+    got = ge.spec.qprob(torch.from_numpy(x).to(gpu), t).cpu().numpy()
+    for r in range(5):
+        z = x[r].astype(np.float64) / t[r]
+        e = np.exp(z - z.max())
+        np.testing.assert_allclose(got[r], e / e.sum(), rtol=1e-12, atol=1e-300)
+    xb, x32 = _bf16(x, gpu)
+    got = ge.spec.qprob(xb, t).cpu().numpy()
+    for r in range(5):
+        z = x32[r].astype(np.float64) / t[r]
+        e = np.exp(z - z.max())
+        np.testing.assert_allclose(got[r], e / e.sum(), rtol=1e-12, atol=1e-300)
+
+
+def test_understated_max_kids_is_reported(ge, gpu):
+    """A C-ABI caller that passes a max_kids below a strict node's kid count: the round cannot decide that node as the
+    reference would (spec.py:91 walks every kid), so the walk stops before it with GSE_WALK_KIDS (the node in
+    emit_nodes[emit_len]) instead of emitting a token; the Python layer raises. Requests that never reach such a node
+    are unaffected."""
+    reqs = ge.workloads.c4(requests=range(3), v=20000)
+    calls = [dict(target=torch.from_numpy(r["target"]).to(gpu), tokens=r["tokens"], parents=r["parents"],
+                  params=r["params"], seed=r["seed"], draft=torch.from_numpy(r["draft"]).to(gpu), draft_t=1.0)
+             for r in reqs]
+    call = ge.spec.VerifyCall(calls)
+    assert call.t.max_kids == 2  # the anchor has two kids
+    call.t.max_kids = 1
+    call.launch()
+    st = call.e_st.cpu().tolist()
+    n = call.e_len.cpu().tolist()
+    nodes = call.e_node.cpu().numpy()
+    for a in range(3):
+        assert st[a] == ge._lib.WALK_KIDS and n[a] == 0, (a, st[a], n[a])
+        assert nodes[a, 0] == call.anchors[a]
+    with pytest.raises(RuntimeError, match="kids"):
+        call.result()
+    call.t.max_kids = 2
+    call.launch()
+    for a, r in enumerate(reqs):
+        want = spo.verify_tree(r["target"], _q_of_draft(r["draft"], r["parents"]), r["tokens"], r["parents"],
+                               r["params"], r["seed"])
+        assert call.result()[a] == want
