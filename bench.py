@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Throughput of the fused token-selection path on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c1|c2|c4|c5|all] [--no-cpu]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c1|c2|c4|c5|all] [--no-cpu] [--no-through-sample]
 
 A step is one call of the selection path over one batch of the chosen workload, with every input already resident in
 HBM (logits, packed grammar masks, token histories, per-row parameters, shared uniforms, draft trees):
@@ -16,6 +16,8 @@ Timed regions, each bracketed by torch.cuda.synchronize():
      dominant kernel's average duration, which gives the roofline (algorithmic bytes per launch / duration). Those
      events add a few microseconds between kernels, which is why regions 1 and 2 carry none.
   4. the read-only ceiling: a plain streaming read (libgse_probe.so) over the same logits, best of a few launch shapes.
+  5. (c1, c2, c3, c5) the drop-in's Python surface, sampling.sample() called as the engine calls it, each call returning
+     its tokens: microseconds per call and the host time per call ("through_sample"; never "value").
 The roofline's "traffic" (HBM bytes per launch of the main kernel) is read from the committed rocprofv3 counter
 summary profiles/main_kernel_<config>_traffic.txt when one exists (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a
 plain copy's reading).
@@ -328,8 +330,65 @@ def run_sample(args, ge, torch, batch):
     per = {kern[i]: kms[i] / calls * 1e3 for i in range(min(len(kern), len(kms)))}
     log("[bench] per call (profiled) " + ", ".join(f"{k} {v:.2f} us" for k, v in per.items()))
     ceil = read_ceiling([s["x"] for s in sets], torch)
+    thr = through_sample(args, ge, torch, batch, [s["x"] for s in sets], gpu_tokens) if args.through_sample else None
     return dict(wall=wall, ts=ts, per=per, dom=("main_kernel", per["main_kernel"]), copies=copies,
-                a_bytes=batch.bytes_per_row() * rows, units=rows, gpu_out=gpu_tokens, ceiling=ceil)
+                a_bytes=batch.bytes_per_row() * rows, units=rows, gpu_out=gpu_tokens, ceiling=ceil, through=thr)
+
+
+def through_sample(args, ge, torch, batch, xs, want):
+    """The drop-in's Python surface timed as the engine calls it (engine.py:271-273: sample(logits, params, seeds,
+    idxs, masks) -> list of ints, one host round trip per call), with the extensions' keywords: the step's SamplingParams
+    objects, per-row seeds and idxs as Python lists, the uniforms as a device tensor, and
+      resident: the grammar masks in a grammar.MaskBatch (packed words in one pinned buffer, one copy) and the penalty
+                histories in a sampling.History (device-resident, read in place);
+      lists:    per-row mask tensors (packed int32, the words xgrammar fills) and per-row history arrays, as a caller
+                that keeps them per request passes them.
+    Per variant: microseconds per sample() call (wall clock over K calls, each returning its tokens), and the host
+    microseconds per call spent before the library call returns (sample_ex over K calls, no synchronisation)."""
+    dev = xs[0].device
+    rows, v = batch.rows, batch.vocab
+    params = list(batch.params)
+    seeds, idxs = list(range(1000, 1000 + rows)), [7] * rows
+    uni = torch.from_numpy(batch.uniforms).to(dev)
+    hist_res = mb = None
+    if batch.history is not None:
+        hist_res = ge.sampling.History(rows, max(len(h) for h in batch.history), dev)
+        for r, hh in enumerate(batch.history):
+            hist_res.set(r, hh)
+    if batch.masks is not None:
+        mb = ge.grammar.MaskBatch(rows, v)
+        for r in range(rows):
+            mb.set(r, batch.masks[r])
+    variants = {"resident": (mb, hist_res),
+                "lists": (None if batch.masks is None else [torch.from_numpy(m) for m in batch.masks],
+                          batch.history)}
+    out = {}
+    steps = max(20, args.steps // 2)
+    for name, (masks, hist) in variants.items():
+        got = ge.sampling.sample(xs[0], params, seeds, idxs, masks, history=hist, uniforms=uni)
+        if got != want:
+            raise RuntimeError(f"through-sample ({name}) tokens differ from gse_sample's")
+        for k in range(3):
+            ge.sampling.sample(xs[k % len(xs)], params, seeds, idxs, masks, history=hist, uniforms=uni)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(steps):
+            ge.sampling.sample(xs[k % len(xs)], params, seeds, idxs, masks, history=hist, uniforms=uni)
+        wall = time.perf_counter() - t0
+        host = 0.0
+        torch.cuda.synchronize()
+        for k in range(steps):
+            t1 = time.perf_counter()
+            ge.sampling.sample_ex(xs[k % len(xs)], params, seeds, idxs, masks, history=hist, uniforms=uni)
+            host += time.perf_counter() - t1
+            if k % 8 == 7:
+                torch.cuda.synchronize()  # (the host keeps at most 8 calls ahead)
+        torch.cuda.synchronize()
+        out[name] = {"us_per_call": round(wall * 1e6 / steps, 2), "rows_per_s": round(rows * steps / wall, 1),
+                     "host_us_per_call": round(host * 1e6 / steps, 2), "calls": steps}
+        log(f"[bench] through sample() ({name}): {out[name]['us_per_call']} us per call, host "
+            f"{out[name]['host_us_per_call']} us")
+    return out
 
 
 def run_verify(args, ge, torch):
@@ -434,6 +493,8 @@ def bench_one(args, config):
         "end_to_end": {"step_us_wall": round(r["wall"] * 1e6 / steps, 3),
                        "hbm_frac": round(a / (r["wall"] / steps) / PEAK_HBM, 4)},
     }
+    if r.get("through"):
+        result["through_sample"] = r["through"]
     if r["ceiling"]:
         c = r["ceiling"]
         result["read_ceiling"] = dict(c, frac_of_peak=round(c["read_GBps"] * 1e9 / PEAK_HBM, 4),
@@ -459,6 +520,8 @@ def main():
     ap.add_argument("--config", default="c3", choices=sorted(WORKLOADS) + ["all"])
     ap.add_argument("--copies", type=int, default=0, help="input copies to rotate over (0: enough to exceed the MALL)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-through-sample", dest="through_sample", action="store_false",
+                    help="skip timing the drop-in's sample() surface (done for c1, c2, c3, c5 by default)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="before the steps, copy a MIB-MiB device buffer 5 times (a plain copy kernel of known size, "
                          "the reference point for rocprofv3 FETCH_SIZE / WRITE_SIZE)")

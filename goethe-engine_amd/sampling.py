@@ -14,6 +14,7 @@ Logits may be torch tensors on the GPU (used in place, fp32 or bf16, any row str
 (copied to the GPU first). There is no CPU path: without a HIP device every call raises RuntimeError.
 """
 import ctypes as C
+import weakref
 from dataclasses import dataclass
 
 import numpy as np
@@ -120,34 +121,71 @@ def _get(p, name, default):
     return default if v is None else v
 
 
-def _rows(params, seeds, idxs, hist_offsets):
-    n = len(params)
-    r = np.zeros(n, dtype=_lib.ROW)
-    for i, p in enumerate(params):
-        t = float(p.temperature)
-        t32 = np.float32(t)
-        r["temperature"][i] = t32
-        if t > 0 and t32 == 0:
-            r["flags"][i] = _lib.ROW_TEMP_UNDERFLOW
-        r["top_k"][i] = min(int(_get(p, "top_k", 0)), 0x7FFFFFFF)
-        r["top_p"][i] = float(_get(p, "top_p", 1.0))
-        r["min_p"][i] = float(_get(p, "min_p", 0.0))
-        r["repetition_penalty"][i] = np.float32(_get(p, "repetition_penalty", 1.0))
-        r["frequency_penalty"][i] = np.float32(_get(p, "frequency_penalty", 0.0))
-        r["presence_penalty"][i] = np.float32(_get(p, "presence_penalty", 0.0))
-        r["logprobs"][i] = int(_get(p, "logprobs", 0))
-        r["seed"][i] = (int(seeds[i]) & M64) if seeds is not None and seeds[i] is not None else 0
-        r["idx"][i] = (int(idxs[i]) & M64) if idxs is not None and idxs[i] is not None else 0
+# Row templates: the 72-byte gse_row of a params object's fields (seed, idx and history range left zero, mask_row -1),
+# kept per live frozen params object. A request's SamplingParams is one frozen object for its whole life (the engine
+# passes s.params every step), so a step's rows are a join of cached templates and a few vectorised columns.
+_tmpl = {}
+
+
+def _template(p):
+    e = _tmpl.get(id(p))
+    if e is not None and e[0]() is p:
+        return e[1]
+    r = np.zeros(1, dtype=_lib.ROW)
+    t = float(p.temperature)
+    t32 = np.float32(t)
+    r["temperature"] = t32
+    r["flags"] = _lib.ROW_TEMP_UNDERFLOW if t > 0 and t32 == 0 else 0
+    r["top_k"] = min(int(_get(p, "top_k", 0)), 0x7FFFFFFF)
+    r["top_p"] = float(_get(p, "top_p", 1.0))
+    r["min_p"] = float(_get(p, "min_p", 0.0))
+    r["repetition_penalty"] = np.float32(_get(p, "repetition_penalty", 1.0))
+    r["frequency_penalty"] = np.float32(_get(p, "frequency_penalty", 0.0))
+    r["presence_penalty"] = np.float32(_get(p, "presence_penalty", 0.0))
+    r["logprobs"] = int(_get(p, "logprobs", 0))
     r["mask_row"] = -1
-    if hist_offsets is not None:
-        r["hist_begin"] = hist_offsets[:-1]
-        r["hist_end"] = hist_offsets[1:]
+    b = r.tobytes()
+    dp = getattr(p, "__dataclass_params__", None)
+    if dp is not None and dp.frozen:  # (a mutable params object is read afresh every call)
+        try:
+            ref = weakref.ref(p, lambda _, k=id(p): _tmpl.pop(k, None))
+        except TypeError:
+            return b
+        _tmpl[id(p)] = (ref, b)
+    return b
+
+
+def _u64_col(vals, n):
+    """A uint64 column from per-row Python ints (taken mod 2^64) or None (0)."""
+    if vals is None:
+        return np.zeros(n, np.uint64)
+    try:
+        return np.fromiter(vals, np.uint64, n)
+    except (TypeError, OverflowError, ValueError):
+        return np.array([(int(v) & M64) if v is not None else 0 for v in vals], np.uint64)
+
+
+def _rows(params, seeds, idxs, hist_range):
+    """gse_row records of the rows: params fields, seeds and idxs (mod 2^64, None -> 0), mask_row -1, and the history
+    range of each row: hist_range is None, CSR offsets [n + 1], or (begin [n], end [n])."""
+    n = len(params)
+    r = np.frombuffer(b"".join([_template(p) for p in params]), dtype=_lib.ROW).copy() if n else \
+        np.zeros(0, dtype=_lib.ROW)
+    r["seed"] = _u64_col(seeds, n)
+    r["idx"] = _u64_col(idxs, n)
+    if hist_range is not None:
+        if isinstance(hist_range, tuple):
+            r["hist_begin"], r["hist_end"] = hist_range
+        else:
+            r["hist_begin"] = hist_range[:-1]
+            r["hist_end"] = hist_range[1:]
     return r
 
 
 def _masks(h, masks, n, v, dev, rows):
-    """Per-row masks (None, bool [V] or packed int32 [>= ceil(V / 32)]), or a grammar.MaskBatch -> device words [k, W]
-    and rows' mask_row."""
+    """Per-row masks (None, bool [V] or packed int32 [>= ceil(V / 32)], torch or numpy), or a grammar.MaskBatch ->
+    device words [k, W] and rows' mask_row. Packed rows go to the device in one copy, bool rows in one copy and one
+    pack launch."""
     if masks is None:
         return None, 0
     words = (v + 31) // 32
@@ -159,54 +197,124 @@ def _masks(h, masks, n, v, dev, rows):
         idx = np.nonzero(masks.filled[:n])[0]
         rows["mask_row"][idx] = idx
         return masks.device_words(dev, n), masks.words
-    packed, bools, where = [], [], []
+    pk_i, pk, bo_i, bo = [], [], [], []
     for i in range(n):
-        m = masks[i]
+        m = masks[i] if i < len(masks) else None
         if m is None:
             continue
-        mt = m if isinstance(m, torch.Tensor) else torch.from_numpy(np.asarray(m))
-        if mt.dtype in (torch.int32, torch.uint32) and mt.numel() >= words and mt.numel() < v:
-            packed.append((i, mt.reshape(-1)[:words].view(torch.int32) if mt.dtype == torch.uint32 else
-                           mt.reshape(-1)[:words]))
+        if not isinstance(m, torch.Tensor):
+            m = torch.from_numpy(np.asarray(m))
+        size = m.numel()
+        if m.dtype in _PACKED and words <= size < v:
+            pk_i.append(i)
+            pk.append(m if size == words and m.dim() == 1 else m.reshape(-1)[:words])
+        elif size == v:
+            bo_i.append(i)
+            bo.append(m if m.dim() == 1 else m.reshape(-1))
         else:
-            if mt.numel() != v:
-                raise ValueError(f"mask of row {i} has {mt.numel()} entries, the row has {v} tokens")
-            bools.append((i, mt.reshape(-1).to(torch.bool)))
-    if not packed and not bools:
+            raise ValueError(f"mask of row {i} has {size} entries, the row has {v} tokens")
+    if not pk and not bo:
         return None, 0
-    out = torch.empty((len(packed) + len(bools), words), dtype=torch.int32, device=dev)
-    k = 0
-    for i, mt in packed:
-        out[k].copy_(mt.to(dev, non_blocking=True))
-        rows["mask_row"][i] = k
-        k += 1
-    if bools:
-        b = torch.stack([mt for _, mt in bools]).to(dev, non_blocking=True).to(torch.uint8)
-        h.ck(h.L.gse_pack_mask(h.h, _lib.ptr(b), b.stride(0), len(bools), v, _lib.ptr(out[k:]), words,
-                               _lib.stream_of(dev.index)), "gse_pack_mask")
-        for j, (i, _) in enumerate(bools):
-            rows["mask_row"][i] = k + j
+    out = torch.empty((len(pk) + len(bo), words), dtype=torch.int32, device=dev)
+    if pk:
+        out[:len(pk)].copy_(_stack(pk, dev).view(torch.int32))
+        rows["mask_row"][pk_i] = np.arange(len(pk), dtype=np.int32)
+    if bo:
+        t = _stack(bo, dev)
+        b = t.view(torch.uint8) if t.dtype == torch.bool else (t != 0).to(torch.uint8)
+        h.call("gse_pack_mask", _lib.ptr(b), b.stride(0), len(bo), v, _lib.ptr(out[len(pk):]), words,
+               _lib.stream_of(dev.index))
+        rows["mask_row"][bo_i] = len(pk) + np.arange(len(bo), dtype=np.int32)
     return out, words
 
 
+_PACKED = (torch.int32, torch.uint32)
+
+
+def _stack(rows, dev):
+    """Equal-length 1-D tensors as one [k, n] tensor on dev: stacked where they are, then one copy."""
+    t = torch.stack(rows) if len({r.device for r in rows}) == 1 else torch.stack([r.cpu() for r in rows])
+    return t.to(dev, non_blocking=True)
+
+
+class History:
+    """Penalty histories resident on the device: row r's token ids are ids[r, :length[r]] of an int32 [rows, capacity]
+    device tensor. sample(..., history=h) reads them in place (each row's range in the buffer, no copy); append() adds
+    one token per row on the device, as an engine does after each step. For the engine's own layout (a list of per-row
+    token sequences) sample() builds the same ranges from one concatenation."""
+
+    is_history = True
+
+    def __init__(self, rows, capacity, device=None):
+        dev = device if device is not None else _device()
+        self.ids = torch.full((int(rows), int(capacity)), -1, dtype=torch.int32, device=dev)
+        self.length = np.zeros(int(rows), np.int64)
+
+    def set(self, row, ids):
+        """Row `row`'s history (its first capacity ids kept)."""
+        t = ids if isinstance(ids, torch.Tensor) else torch.from_numpy(np.asarray(ids, dtype=np.int64))
+        t = t.reshape(-1)[:self.ids.shape[1]]
+        self.ids[row, :t.numel()].copy_(t.to(self.ids.device, torch.int32), non_blocking=True)
+        self.length[row] = t.numel()
+
+    def append(self, tokens):
+        """One token more for each of the first len(tokens) rows (device tensor or list); rows at capacity keep theirs."""
+        n = len(tokens)
+        room = np.nonzero(self.length[:n] < self.ids.shape[1])[0]
+        if not len(room):
+            return
+        t = tokens if isinstance(tokens, torch.Tensor) else torch.tensor(list(tokens), dtype=torch.int32)
+        t = t.to(self.ids.device, torch.int32)
+        ri = torch.from_numpy(room).to(self.ids.device)
+        ci = torch.from_numpy(self.length[room]).to(self.ids.device)
+        self.ids[ri, ci] = t[ri]
+        self.length[room] += 1
+
+    def ranges(self, n):
+        """(begin, end) of the first n rows in the flattened buffer."""
+        cap = self.ids.shape[1]
+        begin = np.arange(n, dtype=np.int64) * cap
+        return begin, begin + self.length[:n]
+
+
 def _history(history, n, dev):
+    """The rows' penalty histories as a device id buffer and each row's (begin, end) in it: None; a History (used in
+    place); a CSR pair (ids, offsets [n + 1]); or per-row id sequences (None: no history), concatenated on the host, or on
+    the device when every row is a device tensor. Ids outside [0, vocab) are ignored by the library."""
     if history is None:
         return None, None
-    parts, offs = [], [0]
-    for i in range(n):
-        hi = history[i] if i < len(history) else None
-        if hi is None:
-            offs.append(offs[-1])
-            continue
-        a = hi.detach().cpu().numpy() if isinstance(hi, torch.Tensor) else np.asarray(hi)
-        a = a.astype(np.int64).reshape(-1)
-        a = a[(a >= 0) & (a < 0x7FFFFFFF)].astype(np.int32)
-        parts.append(a)
-        offs.append(offs[-1] + len(a))
-    if offs[-1] == 0:
+    if getattr(history, "is_history", False):
+        if history.ids.shape[0] < n:
+            raise ValueError(f"history of {history.ids.shape[0]} rows for {n} rows")
+        return history.ids.reshape(-1), history.ranges(n)
+    if isinstance(history, tuple) and len(history) == 2:
+        ids, offs = history
+        offs = np.asarray(offs, dtype=np.int64)
+        if offs.shape != (n + 1,):
+            raise ValueError(f"history offsets must have {n + 1} entries")
+        if offs[-1] == 0:
+            return None, None
+        t = ids if isinstance(ids, torch.Tensor) else torch.from_numpy(np.asarray(ids))
+        return t.to(dev, torch.int32, non_blocking=True).reshape(-1), offs
+    rows = [history[i] if i < len(history) else None for i in range(n)]
+    lens = np.array([0 if h is None else (h.numel() if isinstance(h, torch.Tensor) else len(h)) for h in rows],
+                    np.int64)
+    if lens.sum() == 0:
         return None, None
-    ids = torch.from_numpy(np.concatenate(parts)).to(dev, non_blocking=True)
-    return ids, np.asarray(offs, dtype=np.int64)
+    offs = np.zeros(n + 1, np.int64)
+    np.cumsum(lens, out=offs[1:])
+    live = [h for h, k in zip(rows, lens) if k]
+    if all(isinstance(h, torch.Tensor) and h.device.type == "cuda" for h in live):
+        ids = torch.cat([h.reshape(-1) for h in live]).to(dev)
+        if ids.dtype != torch.int32:
+            ids = torch.where((ids >= 0) & (ids < 0x7FFFFFFF), ids, torch.full_like(ids, -1)).to(torch.int32)
+        return ids, offs
+    a = np.concatenate([h.detach().cpu().numpy().reshape(-1) if isinstance(h, torch.Tensor) else
+                        np.asarray(h).reshape(-1) for h in live])
+    if a.dtype != np.int32:
+        a = a.astype(np.int64)
+        a = np.where((a >= 0) & (a < 0x7FFFFFFF), a, -1).astype(np.int32)
+    return torch.from_numpy(a).to(dev, non_blocking=True), offs
 
 
 class Selection:
@@ -243,21 +351,24 @@ def _prepare(logits, params, seeds, idxs, masks, history, uniforms):
         raise ValueError(f"{len(params)} params for {n} rows")
     dev = x.device
     h = _lib.handle(dev.index, n, v)
-    hist_dev, offs = _history(history, n, dev)
-    rows = _rows(params, seeds, idxs, offs)
+    hist_dev, hrange = _history(history, n, dev)
+    rows = _rows(params, seeds, idxs, hrange)
     mask_dev, mask_ld = _masks(h, masks, n, v, dev, rows)
     rows_dev = torch.from_numpy(rows.view(np.uint8)).to(dev, non_blocking=True)
     uni_dev = None
     if uniforms is not None:
         u = uniforms if isinstance(uniforms, torch.Tensor) else torch.from_numpy(np.asarray(uniforms, np.float64))
         uni_dev = u.to(dev, torch.float64).reshape(-1).contiguous()
-    keep = (x, rows_dev, mask_dev, hist_dev, uni_dev)
+    keep = (x, rows_dev, mask_dev, hist_dev, uni_dev, rows)
     return h, x, code, dev, _batch(x, code, rows_dev, mask_dev, mask_ld, hist_dev, uni_dev, dev), keep
 
 
-def _sample_flags(params):
+def _sample_flags(params, rows=None):
     """GSE_BATCH_* bits the drop-in adds to a gse_sample call: NO_SPLIT when every row is greedy (temperature 0 as
     float32, as the device decides), since greedy rows never take the split-row finish and its launch is saved."""
+    if rows is not None:
+        greedy = (rows["temperature"] == 0) & ((rows["flags"] & _lib.ROW_TEMP_UNDERFLOW) == 0)
+        return _lib.BATCH_NO_SPLIT if len(rows) and bool(greedy.all()) else 0
     return _lib.BATCH_NO_SPLIT if params and all(float(p.temperature) == 0.0 for p in params) else 0
 
 
@@ -273,8 +384,9 @@ def sample_ex(logits, params, seeds, idxs, masks, history=None, uniforms=None, e
     h, x, code, dev, b, keep = _prepare(x, params, seeds, idxs, masks, history, uniforms)
     if exact:
         b.flags |= _lib.BATCH_EXACT
-    b.flags |= int(flags) | _sample_flags(params)
-    nlp = max([int(_get(p, "logprobs", 0)) for p in params] + [0])
+    rows = keep[5]
+    b.flags |= int(flags) | _sample_flags(params, rows)
+    nlp = min(int(rows["logprobs"].max()), _lib.MAX_LOGPROBS) if n else 0
     toks = torch.empty(n, dtype=torch.int32, device=dev)
     o = _lib.Out()
     o.size = C.sizeof(_lib.Out)
@@ -287,7 +399,7 @@ def sample_ex(logits, params, seeds, idxs, masks, history=None, uniforms=None, e
     if processed:
         proc = torch.empty((n, v), dtype=torch.float32, device=dev)
         o.processed, o.processed_ld = proc.data_ptr(), v
-    h.ck(h.L.gse_sample(h.h, C.byref(b), C.byref(o)), "gse_sample")
+    h.call("gse_sample", C.byref(b), C.byref(o))
     sel = Selection(toks, lp_ids, lps, proc)
     sel._keep = keep
     return sel
@@ -305,7 +417,7 @@ def dist_batch(logits, params, masks=None, history=None):
     n, v = x.shape
     h, x, code, dev, b, keep = _prepare(x, params, None, None, masks, history, None)
     out = torch.empty((n, v), dtype=torch.float64, device=dev)
-    h.ck(h.L.gse_dist(h.h, C.byref(b), out.data_ptr(), v), "gse_dist")
+    h.call("gse_dist", C.byref(b), out.data_ptr(), v)
     return out
 
 
@@ -328,8 +440,8 @@ def draw(q, u):
     h = _lib.handle(dev.index, 1, qt.numel())
     ut = torch.tensor([float(u)], dtype=torch.float64, device=dev)
     out = torch.empty(1, dtype=torch.int32, device=dev)
-    h.ck(h.L.gse_draw(h.h, qt.data_ptr(), qt.numel(), 1, qt.numel(), ut.data_ptr(), out.data_ptr(),
-                      _lib.stream_of(dev.index)), "gse_draw")
+    h.call("gse_draw", qt.data_ptr(), qt.numel(), 1, qt.numel(), ut.data_ptr(), out.data_ptr(),
+                      _lib.stream_of(dev.index))
     j = int(out.item())
     if j < 0:
         raise IndexError("draw: no token has positive probability")

@@ -171,12 +171,26 @@ def test_c4_tree_verify(ge, gpu):
         assert res == spo.verify_tree(r["target"], q, r["tokens"], r["parents"], r["params"], r["seed"])
 
 
+def _dev(x, gpu, dtype):
+    """x (fp32 numpy) on the device as fp32 or bf16, and the fp32 values the device holds (bf16 widens exactly)."""
+    d = torch.from_numpy(x).to(gpu)
+    if dtype == "bf16":
+        d = d.to(torch.bfloat16)
+        return d, d.float().cpu().numpy()
+    return d, x
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("v", [1, 7, 33, 8191, 8193, 20000])
-def test_odd_vocab_sizes_and_strides(ge, gpu, v):
+def test_odd_vocab_sizes_and_strides(ge, gpu, v, dtype):
+    """Odd vocabularies, a row stride of v + 5 and a start two elements in (rows not 16-byte aligned), with ties, masks,
+    penalty histories, top-k, top-p and min-p; fp32 and bf16 logits (the bf16 rows against the oracle on the widened
+    values); the fast and the exact path."""
     rng = np.random.default_rng(v)
     n = 12
     x = (rng.normal(0, 2, size=(n, v + 5)) ).astype(np.float32)
     x[3, : min(v, 4)] = 1.0   # ties
+    xd, x = _dev(x, gpu, dtype)
     P = ge.sampling.SamplingParams
     params = [P(), P(temperature=0.9), P(temperature=1.0, top_k=3), P(temperature=1.4, top_p=0.7),
               P(temperature=0.6, min_p=0.1), P(temperature=1.0, repetition_penalty=1.3, frequency_penalty=0.4)] * 2
@@ -185,10 +199,102 @@ def test_odd_vocab_sizes_and_strides(ge, gpu, v):
     m[0] = True
     masks = [m if r % 4 == 1 else None for r in range(n)]
     seeds, idxs = list(range(n)), [5] * n
-    xt = torch.from_numpy(x).to(gpu)[:, 2:2 + v]          # row stride v + 5, misaligned start
+    xt = xd[:, 2:2 + v]                                   # row stride v + 5, misaligned start
     want = ora.sample(x[:, 2:2 + v], params, seeds, idxs, masks, history=hist)
     f, e = both_paths(ge, xt, params, seeds, idxs, masks, history=hist)
     assert f == want and e == want
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_masks_penalties_minp_logprobs(ge, gpu, dtype):
+    """The full stack over one odd vocabulary in both dtypes: bool masks and packed masks in one call, a MaskBatch in
+    another, penalty histories, min-p, top-k / top-p, logprobs, greedy rows with logprobs; rows aligned and rows
+    starting one element in. Tokens, processed logits (bit-exact) and logprobs (1e-5) against the oracle on the
+    device's values, on the fast and the exact path."""
+    rng = np.random.default_rng(21 if dtype == "f32" else 22)
+    n, v = 16, 50257
+    P = ge.sampling.SamplingParams
+    params = [P(temperature=[0.0, 0.7, 1.0, 1.3][r % 4], top_k=[0, 40, 0, 200][(r // 4) % 4],
+                top_p=[1.0, 0.9, 0.95, 0.8][r % 4], min_p=[0.0, 0.05, 0.0, 0.1][(r + 1) % 4],
+                repetition_penalty=[1.0, 1.1, 1.3, 1.05][(r + 2) % 4], frequency_penalty=[0.0, 0.5, 0.2, 1.0][r % 4],
+                presence_penalty=[0.0, 0.3, 0.0, 0.7][(r + 3) % 4], logprobs=[None, 3, 20, 0][(r // 2) % 4])
+              for r in range(n)]
+    hist = [rng.integers(0, v, size=int(rng.integers(0, 400))) for _ in range(n)]
+    hist[5] = None
+    bools = [(rng.random(v) < [0.05, 0.5, 0.9][r % 3]) for r in range(n)]
+    for m in bools:
+        m[int(rng.integers(0, v))] = True
+    masks_np = [bools[r] if r % 3 else None for r in range(n)]
+    masks_in = [None if m is None else (torch.from_numpy(m) if r % 2 else ge.grammar.pack(m))
+                for r, m in enumerate(masks_np)]
+    seeds, idxs = [int(s) for s in rng.integers(0, 1 << 62, size=n)], list(range(n))
+    for off in (0, 1):
+        x = rng.normal(0, 2.5, size=(n, v + 8)).astype(np.float32)
+        xd, x = _dev(x, gpu, dtype)
+        xt, xn = xd[:, off:off + v], x[:, off:off + v]
+        want = ora.sample_full(xn, params, seeds, idxs, masks_np, hist)
+        mb = ge.grammar.MaskBatch(n, v)
+        for r, m in enumerate(masks_np):
+            if m is not None:
+                mb.set(r, m)
+        for exact in (False, True):
+            for masks in (masks_in, mb):
+                sel = ge.sampling.sample_ex(xt, params, seeds, idxs, masks, history=hist, exact=exact, processed=True)
+                assert sel.tolist() == [w["token"] for w in want], (dtype, off, exact)
+                proc = sel.processed.cpu().numpy()
+                ids, lps = sel.logprob_ids.cpu().numpy(), sel.logprobs.cpu().numpy()
+                for r, w in enumerate(want):
+                    assert np.array_equal(proc[r].view(np.uint32), w["processed"].view(np.uint32)), (dtype, off, r)
+                    if "logprob_ids" in w:
+                        k = len(w["logprob_ids"])
+                        assert list(ids[r, :k]) == list(w["logprob_ids"]), (dtype, off, exact, r)
+                        np.testing.assert_allclose(lps[r, :k], w["logprobs"], rtol=LOGPROB_RTOL)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_dist_with_penalties_minp_masks(ge, gpu, dtype):
+    """gse_dist (sampling.py:88-97 with the extensions) against the oracle's dist, row by row within 1e-12: penalty
+    histories, min-p, masks, top-k, top-p, flat rows whose keep set runs deep, bf16 rows unaligned."""
+    rng = np.random.default_rng(31 if dtype == "f32" else 32)
+    n, v = 12, 100003
+    P = ge.sampling.SamplingParams
+    params = [P(temperature=[0.8, 1.0, 1.4][r % 3], top_k=[0, 50, 0, 0][r % 4], top_p=[0.9, 1.0, 0.99, 0.8][r % 4],
+                min_p=[0.0, 0.05, 0.0, 0.02, 0.0, 0.2][r % 6], repetition_penalty=[1.0, 1.2][r % 2],
+                frequency_penalty=[0.3, 0.0, 0.8][r % 3], presence_penalty=[0.0, 0.5][(r // 2) % 2])
+              for r in range(n)]
+    hist = [rng.integers(0, v, size=int(rng.integers(1, 300))) for _ in range(n)]
+    masks = [(rng.random(v) < 0.6) if r % 3 == 1 else None for r in range(n)]
+    x = rng.normal(0, 1.0, size=(n, v + 3)).astype(np.float32)
+    x[::2] *= 2.5  # peaked rows between the flat ones
+    xd, x = _dev(x, gpu, dtype)
+    xt, xn = xd[:, 1:1 + v], x[:, 1:1 + v]
+    d = ge.sampling.dist_batch(xt, params, [None if m is None else torch.from_numpy(m) for m in masks], hist)
+    d = d.cpu().numpy()
+    for r in range(n):
+        np.testing.assert_allclose(d[r], ora.dist(xn[r], params[r], masks[r], hist[r]), rtol=DIST_RTOL,
+                                   atol=1e-300, err_msg=f"{dtype} row {r}")
+
+
+def test_bf16_deep_rows_unaligned(ge, gpu):
+    """The split-row finish over bf16 rows that are not 16-byte aligned (its bf16 scalar-load instance), with masks and
+    penalty histories: tokens against the oracle on the widened values, and the finish took part."""
+    n, v = 16, 100003
+    x, params = _flat_rows(ge, n, v + 3, 17)
+    rng = np.random.default_rng(17)
+    P = ge.sampling.SamplingParams
+    params = [P(temperature=p.temperature, top_p=p.top_p, top_k=p.top_k, min_p=p.min_p, repetition_penalty=1.1,
+                frequency_penalty=0.2) for p in params]
+    masks = [rng.random(v) < 0.8 for _ in range(n)]
+    hist = [rng.integers(0, v, size=200) for _ in range(n)]
+    u = np.array([ora.uniform(4000 + r, 2) for r in range(n)], np.float64)
+    xd, xw = _dev(x, gpu, "bf16")
+    xt, xn = xd[:, 3:3 + v], xw[:, 3:3 + v]
+    got = ge.sampling.sample_ex(xt, params, None, None, [torch.from_numpy(m) for m in masks], history=hist,
+                                uniforms=u).tolist()
+    paths = ge._lib.handle(gpu.index, n, v).row_paths(n)
+    print(f"[bf16 deep] paths {np.bincount(paths, minlength=3).tolist()}", flush=True)
+    assert got == ora.sample(xn, params, None, None, masks, history=hist, uniforms=u)
+    assert (paths == ge._lib.PATH_DEEP).sum() >= 1, paths
 
 
 def test_determinism_and_batch_invariance_full_c3(ge, gpu):
