@@ -316,7 +316,11 @@ def run_sample(args, ge, torch, batch):
     for k in range(args.warmup):
         step(k)
     torch.cuda.synchronize()
+    step(0)  # (copy 0 last: the tokens and the finishing path of each of its rows)
+    torch.cuda.synchronize()
     gpu_tokens = sets[0]["toks"].cpu().tolist()
+    paths = np.bincount(h.row_paths(rows), minlength=3)
+    log(f"[bench] rows finished by the main pass / split-row finish / exact path: {paths.tolist()}")
     wall, ts = timed(step, args.steps, torch)
     log(f"[bench] region 1: {args.steps} steps in {wall * 1e3:.2f} ms; region 2: median {np.median(ts):.2f} us")
     # region 3: per-kernel durations from HIP events on the launch stream
@@ -332,7 +336,8 @@ def run_sample(args, ge, torch, batch):
     ceil = read_ceiling([s["x"] for s in sets], torch)
     thr = through_sample(args, ge, torch, batch, [s["x"] for s in sets], gpu_tokens) if args.through_sample else None
     return dict(wall=wall, ts=ts, per=per, dom=("main_kernel", per["main_kernel"]), copies=copies,
-                a_bytes=batch.bytes_per_row() * rows, units=rows, gpu_out=gpu_tokens, ceiling=ceil, through=thr)
+                a_bytes=batch.bytes_per_row() * rows, units=rows, gpu_out=gpu_tokens, ceiling=ceil, through=thr,
+                paths={"main": int(paths[0]), "split_row": int(paths[1]), "exact": int(paths[2])})
 
 
 def through_sample(args, ge, torch, batch, xs, want):
@@ -493,6 +498,8 @@ def bench_one(args, config):
         "end_to_end": {"step_us_wall": round(r["wall"] * 1e6 / steps, 3),
                        "hbm_frac": round(a / (r["wall"] / steps) / PEAK_HBM, 4)},
     }
+    if r.get("paths"):
+        result["row_paths"] = r["paths"]
     if r.get("through"):
         result["through_sample"] = r["through"]
     if r["ceiling"]:

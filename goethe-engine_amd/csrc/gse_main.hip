@@ -76,12 +76,14 @@ struct Shared {
   double etab[64];             // 2^(j / 64) for exp_nonpos
 };
 
-// A listed element as the stream writes it: the bits of z over the token (the resolve packs it into a sort key).
-__device__ __forceinline__ uint64_t raw_entry(float z, uint32_t tok) {
-  return ((uint64_t)__float_as_uint(z) << 32) | tok;
+// A listed element as the stream writes it: the bits of its x (the processed logit: penalties and mask applied) over the
+// token. The resolve packs it into the sort key of z = RN(x / T) (x itself when the row does not divide).
+__device__ __forceinline__ uint64_t raw_entry(float x, uint32_t tok) {
+  return ((uint64_t)__float_as_uint(x) << 32) | tok;
 }
-__device__ __forceinline__ uint64_t key_of_raw(uint64_t r) {
-  return pack(fkey(__uint_as_float((uint32_t)(r >> 32))), (uint32_t)r);
+__device__ __forceinline__ uint64_t key_of_raw(uint64_t r, bool divide, double Rd) {
+  const float x = __uint_as_float((uint32_t)(r >> 32));
+  return pack(fkey(divide ? div_exact(x, Rd) : x), (uint32_t)r);
 }
 
 __device__ __forceinline__ void lp_invalid(const ScanArgs &a, int row, int nlp) {
@@ -118,83 +120,9 @@ struct RowEval {
   const gse_row *P;
 };
 
-// Sorts the head sh.r.head[0, n) descending in place. Keys lie in [kappa, mk]: a counting sort over NBK buckets of
-// equal key width (count, scan, scatter), then each element's rank inside its bucket by counting; a bucket larger than
-// BKT (many equal or close keys) makes the whole head take a bitonic sort instead. Rolled loops: compact code.
+// Sorts the head sh.r.head[0, n) descending in place (keys in [kappa, mk]): the counting sort of sort_desc_counting.
 __device__ __forceinline__ void sort_head(Shared &sh, int n, uint32_t mk, uint32_t kappa) {
-  const int tid = threadIdx.x;
-  const uint32_t span = mk - kappa;
-  int shift = 0;
-  while ((span >> shift) >= (uint32_t)NBK) ++shift;
-  for (int b = tid; b < NBK; b += MT) sh.r.bcnt[b] = 0;
-  if (tid == 0) sh.bmax = 0;
-  __syncthreads();
-#pragma unroll 1
-  for (int i = tid; i < n; i += MT) atomicAdd(&sh.r.bcnt[(mk - pk_key(sh.r.head[i])) >> shift], 1u);
-  __syncthreads();
-  // bucket starts: NBK / MT buckets per thread, contiguous
-  constexpr int BPT = NBK / MT;
-  uint32_t c[BPT], loc = 0, mx = 0;
-#pragma unroll
-  for (int j = 0; j < BPT; ++j) {
-    c[j] = sh.r.bcnt[tid * BPT + j];
-    loc += c[j];
-    mx = max(mx, c[j]);
-  }
-  const uint32_t inc = wave_incl_scan_u32(loc);
-  mx = wave_max_u32(mx);
-  if (lane_id() == WAVE - 1) sh.wcnt[tid >> 6] = inc;
-  if (lane_id() == 0) atomicMax(&sh.bmax, mx);
-  __syncthreads();
-  uint32_t run = inc - loc;
-  for (int w = 0; w < NWV; ++w) run += w < (tid >> 6) ? sh.wcnt[w] : 0u;
-#pragma unroll
-  for (int j = 0; j < BPT; ++j) {
-    sh.r.bofs[tid * BPT + j] = run;
-    sh.r.bcnt[tid * BPT + j] = run;  // (the running end while scattering)
-    run += c[j];
-  }
-  __syncthreads();
-  if (sh.bmax <= (uint32_t)BKT) {
-#pragma unroll 1
-    for (int i = tid; i < n; i += MT) {
-      const uint64_t v = sh.r.head[i];
-      sh.r.tmp[atomicAdd(&sh.r.bcnt[(mk - pk_key(v)) >> shift], 1u)] = v;
-    }
-    __syncthreads();
-#pragma unroll 1
-    for (int i = tid; i < n; i += MT) {
-      const uint64_t v = sh.r.tmp[i];
-      const uint32_t b = (mk - pk_key(v)) >> shift;
-      const uint32_t b0 = sh.r.bofs[b], b1 = sh.r.bcnt[b];
-      uint32_t r = b0;
-#pragma unroll 1
-      for (uint32_t q = b0; q < b1; ++q) r += sh.r.tmp[q] > v ? 1u : 0u;
-      sh.r.head[r] = v;
-    }
-    __syncthreads();
-  } else {
-    int N = 2;
-    while (N < n) N <<= 1;
-    for (int i = n + tid; i < N; i += MT) sh.r.head[i] = 0ull;
-    __syncthreads();
-#pragma unroll 1
-    for (int k = 2; k <= N; k <<= 1) {
-#pragma unroll 1
-      for (int j = k >> 1; j > 0; j >>= 1) {
-#pragma unroll 1
-        for (int i = tid; i < N / 2; i += MT) {
-          const int lo = ((i & ~(j - 1)) << 1) | (i & (j - 1)), hi = lo + j;
-          const uint64_t x = sh.r.head[lo], y = sh.r.head[hi];
-          if ((lo & k) == 0 ? x < y : x > y) {
-            sh.r.head[lo] = y;
-            sh.r.head[hi] = x;
-          }
-        }
-        __syncthreads();
-      }
-    }
-  }
+  sort_desc_counting<NBK, BKT>(sh.r.head, sh.r.tmp, sh.r.bcnt, sh.r.bofs, sh.wcnt, &sh.bmax, n, mk, kappa);
 }
 
 // Decides the keep prefix, the draw and the logprobs over the sorted head arr[0, n) (the whole certified head).
@@ -401,6 +329,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
 
   // z = x / T: no finite z over the allowed tokens may still hide a finite x whose quotient overflowed
   const bool divide = !greedy && P.temperature != 1.0f;
+  const double Rd = 1.0 / (double)P.temperature;  // (the lists hold x; their keys are of z = RN(x / T))
   if (((flags & F_HOVER) && (greedy || bad)) ||
       (((flags & F_PINF) || (divide && !(flags & F_FINITE))) && !(flags & F_NAN))) {
     // more distinct history ids than a part can count, or a maximum of z that is not finite (the parts do not know
@@ -457,7 +386,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   // and its length is its cost.
   auto batch = [&](const uint64_t(&pk)[GPT], const bool(&ok)[GPT]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int g = 0; g < GPT; ++g) sh.r.tmp[g * MT + tid] = ok[g] ? key_of_raw(pk[g]) : 0ull;
+    for (int g = 0; g < GPT; ++g) sh.r.tmp[g * MT + tid] = ok[g] ? key_of_raw(pk[g], divide, Rd) : 0ull;
 #pragma unroll 1
     for (int g = 0; g < GPT; ++g) {
       const uint64_t v = sh.r.tmp[g * MT + tid];
@@ -583,18 +512,28 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
 // the listing is skipped for a whole chunk when the lane maxima lie below the threshold, and the unlisted terms are
 // summed in fp32 per chunk.
 
+// The stream works on x, the processed logit (-inf where the mask or the history exclusion removes the token), never on
+// z = RN(x / T): z is a monotone non-decreasing function of x (T > 0), so maxima and thresholds carry over (the maximum of
+// z is z of the maximum of x; every z above z(x_t) belongs to an x above x_t), and each unlisted term exp(z - R) comes
+// from one fma of x. Only the part maximum, a threshold and the listed elements are ever divided.
+//
 // Per-lane running state of a wave.
 struct Run {
-  float m;         // running maximum of this lane's z
-  double s;        // sum of this lane's unlisted exp(z - tau) (fp32 terms), tau the wave's threshold value
+  float m;         // running maximum of this lane's x
+  double s;        // sum of this lane's unlisted exp(z - R) (fp32 terms), R = z(xt) the wave's threshold in z
   double b;        // its error bound
-  uint32_t kap;    // the wave's listing threshold key (uniform in the wave; only rises)
-  float tau;       // its value: every element at or above it is listed, so every unlisted term is at most 1
+  uint32_t xkey;   // the wave's listing threshold as a key of x (uniform in the wave; only rises)
+  float xt;        // its value: every element with x >= xt is listed
+  float R;         // z(xt): every unlisted element has z <= R
+  float c1, c0;    // the exponent of an unlisted term: t = fma(x, c1, c0), (x / T - R) log2(e) rounded
+  double bR;       // the part of a term's error bound that grows with |R| (the roundings of z, c1 and c0)
+  uint32_t kcert;  // certified key of z: every element with key >= kcert is listed (fkey(R) + 1)
+  bool ovf;        // c0 out of the fp32 range: the part's sums cannot be trusted
   uint32_t woff;   // elements the wave has listed (uniform)
   uint32_t vnext;  // list length at which the valve next recomputes the threshold (uniform)
   float g;         // greedy rows: largest nan_to_num(x) so far, at the lowest token gid holding it
   uint32_t gid;
-  uint32_t fid;    // lowest token of this lane with z not NaN (found in the lane's first chunk)
+  uint32_t fid;    // lowest token of this lane with x not NaN (found in the lane's first chunk)
   uint64_t nanm;   // lanes that saw a NaN before the mask (wave-uniform)
 };
 
@@ -655,7 +594,8 @@ __device__ __forceinline__ void load_u(const RowCtx &c, const RowBufs &rb, int c
 }
 
 // The history words of a chunk's vectors (bit o of the part's history bitset = token p0 + o is in the row's history),
-// read from LDS with the chunk's loads, so that the read is done by the time the chunk is processed.
+// read from LDS with the chunk's loads, so that the read is done by the time the chunk is processed. Raw words: token k
+// of lane l's vector is bit (l VEC) % 32 + k (chunk starts lie 512 tokens apart from the part start, a multiple of 32).
 template <int DT>
 __device__ __forceinline__ void hist_words(const HistTab &h, int cb, int p0, int p1, uint32_t (&hw)[Lay<DT>::NV]) {
   using L = Lay<DT>;
@@ -663,15 +603,73 @@ __device__ __forceinline__ void hist_words(const HistTab &h, int cb, int p0, int
 #pragma unroll
   for (int v = 0; v < L::NV; ++v) {
     const int o = min(cb + v * L::STRIDE + l * L::VEC, p1 - 1) - p0;  // (a vector past the end reads a valid word)
-    hw[v] = h.bits[o >> 5] >> (o & 31);
+    hw[v] = h.bits[o >> 5];
   }
 }
 
-// z of one chunk in place: the mask and the history exclusion (-inf for tokens the stream does not carry; a select only
+// x of a full chunk (every token below the stream end) of a sampled row in place: the keep bits of each vector, mask AND
+// NOT history, from the raw words with one bit-field extract; the NaN flag; -inf where a token is not kept (no select
+// when the whole wave's chunk keeps everything); the lane's chunk maximum. The same results as chunk_z for such a chunk,
+// with the range tests and shifts of the general chunk left out.
+template <int DT, bool MASKED>
+__device__ __forceinline__ float chunk_x_full(const RowCtx &c, int cb, float (&xr)[EPL], const uint32_t (&mw)[Lay<DT>::NV],
+                                              const uint32_t (&hw)[Lay<DT>::NV], Run &rn, float *proc) {
+  using L = Lay<DT>;
+  constexpr uint32_t VMASK = (1u << L::VEC) - 1u;
+  const int l = lane_id();
+  const uint32_t sh = (uint32_t)(l * L::VEC) & 31u;
+  uint32_t keep[L::NV];
+  bool full = true;
+#pragma unroll
+  for (int v = 0; v < L::NV; ++v) {
+    uint32_t w = MASKED ? mw[v] : 0xFFFFFFFFu;
+    if (c.pen) w &= ~hw[v];
+    keep[v] = __builtin_amdgcn_ubfe(w, sh, (uint32_t)L::VEC);
+    full = full && keep[v] == VMASK;
+  }
+  if (proc) {  // processed logits (after penalties and mask, before T) of the streamed (non-history) tokens
+#pragma unroll
+    for (int v = 0; v < L::NV; ++v) {
+      const int t0 = cb + v * L::STRIDE + l * L::VEC;
+      const uint32_t al = MASKED ? __builtin_amdgcn_ubfe(mw[v], sh, (uint32_t)L::VEC) : VMASK;
+      const uint32_t hx = c.pen ? __builtin_amdgcn_ubfe(hw[v], sh, (uint32_t)L::VEC) : 0u;
+#pragma unroll
+      for (int k = 0; k < L::VEC; ++k)
+        if (!((hx >> k) & 1u)) proc[t0 + k] = keep_or_ninf(xr[v * L::VEC + k], al, k);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < EPL; i += 2) rn.nanm |= ballot64(__builtin_isunordered(xr[i], xr[i + 1]));  // (a NaN in either)
+  float cmax = -INFINITY;
+  if (ballot64(!full) == 0ull) {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) cmax = fmaxf(cmax, xr[i]);
+  } else {
+#pragma unroll
+    for (int v = 0; v < L::NV; ++v) {
+#pragma unroll
+      for (int k = 0; k < L::VEC; ++k) {
+        const int i = v * L::VEC + k;
+        xr[i] = keep_or_ninf(xr[i], keep[v], k);
+        cmax = fmaxf(cmax, xr[i]);
+      }
+    }
+  }
+  if (rn.fid == 0xFFFFFFFFu) {  // (only until the lane has seen a value that is not NaN)
+#pragma unroll
+    for (int i = EPL - 1; i >= 0; --i) {
+      const int t = cb + (i / L::VEC) * L::STRIDE + l * L::VEC + (i % L::VEC);
+      if (xr[i] == xr[i]) rn.fid = (uint32_t)t;
+    }
+  }
+  return cmax;
+}
+
+// x of one chunk in place: the mask and the history exclusion (-inf for tokens the stream does not carry; a select only
 // in chunks where some lane has such a token), the NaN flag (every loaded value is one of the row's own, so any NaN seen
-// is the row's), the division by T (div_exact), the lane's chunk maximum; greedy rows track the first maximum of
-// nan_to_num(x).
-template <int DT, bool AL, bool MASKED, bool GREEDY, bool DIV>
+// is the row's), the lane's chunk maximum; greedy rows track the first maximum of nan_to_num(x). hw holds the raw
+// history bitset words of the chunk's vectors (bit (l VEC) % 32 + k is token k of lane l's vector).
+template <int DT, bool AL, bool MASKED, bool GREEDY>
 __device__ __forceinline__ float chunk_z(const RowCtx &c, int cb, int p0, int pv, int p1, float (&xr)[EPL],
                                          const uint32_t (&mw)[Lay<DT>::NV], const uint32_t (&hw)[Lay<DT>::NV],
                                          Run &rn, float *proc) {
@@ -686,7 +684,7 @@ __device__ __forceinline__ float chunk_z(const RowCtx &c, int cb, int p0, int pv
     uint32_t in;
     if constexpr (AL) in = t0 + L::VEC <= pv ? VMASK : 0u;
     else in = t0 + L::VEC <= pv ? VMASK : (t0 >= pv ? 0u : (1u << (pv - t0)) - 1u);
-    if (c.pen) in &= ~hw[v];
+    if (c.pen) in &= ~(hw[v] >> ((l * L::VEC) & 31));
     inr[v] = in & VMASK;
     keep[v] = (MASKED ? (mw[v] >> ((l * L::VEC) & 31)) : VMASK) & inr[v];
     full = full && keep[v] == VMASK;
@@ -706,11 +704,7 @@ __device__ __forceinline__ float chunk_z(const RowCtx &c, int cb, int p0, int pv
   float cmax = -INFINITY;
   if (!GREEDY && ballot64(!full) == 0ull) {  // every token of the chunk is carried and allowed: no select
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      const float z = DIV ? div_exact(xr[i], c.Rd) : xr[i];
-      xr[i] = z;
-      cmax = fmaxf(cmax, z);
-    }
+    for (int i = 0; i < EPL; ++i) cmax = fmaxf(cmax, xr[i]);
   } else {
 #pragma unroll
     for (int v = 0; v < L::NV; ++v) {
@@ -726,9 +720,8 @@ __device__ __forceinline__ float chunk_z(const RowCtx &c, int cb, int p0, int pv
             rn.gid = (uint32_t)(t0 + k);
           }
         }
-        const float z = DIV ? div_exact(xm, c.Rd) : xm;
-        xr[i] = z;
-        cmax = fmaxf(cmax, z);
+        xr[i] = xm;
+        cmax = fmaxf(cmax, xm);
       }
     }
   }
@@ -756,49 +749,61 @@ __device__ __forceinline__ float pairwise(F &f) {
   }
 }
 
-// Raises the wave's threshold to kap (uniform) and rescales the lanes' sums to the new reference (fp64).
-__device__ __forceinline__ void set_tau(Run &rn, uint32_t kap) {
-  const float tnew = fkey_inv(kap);
-  if (rn.tau > -INFINITY && tnew > rn.tau) {
-    const double f = exp((double)rn.tau - (double)tnew);
+// Raises the wave's listing threshold to the x key k (uniform): xt = the value of k, R = z(xt), and the lanes' sums
+// rescaled to the new reference (fp64). c0 = RN(-R log2(e)); an R whose c0 leaves the fp32 range (|R| > 2.3e38) marks
+// the part (its row takes the split-row finish or the exact path). An R of -inf leaves only -inf elements unlisted, of
+// mass 0: c0 = -inf gives them exp2(-256) = 0.
+__device__ __forceinline__ void set_threshold(Run &rn, uint32_t k, bool divide, double Rd) {
+  const float xt = fkey_inv(k);
+  const float R = divide ? div_exact(xt, Rd) : xt;
+  if (rn.R > -INFINITY && R > rn.R) {
+    const double f = exp((double)rn.R - (double)R);
     rn.s *= f;
     rn.b *= f;
   }
-  rn.kap = kap;
-  rn.tau = tnew;
+  const double cr = -(double)R * 1.4426950408889634;
+  const bool fin = fabsf(R) < INFINITY;
+  rn.ovf = rn.ovf || (fin && !(fabs(cr) <= 3.4028234663852886e38));
+  rn.c0 = fin && fabs(cr) <= 3.4028234663852886e38 ? (float)cr : -INFINITY;
+  rn.bR = fin ? 1.8e-7 * fabs((double)R) : 0.0;
+  rn.xkey = k;
+  rn.xt = xt;
+  rn.R = R;
+  rn.kcert = fkey(R) + 1u;
 }
 
-// The lane maximum, the threshold valve, the unlisted terms exp2(t), t = (z - tau) log2(e) (fp32 per chunk, fp64
-// across chunks; z < tau for every unlisted element, so t < 0), the listing. tok(i) gives the token of slot i.
+// The lane maximum, the threshold valve, the unlisted terms exp2(t), t = fma(x, c1, c0) = (x / T - R) log2(e) rounded
+// (fp32 per chunk, fp64 across chunks; x < xt for every unlisted element, so z <= R and t <= 0 up to rounding), the
+// listing of the elements with x >= xt. tok(i) gives the token of slot i.
 template <int N, typename Tok>
-__device__ __forceinline__ void chunk_sum(const ScanArgs &a, int row, int wl, float cmax, const float (&zr)[N],
-                                          Run &rn, Tok tok) {
+__device__ __forceinline__ void chunk_sum(const ScanArgs &a, int row, int wl, float cmax, const float (&xr)[N],
+                                          Run &rn, Tok tok, bool divide, double Rd) {
   static_assert((N & (N - 1)) == 0 && N <= 256, "");
   rn.m = fmaxf(rn.m, cmax);
   if (rn.woff >= rn.vnext) {  // (again after every KV / 2 more listed elements)
-    const uint32_t k = max(rn.kap, wave_kth_largest_u16(fkey(rn.m) >> 16, KV) << 16);
-    if (k > rn.kap) set_tau(rn, k);
+    const uint32_t k = max(rn.xkey, wave_kth_largest_u16(fkey(rn.m) >> 16, KV) << 16);
+    if (k > rn.xkey) set_threshold(rn, k, divide, Rd);
     rn.vnext = rn.woff + KV / 2;
   }
-  const float tauf = rn.tau;
-  // -inf (masked, excluded) gives t = -256 and e = 0
+  const float xt = rn.xt, c1 = rn.c1, c0 = rn.c0;
+  // -inf (masked, excluded) gives t = -256 and e = 0; a NaN x gives t = -256 too (the NaN flag is kept apart)
   float e[N], t[N];
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    t[i] = fmaxf((zr[i] - tauf) * LOG2E, -256.0f);
+    t[i] = fmaxf(fmaf(xr[i], c1, c0), -256.0f);
     e[i] = __builtin_amdgcn_exp2f(t[i]);
   }
-  if (ballot64(cmax >= tauf)) {  // some lane holds an element at or above the threshold: list them (they leave the sum)
+  if (ballot64(cmax >= xt)) {  // some lane holds an element at or above the threshold: list them (they leave the sum)
     uint64_t *cl = a.cand + ((size_t)row * a.nparts * PWAVES + wl) * CAPW;
     uint32_t woff = rn.woff;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      const bool p = zr[i] >= tauf;
+      const bool p = xr[i] >= xt;
       const uint64_t bl = ballot64(p);
       if (bl) {
         if (p) {
           const uint32_t pos = woff + lanes_below(bl);
-          if (pos < (uint32_t)CAPW) st_ag(&cl[pos], raw_entry(zr[i], tok(i)));
+          if (pos < (uint32_t)CAPW) st_ag(&cl[pos], raw_entry(xr[i], tok(i)));
           e[i] = 0.0f;
           t[i] = 0.0f;
         }
@@ -812,18 +817,19 @@ __device__ __forceinline__ void chunk_sum(const ScanArgs &a, int row, int wl, fl
   for (int i = 0; i < N; ++i) mom = fmaf(e[i], t[i], mom);
   auto term = [&](auto ic) __attribute__((always_inline)) { return e[decltype(ic)::value]; };
   const float s = pairwise<0, N>(term);
-  // error bound: v_exp_f32 (2 ulp), log2(N) fp32 pairwise additions, flushed subnormal results; the exponent's
-  // roundings (z - tau exact or rounded once, the product by log2(e) rounded, log2(e) rounded: 3 ulp of |t|, times
-  // ln 2; mom = -sum e |t|)
+  // error bound, relative to the terms: v_exp_f32 (2 ulp), log2(N) fp32 pairwise additions, flushed subnormal results;
+  // the exponent's roundings: z = RN(x / T) against x / T, c1 = RN(log2(e) / T) and c0 = RN(-R log2(e)) (each 2^-24
+  // relative: 2^-24 log2(e) (2 |x / T| + |R|) <= 2^-24 (4.33 |R| + 2 |t|), since |x / T| <= |R| + |t| ln 2), the fma's
+  // own rounding (2^-24 |t|): times ln 2, 1.8e-7 |R| (bR) + 1.25e-7 |t| (mom = -sum e |t|)
   constexpr double LV = N >= 16 ? 4.0 : N >= 8 ? 3.0 : N >= 4 ? 2.0 : 1.0;
   rn.s += (double)s;
-  rn.b += (double)s * (2.4e-7 + LV * 6.0e-8 + 5e-8) - (double)mom * 1.25e-7 + 1e-36;
+  rn.b += (double)s * (2.4e-7 + LV * 6.0e-8 + 5e-8 + rn.bR) - (double)mom * 1.25e-7 + 1e-36;
 }
 
 // Tokens outside the stream (history tokens with their counts, ragged tokens with count 0; tok < 0: empty slot), with
 // their logits x0 and mask bits al: penalties, NaN test, mask, z, then the same running state as the stream (tokens out
 // of order: ties go to the lower id). Every thread of the wave takes part, with empty slots where it has no token.
-template <int N, bool GREEDY, bool DIV>
+template <int N, bool GREEDY>
 __device__ __forceinline__ void side_tokens(const ScanArgs &a, const RowCtx &c, int row, int wl,
                                             bool listing, const int (&tk)[N], const uint32_t (&cnt)[N],
                                             const float (&x0)[N], const bool (&al)[N], Run &rn, float *proc) {
@@ -847,12 +853,12 @@ __device__ __forceinline__ void side_tokens(const ScanArgs &a, const RowCtx &c, 
           rn.gid = t;
         }
       }
-      xr[k] = DIV ? div_exact(xm, c.Rd) : xm;
-      cmax = fmaxf(cmax, xr[k]);
+      xr[k] = xm;
+      cmax = fmaxf(cmax, xm);
     }
   }
   rn.nanm |= ballot64(hnan);
-  if (listing) chunk_sum<N>(a, row, wl, cmax, xr, rn, [&](int i) { return (uint32_t)tk[i]; });
+  if (listing) chunk_sum<N>(a, row, wl, cmax, xr, rn, [&](int i) { return (uint32_t)tk[i]; }, c.divide, c.Rd);
   else rn.m = fmaxf(rn.m, cmax);
 }
 
@@ -890,9 +896,6 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   // most 2^21 tokens): its buffer loads fail the range check and return zeros without a memory access (unaligned rows
   // clamp to the part instead), so the loads a wave issues ahead of its last chunk fetch nothing.
   const auto cst = [&](int ck) -> int { return ck < nck ? p0 + ck * CHK : (1 << 28); };
-  load_u<DT, AL, MASKED>(c, rbuf, cst(c0), pv, p1, xa, ma);
-  load_u<DT, AL, MASKED>(c, rbuf, cst(c1), pv, p1, xb, mb);
-  load_u<DT, AL, MASKED>(c, rbuf, cst(c3), pv, p1, xd, md);
   // allowed tokens of the part's stream range (masked rows: popcounts of its mask words, every load issued before the
   // first is used; the sum comes after the history build)
   constexpr int APW = (PTOK / 32 + MT - 1) / MT;  // mask words per thread
@@ -905,6 +908,16 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
 #pragma unroll
     for (int k = 0; k < APW; ++k) mwd[k] = c.mw[(p0 >> 5) + max(min(tid + k * MT, nmw - 1), 0)];
   }
+  // The first chunks' loads go out once the history ids are in: issued with them, they queued behind every workgroup's
+  // first chunks (about 40 MB over the device at C3) and the ids, the history build and the first chunk's processing
+  // waited for them (C3: ids in at 6-8 us, first chunk processed at 15-17 us); issued after them, they stream in while
+  // the history tables are built.
+  if (c.pen) asm volatile("" ::"v"(hid[0]), "v"(hid[1]), "v"(hid[2]), "v"(hid[3]), "v"(hid[4]), "v"(hid[5]),
+                          "v"(hid[6]), "v"(hid[7]));
+  static_assert(HPT == 8, "");
+  load_u<DT, AL, MASKED>(c, rbuf, cst(c0), pv, p1, xa, ma);
+  load_u<DT, AL, MASKED>(c, rbuf, cst(c1), pv, p1, xb, mb);
+  load_u<DT, AL, MASKED>(c, rbuf, cst(c3), pv, p1, xd, md);
   if (tid == 0) sh.hover = 0;
   if (c.pen) build_history(c, a.hist, hid, p0, p1, sh.h, sh.wcnt, sh.hover);
   else __syncthreads();
@@ -948,8 +961,14 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   rn.m = -INFINITY;
   rn.s = 0.0;
   rn.b = 0.0;
-  rn.kap = 0;
-  rn.tau = -INFINITY;
+  rn.xkey = 0;
+  rn.xt = -INFINITY;
+  rn.R = -INFINITY;
+  rn.c1 = DIV ? (float)(1.4426950408889634 * c.Rd) : LOG2E;  // RN(log2(e) / T)
+  rn.c0 = -INFINITY;
+  rn.bR = 0.0;
+  rn.kcert = 0;
+  rn.ovf = false;
   rn.woff = 0;
   rn.vnext = CAPW / 4 + 1;
   rn.g = -INFINITY;
@@ -968,7 +987,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   };
   // First chunk of each wave; the part's listing threshold from the 256 lane maxima.
   float cmax = -INFINITY;
-  if (c0 < nck) cmax = chunk_z<DT, AL, MASKED, GREEDY, DIV>(c, p0 + c0 * CHK, p0, pv, p1, xa, ma, ha, rn, proc);
+  if (c0 < nck) cmax = chunk_z<DT, AL, MASKED, GREEDY>(c, p0 + c0 * CHK, p0, pv, p1, xa, ma, ha, rn, proc);
   if (listing) {
     // The listing threshold: the rank-kp largest of the 256 lane maxima of the waves' first chunks (a 2048-token
     // sample). kp is scaled so that about T tokens of the part lie above it: kp = T * (allowed tokens in the sample) /
@@ -995,7 +1014,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     }
     const uint32_t T = P.top_k > 0 ? min(2u * KT, (uint32_t)(3 * max(P.top_k, nlp_of(a, P)) + 32)) : (uint32_t)KT;
     // (a sample with few allowed tokens estimates nothing: then the lowest lane maximum, and the valve bounds the lists)
-    const uint32_t kp = As < 16u ? max(act, 1u) : max(1u, min(act, (uint32_t)(((uint64_t)T * As + Ap - 1) / max(Ap, 1u))));
+    const uint32_t kp = As < 16u ? max(act, 1u) : max(1u, min(act, (T * As + Ap - 1) / max(Ap, 1u)));  // (T As < 2^20)
     uint32_t r = 0;
 #pragma unroll
     for (int b = 15; b >= 0; --b) {
@@ -1005,7 +1024,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
       for (int q = 0; q < NWV; ++q) cnt += (uint32_t)__popcll(ballot64(sh.lmax[q * WAVE + lane] >= cand));
       if ((int)cnt >= (int)kp) r = cand;
     }
-    set_tau(rn, max(r << 16, KEY_NEGINF + 1u));
+    set_threshold(rn, max(r << 16, KEY_NEGINF + 1u), DIV, c.Rd);
   }
   int c2 = grab();
   load_u<DT, AL, MASKED>(c, rbuf, cst(c2), pv, p1, xc, mcw);
@@ -1022,15 +1041,20 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     }
   }
   if (c0 < nck) {
-    if (listing) chunk_sum<EPL>(a, row, wl, cmax, xa, rn, tok_of(p0 + c0 * CHK));
+    if (listing) chunk_sum<EPL>(a, row, wl, cmax, xa, rn, tok_of(p0 + c0 * CHK), DIV, c.Rd);
     else rn.m = fmaxf(rn.m, cmax);
   }
   // Steady state: three chunks loading while the wave works on a fourth (chunk indices rise, so the first past the end
   // ends the wave's stream). In processing order: b, d, c, a, b, d, ... (a was processed above).
   auto step = [&](int ck, float(&x)[EPL], const uint32_t(&mw)[L::NV], const uint32_t(&hw)[L::NV])
                   __attribute__((always_inline)) {
-    const float cm = chunk_z<DT, AL, MASKED, GREEDY, DIV>(c, p0 + ck * CHK, p0, pv, p1, x, mw, hw, rn, proc);
-    if (listing) chunk_sum<EPL>(a, row, wl, cm, x, rn, tok_of(p0 + ck * CHK));
+    float cm;
+    if (!GREEDY && AL && p0 + (ck + 1) * CHK <= pv) {  // a full chunk (uniform): the lean path
+      cm = chunk_x_full<DT, MASKED>(c, p0 + ck * CHK, x, mw, hw, rn, proc);
+    } else {
+      cm = chunk_z<DT, AL, MASKED, GREEDY>(c, p0 + ck * CHK, p0, pv, p1, x, mw, hw, rn, proc);
+    }
+    if (listing) chunk_sum<EPL>(a, row, wl, cm, x, rn, tok_of(p0 + ck * CHK), DIV, c.Rd);
     else rn.m = fmaxf(rn.m, cm);
   };
   // (c2 was issued above; c3 before the history build: processing order c1, c3, c2, then the next grabs)
@@ -1078,7 +1102,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
         al[k] = tk[k] >= 0 && mask_bit(c, tk[k]);
       }
     }
-    side_tokens<KH, GREEDY, DIV>(a, c, row, wl, listing, tk, cn, x0, al, rn, proc);
+    side_tokens<KH, GREEDY>(a, c, row, wl, listing, tk, cn, x0, al, rn, proc);
   }
   if (AL && pv < p1 && w == 0) {  // (uniform: at most VEC - 1 tokens, wave 0)
     const int t = pv + lane;
@@ -1090,10 +1114,10 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     }
     const float x0[1] = {tk[0] >= 0 ? load_one(c, tk[0]) : 0.0f};
     const bool al[1] = {tk[0] >= 0 && mask_bit(c, tk[0])};
-    side_tokens<1, GREEDY, DIV>(a, c, row, wl, listing, tk, cn, x0, al, rn, proc);
+    side_tokens<1, GREEDY>(a, c, row, wl, listing, tk, cn, x0, al, rn, proc);
   }
 
-  // Part record: the part maximum, then every lane's sum rescaled to it (fp64, fixed order).
+  // Part record: the part maximum of z (z of the maximum of x), then every lane's sum rescaled to it (fp64, fixed order).
   const float wm = wave_max_f32(rn.m);
   uint64_t top;
   if (GREEDY) {
@@ -1104,18 +1128,19 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   top = wave_max_u64(top);
   if (lane == 0) {
     sh.wmax[w] = wm;
-    sh.wflags[w] = rn.nanm ? F_NAN : 0u;
+    sh.wflags[w] = (rn.nanm ? F_NAN : 0u) | (rn.ovf ? F_OVERFLOW : 0u);  // (rn.ovf is wave-uniform)
     sh.wtop[w] = top;
-    sh.wkap[w] = rn.kap;
+    sh.wkap[w] = rn.kcert;
     sh.wcnt[w] = rn.woff;
   }
   __syncthreads();
-  float M = sh.wmax[0];
+  float Mx = sh.wmax[0];
 #pragma unroll
-  for (int k = 1; k < NWV; ++k) M = fmaxf(M, sh.wmax[k]);
+  for (int k = 1; k < NWV; ++k) Mx = fmaxf(Mx, sh.wmax[k]);
+  const float M = DIV ? div_exact(Mx, c.Rd) : Mx;
   double s = 0.0, b = 0.0;
-  if (rn.tau > -INFINITY && fabsf(M) < INFINITY) {  // the lane's sum, relative to its wave's threshold, to M
-    const double f = exp((double)rn.tau - (double)M);
+  if (rn.R > -INFINITY && fabsf(M) < INFINITY) {  // the lane's sum, relative to its wave's threshold R, to M
+    const double f = exp((double)rn.R - (double)M);
     s = rn.s * f;
     b = rn.b * f;
   }

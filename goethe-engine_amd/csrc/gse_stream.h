@@ -232,6 +232,91 @@ __device__ __forceinline__ void sort_regs(uint64_t (&v)[S], uint64_t *buf) {
   }
 }
 
+// Sorts a[0, n) (packed keys, descending: key desc, then token id asc) in place, every key in [klo, khi], by the whole
+// workgroup (MT threads): a counting sort over NB buckets of equal key width (count, scan, scatter into tmp), then each
+// element's rank inside its bucket by counting; a bucket larger than BK (many equal or close keys) makes the whole array
+// take a bitonic sort instead. a and tmp hold at least pow2_ceil(n) entries, bcnt and bofs NB; wsum NWV words, bmax one
+// word of scratch. Rolled loops: compact code (this runs once per row, from a cold instruction cache). Ends with a
+// barrier.
+template <int NB, int BK>
+__device__ __forceinline__ void sort_desc_counting(uint64_t *a, uint64_t *tmp, uint32_t *bcnt, uint32_t *bofs,
+                                                   uint32_t *wsum, uint32_t *bmax, int n, uint32_t khi, uint32_t klo) {
+  static_assert(NB % MT == 0, "");
+  const int tid = threadIdx.x;
+  const uint32_t span = khi - klo;
+  int shift = 0;
+  while ((span >> shift) >= (uint32_t)NB) ++shift;
+  for (int b = tid; b < NB; b += MT) bcnt[b] = 0;
+  if (tid == 0) *bmax = 0;
+  __syncthreads();
+#pragma unroll 1
+  for (int i = tid; i < n; i += MT) atomicAdd(&bcnt[(khi - pk_key(a[i])) >> shift], 1u);
+  __syncthreads();
+  // bucket starts: NB / MT buckets per thread, contiguous
+  constexpr int BPT = NB / MT;
+  uint32_t c[BPT], loc = 0, mx = 0;
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    c[j] = bcnt[tid * BPT + j];
+    loc += c[j];
+    mx = max(mx, c[j]);
+  }
+  const uint32_t inc = wave_incl_scan_u32(loc);
+  mx = wave_max_u32(mx);
+  if (lane_id() == WAVE - 1) wsum[tid >> 6] = inc;
+  if (lane_id() == 0) atomicMax(bmax, mx);
+  __syncthreads();
+  uint32_t run = inc - loc;
+  for (int w = 0; w < NWV; ++w) run += w < (tid >> 6) ? wsum[w] : 0u;
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    bofs[tid * BPT + j] = run;
+    bcnt[tid * BPT + j] = run;  // (the running end while scattering)
+    run += c[j];
+  }
+  __syncthreads();
+  if (*bmax <= (uint32_t)BK) {
+#pragma unroll 1
+    for (int i = tid; i < n; i += MT) {
+      const uint64_t v = a[i];
+      tmp[atomicAdd(&bcnt[(khi - pk_key(v)) >> shift], 1u)] = v;
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int i = tid; i < n; i += MT) {
+      const uint64_t v = tmp[i];
+      const uint32_t b = (khi - pk_key(v)) >> shift;
+      const uint32_t b0 = bofs[b], b1 = bcnt[b];
+      uint32_t r = b0;
+#pragma unroll 1
+      for (uint32_t q = b0; q < b1; ++q) r += tmp[q] > v ? 1u : 0u;
+      a[r] = v;
+    }
+    __syncthreads();
+  } else {
+    int N = 2;
+    while (N < n) N <<= 1;
+    for (int i = n + tid; i < N; i += MT) a[i] = 0ull;
+    __syncthreads();
+#pragma unroll 1
+    for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll 1
+      for (int j = k >> 1; j > 0; j >>= 1) {
+#pragma unroll 1
+        for (int i = tid; i < N / 2; i += MT) {
+          const int lo = ((i & ~(j - 1)) << 1) | (i & (j - 1)), hi = lo + j;
+          const uint64_t x = a[lo], y = a[hi];
+          if ((lo & k) == 0 ? x < y : x > y) {
+            a[lo] = y;
+            a[hi] = x;
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
+}
+
 // An all-ones mask word: what unmasked rows read in place of their mask words in load_full.
 static __device__ const uint32_t ONES_WORD[1] = {0xFFFFFFFFu};
 
