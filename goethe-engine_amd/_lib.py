@@ -26,6 +26,7 @@ BATCH_EXACT = 1
 BATCH_PROFILE = 2
 BATCH_NO_PLAN_WAIT = 4
 BATCH_NO_SPLIT = 8  # (ABI 1.3)
+BATCH_SUBBIN_FINISH = 16  # (ABI 1.4, testing)
 MAX_LOGPROBS = 64
 P_ = C.POINTER
 

@@ -197,6 +197,7 @@ gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   a.xcd_map = 1;
   a.force_exact = (b.flags & GSE_BATCH_EXACT) ? 1 : 0;
   a.plan_wait = (b.flags & GSE_BATCH_NO_PLAN_WAIT) ? 0u : 400000u;  // 4 ms: only a grid the device cannot hold waits it out
+  a.fin_sorted = (b.flags & GSE_BATCH_SUBBIN_FINISH) ? 0 : 1;
   a.params = b.params;
   a.mask = b.mask;
   a.mask_ld = b.mask_ld;

@@ -706,6 +706,251 @@ __device__ __noinline__ void finish_row(const FinArgs a, DeepSlot *ds, FinShared
   }
 }
 
+// The finish of a window list of at most LC entries, sorted whole. The entries stay in registers (SP per thread) and
+// are ranked with a counting sort: FB key buckets per window (the draw window's entries rank above the cut window's),
+// an atomic slot in its bucket for every entry, the buckets' starts, a scatter into bucket order, and the rank inside
+// the bucket by counting its greater members (buckets hold a few entries). Every entry's exact mass then goes to its
+// rank, one exclusive scan in rank order (thread t: ranks [SP t, SP t + SP)) gives every prefix, and the keep cut (the
+// first entry not kept) and the draw (the first entry whose inclusive prefix reaches u c_last) are one test per rank
+// and one block minimum each. The unlisted region between the windows (X1, c1 elements) counts before the cut
+// window's entries. The tests and fixed-point sums are finish_row's; a failed check leaves the row to the exact path.
+constexpr int FB = 1024;  // key buckets per window
+static_assert(2 * 2 * FB * sizeof(uint32_t) <= SUBC * sizeof(uint64_t), "bucket counts and starts live in sub");
+static_assert(SUBC >= LC, "masses by rank live in sub");
+
+__device__ __noinline__ void finish_sorted(const FinArgs a, DeepSlot *ds, FinShared &sh, const double *etab, int n) {
+  constexpr int SP = LC / MT;  // entries (and ranks) per thread
+  const int tid = threadIdx.x, w = tid >> 6;
+  const gse_row &P = ds->P;
+  const int row = ds->row;
+  const float Mf = ds->M;
+  const double M = (double)Mf;
+  const uint32_t w2hi = ld_ag(&ds->w2hi), w1lo = ld_ag(&ds->w1lo);
+  const bool sep = w1lo > w2hi;
+  uint64_t v[SP];  // the thread's entries (list order), every load issued before the first is used
+#pragma unroll
+  for (int j = 0; j < SP; ++j) v[j] = j * MT + tid < n ? ld_ag(&a.lst[j * MT + tid]) : 0ull;
+  uint32_t *bcnt = reinterpret_cast<uint32_t *>(sh.sub), *bofs = bcnt + 2 * FB;
+  double *msr = reinterpret_cast<double *>(sh.sub);  // (after the ranks: the masses by rank)
+  for (int b = tid; b < 2 * FB; b += MT) bcnt[b] = 0;
+  if (tid < 2) sh.q[tid] = NONE;
+  // each entry's window and the key range of each window (per-wave ranges in wred / wred2, no atomics)
+  uint32_t gm = 0, kx0 = 0, kx1 = 0, kn0 = NONE, kn1 = NONE;
+#pragma unroll
+  for (int j = 0; j < SP; ++j) {
+    if (j * MT + tid < n) {
+      const uint32_t k = pk_key(v[j]);
+      if (sep && dbin(fkey_inv(k), Mf) >= w1lo) {
+        gm |= 1u << j;
+        kx1 = max(kx1, k);
+        kn1 = min(kn1, k);
+      } else {
+        kx0 = max(kx0, k);
+        kn0 = min(kn0, k);
+      }
+    }
+  }
+  kx0 = wave_max_u32(kx0);
+  kx1 = wave_max_u32(kx1);
+  kn0 = wave_min_u32(kn0);
+  kn1 = wave_min_u32(kn1);
+  if (lane_id() == 0) {
+    sh.wred[w] = (uint64_t)kx1 << 32 | kx0;
+    sh.wred2[w] = (uint64_t)kn1 << 32 | kn0;
+  }
+  __syncthreads();
+  uint32_t top[2] = {0u, 0u}, sft[2];
+  {
+    uint32_t lo[2] = {NONE, NONE};
+    for (int k = 0; k < NWV; ++k) {
+      top[0] = max(top[0], (uint32_t)sh.wred[k]);
+      top[1] = max(top[1], (uint32_t)(sh.wred[k] >> 32));
+      lo[0] = min(lo[0], (uint32_t)sh.wred2[k]);
+      lo[1] = min(lo[1], (uint32_t)(sh.wred2[k] >> 32));
+    }
+    for (int g = 0; g < 2; ++g) {
+      const uint32_t span = top[g] >= lo[g] ? top[g] - lo[g] : 0u;
+      uint32_t s = 0;
+      while (s < 31 && (span >> s) >= (uint32_t)FB) ++s;
+      sft[g] = s;
+    }
+  }
+  // bucket and slot of every entry; its exact mass (the table loads overlap the LDS atomics)
+  uint32_t bk[SP], sl[SP];
+  double m[SP];
+#pragma unroll
+  for (int j = 0; j < SP; ++j) {
+    bk[j] = 0;
+    sl[j] = 0;
+    m[j] = 0.0;
+    if (j * MT + tid < n) {
+      const uint32_t k = pk_key(v[j]);
+      const int g = (gm >> j) & 1;
+      bk[j] = g * FB + min((top[g] - k) >> sft[g], (uint32_t)(FB - 1));
+      sl[j] = atomicAdd(&bcnt[bk[j]], 1u);
+      m[j] = exp_nonpos((double)fkey_inv(k) - M, etab);
+    }
+  }
+  __syncthreads();
+  // bucket starts: thread t owns buckets [8 t, 8 t + 8)
+  {
+    constexpr int BT = 2 * FB / MT;
+    uint32_t c[BT], loc = 0;
+#pragma unroll
+    for (int j = 0; j < BT; ++j) {
+      c[j] = bcnt[tid * BT + j];
+      loc += c[j];
+    }
+    const uint32_t inc = wave_incl_scan_u32(loc);
+    if (lane_id() == WAVE - 1) sh.wsum[w] = inc;
+    __syncthreads();
+    uint32_t run = inc - loc;
+    for (int k = 0; k < NWV; ++k) run += k < w ? sh.wsum[k] : 0u;
+#pragma unroll
+    for (int j = 0; j < BT; ++j) {
+      bofs[tid * BT + j] = run;
+      run += c[j];
+    }
+  }
+  __syncthreads();
+  const uint32_t n0 = bofs[FB];  // entries of the draw window (they rank first)
+#pragma unroll
+  for (int j = 0; j < SP; ++j)
+    if (j * MT + tid < n) sh.lc[bofs[bk[j]] + sl[j]] = v[j];
+  __syncthreads();
+  // rank = bucket start + greater members of the bucket
+  uint32_t rk[SP];
+#pragma unroll
+  for (int j = 0; j < SP; ++j) {
+    rk[j] = 0;
+    if (j * MT + tid < n) {
+      const uint32_t b0 = bofs[bk[j]], b1 = b0 + bcnt[bk[j]];
+      uint32_t r = b0;
+#pragma unroll 1
+      for (uint32_t q = b0; q < b1; ++q) r += sh.lc[q] > v[j] ? 1u : 0u;
+      rk[j] = r;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < SP; ++j) {
+    if (j * MT + tid < n) {
+      sh.lc[rk[j]] = v[j];
+      msr[rk[j]] = m[j];
+    }
+  }
+  __syncthreads();
+  // exclusive prefix at rank SP t (one block scan of the fixed-point masses)
+  const int r0 = tid * SP;
+  uint64_t hi = 0, lo = 0;
+#pragma unroll
+  for (int s = 0; s < SP; ++s) {
+    if (r0 + s < n) {
+      const Fx f = fx_of(msr[r0 + s]);
+      hi += f.hi;
+      lo += f.lo;
+    }
+  }
+  const Fx X0{ld_ag(&ds->acc[DA_X0HI]), ld_ag(&ds->acc[DA_X0LO])}, X1{ld_ag(&ds->acc[DA_X1HI]), ld_ag(&ds->acc[DA_X1LO])};
+  const Fx SF = fx_add(fx_add(X0, X1), Fx{ld_ag(&ds->acc[DA_RHI]), ld_ag(&ds->acc[DA_RLO])});
+  const uint64_t c0 = ld_ag(&ds->acc[DA_C0]), c1 = ld_ag(&ds->acc[DA_C1]), tail = ld_ag(&ds->acc[DA_C2]);
+  const uint64_t cmax = a.info[row].cmax;  // (written by the main pass; used at the end)
+  const double Sd = fx_val(SF);
+  {
+    const uint64_t ih = wave_incl_scan_u64(hi), il = wave_incl_scan_u64(lo);
+    if (lane_id() == WAVE - 1) {
+      sh.wred[w] = ih;
+      sh.wred2[w] = il;
+    }
+    __syncthreads();
+    uint64_t ph = ih - hi, pl = il - lo, th = 0, tl = 0;
+    for (int k = 0; k < NWV; ++k) {
+      ph += k < w ? sh.wred[k] : 0ull;
+      pl += k < w ? sh.wred2[k] : 0ull;
+      th += sh.wred[k];
+      tl += sh.wred2[k];
+    }
+    hi = ph;  // (now the exclusive prefix at rank r0)
+    lo = pl;
+    sh.pub[0] = th;  // (the same value from every thread)
+    sh.pub[1] = tl;
+  }
+  const uint64_t K = P.top_k > 0 ? (uint64_t)P.top_k : ~0ull;
+  const double topp = P.top_p, minp = P.min_p, q0 = 1.0 / Sd;
+  // the first entry that is not kept (sampling.py:80, with min-p); the thread holding it publishes its exclusive prefix
+  // (the inclusive prefix of the last kept entry)
+  {
+    Fx A = fx_add(X0, Fx{hi, lo});
+    uint32_t fc = NONE;
+#pragma unroll 1
+    for (int s = 0; s < SP && r0 + s < n; ++s) {
+      const uint32_t r = (uint32_t)(r0 + s);
+      const bool g1 = r >= n0;
+      const Fx Ar = g1 ? fx_add(A, X1) : A, f = fx_of(msr[r]);
+      if (c0 + r + (g1 ? c1 : 0ull) >= K || (minp > 0.0 && !(fx_val(f) / Sd >= minp * q0)) ||
+          fx_val(Ar) / Sd >= topp) {
+        fc = r;
+        sh.shi[tid] = Ar.hi;
+        sh.slo[tid] = Ar.lo;
+        break;
+      }
+      A = fx_add(A, f);
+    }
+    fc = wave_min_u32(fc);
+    if (lane_id() == 0 && fc != NONE) atomicMin(&sh.q[0], fc);
+  }
+  __syncthreads();
+  const uint32_t fc = sh.q[0];
+  const int last = fc == NONE ? n - 1 : (int)fc - 1;  // the last kept entry
+  const bool glast = last >= 0 && (uint32_t)last >= n0;
+  bool ok = n > 0 && Sd > 0.0 && last >= 0;
+  Fx Al{0, 0};  // c_last, unnormalized
+  if (fc != NONE) {
+    Al = Fx{sh.shi[fc / SP], sh.slo[fc / SP]};
+    ok = ok && !(fc >= n0 && !glast && c1 > 0);  // (the first cut entry right after the gap: the cut may be inside it)
+  } else {
+    Al = fx_add(fx_add(X0, Fx{sh.pub[0], sh.pub[1]}), glast ? X1 : Fx{0, 0});
+    const uint64_t rl = c0 + (uint64_t)last + (glast ? c1 : 0ull);
+    const uint64_t after = (!sep || glast) ? tail : c1 + tail;  // unlisted elements ranked after the list
+    ok = ok && (after == 0 || rl + 1 >= K || fx_val(Al) / Sd >= topp);
+  }
+  const double clast = fx_val(Al) / Sd;
+  if (ok && a.mode == MODE_SAMPLE) {
+    // the draw: the first kept entry whose inclusive prefix reaches u c_last; its exclusive prefix must lie below it
+    // (else the draw falls in an unlisted region: before the list, or in the gap). Packed as rank << 1 | (not below).
+    const double thr = ds->u * clast;
+    Fx A = fx_add(X0, Fx{hi, lo});
+    uint32_t fj = NONE;
+#pragma unroll 1
+    for (int s = 0; s < SP && r0 + s <= last; ++s) {
+      const uint32_t r = (uint32_t)(r0 + s);
+      const Fx Ar = r >= n0 ? fx_add(A, X1) : A, f = fx_of(msr[r]);
+      if (fx_val(fx_add(Ar, f)) / Sd >= thr) {
+        fj = r << 1 | (fx_val(Ar) / Sd < thr ? 0u : 1u);
+        break;
+      }
+      A = fx_add(A, f);
+    }
+    fj = wave_min_u32(fj);
+    if (lane_id() == 0 && fj != NONE) atomicMin(&sh.q[1], fj);
+    __syncthreads();
+    fj = sh.q[1];
+    ok = fj != NONE && (fj & 1u) == 0u;
+  }
+  if (tid == 0 && ok) {
+    const int32_t tok = a.mode == MODE_SAMPLE ? (int32_t)pk_id(sh.lc[sh.q[1] >> 1]) : -1;
+    RowInfo r = {};
+    r.cmax = cmax;
+    r.kkeep = sh.lc[last];
+    r.S = Sd;
+    r.Z = clast;
+    r.flags = R_DONE | R_BY_DEEP;
+    r.token = tok;
+    a.info[row] = r;
+    if (a.mode == MODE_SAMPLE) a.tokens[row] = tok;
+  }
+}
+
 // The plan's tables lie past the history tables, so that the planning workgroup's pick item (the same slice) keeps
 // them.
 union PickShared {
@@ -841,8 +1086,12 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
   __syncthreads();
   if (sh.ticket != (uint32_t)(g.S - 1)) return;
   __builtin_amdgcn_s_setprio(3);  // (the finish is the row's critical path)
-  if (planned && ld_ag(&ds->spoil) == 0u)
-    finish_row(FinArgs{a.dlist + (size_t)slot * DCAP, a.info, a.tokens, a.mode}, ds, ps.f, etab);
+  if (planned && ld_ag(&ds->spoil) == 0u) {
+    const FinArgs fa{a.dlist + (size_t)slot * DCAP, a.info, a.tokens, a.mode};
+    const uint32_t n = ld_ag(&ds->lcnt);
+    if (a.fin_sorted && n <= (uint32_t)LC) finish_sorted(fa, ds, ps.f, etab, (int)n);
+    else finish_row(fa, ds, ps.f, etab);
+  }
   __syncthreads();  // (every thread has read the row's sums)
   uint64_t *gh = a.dhist + (size_t)slot * 3 * DNB;
   for (int b = tid; b < 3 * DNB; b += MT) gh[b] = 0;

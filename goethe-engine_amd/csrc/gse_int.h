@@ -141,6 +141,7 @@ struct ScanArgs {
   int dslots;          // split-row slots of the workspace
   int dslices, dgrid;  // split-row finish enabled (slices per deep row, at most), workgroups per pass
   uint64_t plan_wait;  // wall-clock ticks (100 MHz) a split-row pick slice waits for its row's plan
+  int fin_sorted;      // the split-row finish sorts short window lists whole (else every list takes the sub-bin walk)
   int tree;            // a verify round (gse_verify_tree): GSE_ROW_MSS rows need dist's keep boundary, not a token
   int32_t pstart[MAXP + 1];  // part p of every row is [pstart[p], pstart[p + 1]) (multiples of 1024; pstart[nparts] = V)
 };

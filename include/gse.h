@@ -105,9 +105,11 @@ enum {
   GSE_BATCH_PROFILE = 2u, /* record HIP events around each kernel of this call on its stream (read with gse_profile) */
   GSE_BATCH_NO_PLAN_WAIT = 4u, /* testing: a split-row finish slice whose row's plan is not out when it first looks
                                 * does not wait; the row takes the exact path (same results, slower) */
-  GSE_BATCH_NO_SPLIT = 8u /* the split-row finish is not launched: a row that would take it takes the exact path
-                           * (same results). For batches that cannot use it, to save its launch: greedy rows of
-                           * gse_sample never do (the Python layer sets it when every row is greedy). Since ABI 1.3. */
+  GSE_BATCH_NO_SPLIT = 8u, /* the split-row finish is not launched: a row that would take it takes the exact path
+                            * (same results). For batches that cannot use it, to save its launch: greedy rows of
+                            * gse_sample never do (the Python layer sets it when every row is greedy). Since ABI 1.3. */
+  GSE_BATCH_SUBBIN_FINISH = 16u /* testing: the split-row finish of every row takes its sub-bin walk, which it otherwise
+                                 * keeps for window lists longer than 2048 entries (same results). Since ABI 1.4. */
 };
 
 typedef struct gse_out {

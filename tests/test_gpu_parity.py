@@ -69,13 +69,13 @@ def test_golden_dist_draw_mss(ge, gpu, golden):
     assert [-1 if k is None else k for k in ks] == list(g["mss_out_kid"])
 
 
-def _run(ge, batch, gpu, exact=False, processed=False):
+def _run(ge, batch, gpu, exact=False, processed=False, flags=0):
     x = torch.from_numpy(batch.logits).to(gpu)
     if batch.bf16:
         x = x.view(torch.bfloat16)
     masks = None if batch.masks is None else [torch.from_numpy(m) for m in batch.masks]
     return ge.sampling.sample_ex(x, batch.params, None, None, masks, history=batch.history, uniforms=batch.uniforms,
-                                 exact=exact, processed=processed)
+                                 exact=exact, processed=processed, flags=flags)
 
 
 def _oracle(batch):
@@ -347,6 +347,28 @@ def test_deep_rows_sample_and_dist(ge, gpu):
     d = ge.sampling.dist_batch(xt, params).cpu().numpy()
     for r in range(0, n, 5):
         np.testing.assert_allclose(d[r], ora.dist(x[r], params[r]), rtol=DIST_RTOL, atol=1e-300)
+
+
+def test_deep_rows_subbin_finish(ge, gpu):
+    """The split-row finish has two ways to the cut and the draw: one sort of the whole window list (lists of at most
+    2048 entries, nearly every row) and the sub-bin walk (longer lists). GSE_BATCH_SUBBIN_FINISH sends every list to
+    the walk: on the flat rows and on the whole C3 batch both give the oracle's tokens, on the split-row path."""
+    n, v = 24, 151936
+    x, params = _flat_rows(ge, n, v, 7)
+    u = np.array([ora.uniform(1000 + r, 3) for r in range(n)], np.float64)
+    xt = torch.from_numpy(x).to(gpu)
+    want = ora.sample(x, params, None, None, None, uniforms=u)
+    for flags in (0, ge._lib.BATCH_SUBBIN_FINISH):
+        got = ge.sampling.sample_ex(xt, params, None, None, None, uniforms=u, flags=flags).tolist()
+        paths = ge._lib.handle(gpu.index, n, v).row_paths(n)
+        assert got == want, flags
+        assert (paths == ge._lib.PATH_DEEP).sum() >= n // 2, (flags, paths)
+    b = ge.workloads.c3()
+    a0 = _run(ge, b, gpu).tolist()
+    a1 = _run(ge, b, gpu, flags=ge._lib.BATCH_SUBBIN_FINISH).tolist()
+    paths = ge._lib.handle(gpu.index, b.rows, b.vocab).row_paths(b.rows)
+    assert a0 == a1 == [w["token"] for w in _oracle(b)]
+    assert (paths == ge._lib.PATH_DEEP).sum() > 0 and (paths == ge._lib.PATH_EXACT).sum() == 0, paths
 
 
 def test_deep_rows_odd_vocab_masks_history(ge, gpu):
