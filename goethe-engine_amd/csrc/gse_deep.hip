@@ -382,6 +382,7 @@ struct FinShared {
   uint64_t wred[NWV], wred2[NWV];
   uint32_t wsum[NWV];
   uint64_t pub[8];
+  uint64_t acc[DA_N];           // the sorted finish: the plan's sums and counts
 };
 
 // Exclusive prefix of two u64 values per thread, in thread order; ta, tb receive the totals.
@@ -718,18 +719,140 @@ constexpr int FB = 1024;  // key buckets per window
 static_assert(2 * 2 * FB * sizeof(uint32_t) <= SUBC * sizeof(uint64_t), "bucket counts and starts live in sub");
 static_assert(SUBC >= LC, "masses by rank live in sub");
 
-__device__ __noinline__ void finish_sorted(const FinArgs a, DeepSlot *ds, FinShared &sh, const double *etab, int n) {
+__device__ __forceinline__ uint64_t rl64(uint64_t x, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), lane);
+  return (uint64_t)hi << 32 | lo;
+}
+
+// The least x >= 0 with RN(x / S) >= t, for finite S > 0 and t >= 0: RN(x / S) is non-decreasing in x, so a test
+// RN(x / S) >= t reads x >= that least x, one comparison in place of a division per element. It lies within an ulp or
+// two of RN(t S): lane i of the wave (i < 16) tests RN(t S) + (i - 8) ulps, all at once, and the first lane whose
+// test holds gives it. ok turns false when the 16 candidates do not bracket it (the row then goes to the exact path).
+// Every lane of the wave must call it.
+__device__ __forceinline__ double least_ge(double t, double S, bool &ok) {
+  const double x0 = t * S;
+  const int i = lane_id() & 15;
+  const long long b0 = __double_as_longlong(x0) + (long long)(i - 8);
+  const double x = b0 > 0 ? __longlong_as_double(b0) : 0.0;
+  const uint64_t m = ballot64(lane_id() < 16 && x / S >= t);
+  const bool fin = x0 >= 0.0 && x0 < INFINITY;
+  // the first candidate that holds; candidate 0 only when it is 0 (nothing lies below)
+  const int f = m ? (int)__builtin_ctzll(m) : 16;
+  const double xf = __longlong_as_double((long long)rl64((uint64_t)__double_as_longlong(x), f & 15));
+  ok = ok && fin && f < 16 && (f > 0 || xf == 0.0);
+  return xf;
+}
+
+// The sorted finish of a list of at most 64 entries, by wave 0 alone (no barrier): lane l holds entry l; its rank is
+// the count of greater entries (read back from LDS, wave-local), the entries return to LDS in rank order, and lane r
+// takes rank r. The prefix sums are one wave scan, the cut and the draw one ballot each; the tests are finish_row's.
+// acc: lane i holds the plan's acc[i].
+__device__ __forceinline__ void finish_wave(const FinArgs a, DeepSlot *ds, FinShared &sh, const double *etab, int n,
+                                         uint64_t e, uint64_t accv, int row, float Mf, double u, uint64_t K,
+                                         double topp, double minp, bool sep, uint32_t w1lo) {
+  const int l = lane_id();
+  const bool val = l < n;
+  const double M = (double)Mf;
+  const bool g1o = val && sep && dbin(fkey_inv(pk_key(e)), Mf) >= w1lo;
+  const uint32_t n0 = (uint32_t)__popcll(ballot64(val && !g1o));  // entries of the draw window (they rank first)
+  if (val) sh.lc[l] = e;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  uint32_t r = 0;
+  {
+    int m = 0;
+#pragma unroll 1
+    for (; m + 2 <= n; m += 2) r += (sh.lc[m] > e ? 1u : 0u) + (sh.lc[m + 1] > e ? 1u : 0u);
+    if (m < n) r += sh.lc[m] > e ? 1u : 0u;
+  }
+  if (val) sh.sub[r] = e;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const uint64_t es = val ? sh.sub[l] : 0ull;  // rank l
+  const Fx f = val ? fx_of(exp_nonpos((double)fkey_inv(pk_key(es)) - M, etab)) : Fx{0, 0};
+  const Fx X0{rl64(accv, DA_X0HI), rl64(accv, DA_X0LO)}, X1{rl64(accv, DA_X1HI), rl64(accv, DA_X1LO)};
+  const Fx SF = fx_add(fx_add(X0, X1), Fx{rl64(accv, DA_RHI), rl64(accv, DA_RLO)});
+  const uint64_t c0 = rl64(accv, DA_C0), c1 = rl64(accv, DA_C1), tail = rl64(accv, DA_C2);
+  const double Sd = fx_val(SF), q0 = 1.0 / Sd;
+  bool okd = Sd > 0.0 && Sd < INFINITY;  // (x / Sd >= t reads x >= least_ge(t, Sd))
+  const double ap = least_ge(topp, Sd, okd), am = minp > 0.0 ? least_ge(minp * q0, Sd, okd) : 0.0;
+  const uint64_t ih = wave_incl_scan_u64(f.hi), il = wave_incl_scan_u64(f.lo);
+  const bool g1 = (uint32_t)l >= n0;
+  const Fx Ar = fx_add(fx_add(X0, Fx{ih - f.hi, il - f.lo}), g1 ? X1 : Fx{0, 0});  // exclusive prefix of rank l
+  // the first entry that is not kept (sampling.py:80, with min-p)
+  const bool cut = val && ((c0 + (uint64_t)l + (g1 ? c1 : 0ull) >= K) | (minp > 0.0 && !(fx_val(f) >= am)) |
+                           (fx_val(Ar) >= ap));
+  const uint64_t cb = ballot64(cut);
+  const int fc = cb ? (int)__builtin_ctzll(cb) : -1;
+  const int last = fc >= 0 ? fc - 1 : n - 1;  // the last kept entry
+  const bool glast = last >= 0 && (uint32_t)last >= n0;
+  bool ok = n > 0 && okd && last >= 0;
+  if (!ok) return;
+  Fx Al;  // c_last, unnormalized
+  if (fc >= 0) {
+    Al = Fx{rl64(Ar.hi, fc), rl64(Ar.lo, fc)};
+    ok = !((uint32_t)fc >= n0 && !glast && c1 > 0);  // (the first cut entry right after the gap: the cut may be inside it)
+  } else {
+    Al = fx_add(fx_add(X0, Fx{rl64(ih, n - 1), rl64(il, n - 1)}), glast ? X1 : Fx{0, 0});
+    const uint64_t rl = c0 + (uint64_t)last + (glast ? c1 : 0ull);
+    const uint64_t after = (!sep || glast) ? tail : c1 + tail;  // unlisted elements ranked after the list
+    ok = after == 0 || rl + 1 >= K || fx_val(Al) / Sd >= topp;
+  }
+  const double clast = fx_val(Al) / Sd;
+  int32_t tok = -1;
+  if (ok && a.mode == MODE_SAMPLE) {
+    // the draw: the first kept entry whose inclusive prefix reaches u c_last; its exclusive prefix must lie below it
+    const double at = least_ge(u * clast, Sd, ok);
+    const uint64_t hb = ballot64(l <= last && fx_val(fx_add(Ar, f)) >= at);
+    const uint64_t bb = ballot64(!(fx_val(Ar) >= at));
+    ok = ok && hb != 0;
+    if (ok) {
+      const int fj = (int)__builtin_ctzll(hb);
+      ok = ((bb >> fj) & 1ull) != 0;
+      tok = (int32_t)pk_id(rl64(es, fj));
+    }
+  }
+  const uint64_t kkeep = rl64(es, last);
+  if (l == 0 && ok) {  // (the main pass's cmax stays)
+    RowInfo *ri = a.info + row;
+    ri->kkeep = kkeep;
+    ri->S = Sd;
+    ri->Z = clast;
+    ri->flags = R_DONE | R_BY_DEEP;
+    ri->ncert = 0;
+    ri->token = tok;
+    if (a.mode == MODE_SAMPLE) a.tokens[row] = tok;
+  }
+}
+
+__device__ __noinline__ int finish_sorted(const FinArgs a, DeepSlot *ds, FinShared &sh, const double *etab) {
   constexpr int SP = LC / MT;  // entries (and ranks) per thread
   const int tid = threadIdx.x, w = tid >> 6;
-  const gse_row &P = ds->P;
+  // every load the finish makes, issued together: the list's first LC entries (entries past its end are stale and
+  // never used), the plan's windows, sums and counts (lanes of wave 0, into LDS), the row's parameters
+  const uint32_t nraw = ld_ag(&ds->lcnt), spoil = ld_ag(&ds->spoil);
+  const uint32_t w2hi = ld_ag(&ds->w2hi), w1lo = ld_ag(&ds->w1lo);
+  uint64_t v[SP];
+#pragma unroll
+  for (int j = 0; j < SP; ++j) v[j] = ld_ag(&a.lst[j * MT + tid]);
+  const uint64_t accv = tid < DA_N ? ld_ag(&ds->acc[tid]) : 0ull;  // (lane i of wave 0: acc[i])
   const int row = ds->row;
   const float Mf = ds->M;
-  const double M = (double)Mf;
-  const uint32_t w2hi = ld_ag(&ds->w2hi), w1lo = ld_ag(&ds->w1lo);
+  const double M = (double)Mf, u = ds->u;
+  const uint64_t K = ds->P.top_k > 0 ? (uint64_t)ds->P.top_k : ~0ull;
+  const double topp = ds->P.top_p, minp = ds->P.min_p;
+  if (spoil != 0u) return 0;  // (a slice gave up waiting for the plan: the exact path takes the row)
+  if (nraw > (uint32_t)LC) return 1;
+  const int n = (int)nraw;
   const bool sep = w1lo > w2hi;
-  uint64_t v[SP];  // the thread's entries (list order), every load issued before the first is used
-#pragma unroll
-  for (int j = 0; j < SP; ++j) v[j] = j * MT + tid < n ? ld_ag(&a.lst[j * MT + tid]) : 0ull;
+  if (n <= WAVE) {  // one wave does it all, without a barrier
+    if (tid < WAVE) finish_wave(a, ds, sh, etab, n, v[0], accv, row, Mf, u, K, topp, minp, sep, w1lo);
+    return 0;
+  }
+  if (tid < DA_N) sh.acc[tid] = accv;
   uint32_t *bcnt = reinterpret_cast<uint32_t *>(sh.sub), *bofs = bcnt + 2 * FB;
   double *msr = reinterpret_cast<double *>(sh.sub);  // (after the ranks: the masses by rank)
   for (int b = tid; b < 2 * FB; b += MT) bcnt[b] = 0;
@@ -769,28 +892,21 @@ __device__ __noinline__ void finish_sorted(const FinArgs a, DeepSlot *ds, FinSha
       lo[1] = min(lo[1], (uint32_t)(sh.wred2[k] >> 32));
     }
     for (int g = 0; g < 2; ++g) {
-      const uint32_t span = top[g] >= lo[g] ? top[g] - lo[g] : 0u;
+      const uint32_t span = top[g] >= lo[g] ? top[g] - lo[g] : 0u, nb = sep ? (uint32_t)FB : 2u * FB;
       uint32_t s = 0;
-      while (s < 31 && (span >> s) >= (uint32_t)FB) ++s;
+      while (s < 31 && (span >> s) >= nb) ++s;
       sft[g] = s;
     }
   }
-  // bucket and slot of every entry; its exact mass (the table loads overlap the LDS atomics)
-  uint32_t bk[SP], sl[SP];
-  double m[SP];
+  const uint32_t nb0 = sep ? (uint32_t)FB : 2u * FB;  // buckets of the draw window (all of them when one window)
+  // bucket of entry j (recomputed where used: fewer registers live across the phases) and its slot in the bucket
+  auto bucket = [&](int j) __attribute__((always_inline)) {
+    const uint32_t k = pk_key(v[j]);
+    return ((gm >> j) & 1u) ? FB + min((top[1] - k) >> sft[1], (uint32_t)(FB - 1)) : min((top[0] - k) >> sft[0], nb0 - 1u);
+  };
+  uint32_t sl[SP];
 #pragma unroll
-  for (int j = 0; j < SP; ++j) {
-    bk[j] = 0;
-    sl[j] = 0;
-    m[j] = 0.0;
-    if (j * MT + tid < n) {
-      const uint32_t k = pk_key(v[j]);
-      const int g = (gm >> j) & 1;
-      bk[j] = g * FB + min((top[g] - k) >> sft[g], (uint32_t)(FB - 1));
-      sl[j] = atomicAdd(&bcnt[bk[j]], 1u);
-      m[j] = exp_nonpos((double)fkey_inv(k) - M, etab);
-    }
-  }
+  for (int j = 0; j < SP; ++j) sl[j] = j * MT + tid < n ? atomicAdd(&bcnt[bucket(j)], 1u) : 0u;
   __syncthreads();
   // bucket starts: thread t owns buckets [8 t, 8 t + 8)
   {
@@ -813,10 +929,10 @@ __device__ __noinline__ void finish_sorted(const FinArgs a, DeepSlot *ds, FinSha
     }
   }
   __syncthreads();
-  const uint32_t n0 = bofs[FB];  // entries of the draw window (they rank first)
+  const uint32_t n0 = sep ? bofs[FB] : (uint32_t)n;  // entries of the draw window (they rank first)
 #pragma unroll
   for (int j = 0; j < SP; ++j)
-    if (j * MT + tid < n) sh.lc[bofs[bk[j]] + sl[j]] = v[j];
+    if (j * MT + tid < n) sh.lc[bofs[bucket(j)] + sl[j]] = v[j];
   __syncthreads();
   // rank = bucket start + greater members of the bucket
   uint32_t rk[SP];
@@ -824,10 +940,14 @@ __device__ __noinline__ void finish_sorted(const FinArgs a, DeepSlot *ds, FinSha
   for (int j = 0; j < SP; ++j) {
     rk[j] = 0;
     if (j * MT + tid < n) {
-      const uint32_t b0 = bofs[bk[j]], b1 = b0 + bcnt[bk[j]];
-      uint32_t r = b0;
+      const uint32_t bj = bucket(j), b0 = bofs[bj], b1 = b0 + bcnt[bj];
+      uint32_t r = b0, q = b0;
 #pragma unroll 1
-      for (uint32_t q = b0; q < b1; ++q) r += sh.lc[q] > v[j] ? 1u : 0u;
+      for (; q + 4 <= b1; q += 4)
+        r += (sh.lc[q] > v[j] ? 1u : 0u) + (sh.lc[q + 1] > v[j] ? 1u : 0u) + (sh.lc[q + 2] > v[j] ? 1u : 0u) +
+             (sh.lc[q + 3] > v[j] ? 1u : 0u);
+#pragma unroll 1
+      for (; q < b1; ++q) r += sh.lc[q] > v[j] ? 1u : 0u;
       rk[j] = r;
     }
   }
@@ -836,7 +956,7 @@ __device__ __noinline__ void finish_sorted(const FinArgs a, DeepSlot *ds, FinSha
   for (int j = 0; j < SP; ++j) {
     if (j * MT + tid < n) {
       sh.lc[rk[j]] = v[j];
-      msr[rk[j]] = m[j];
+      msr[rk[j]] = exp_nonpos((double)fkey_inv(pk_key(v[j])) - M, etab);  // (the entry's exact mass)
     }
   }
   __syncthreads();
@@ -851,11 +971,13 @@ __device__ __noinline__ void finish_sorted(const FinArgs a, DeepSlot *ds, FinSha
       lo += f.lo;
     }
   }
-  const Fx X0{ld_ag(&ds->acc[DA_X0HI]), ld_ag(&ds->acc[DA_X0LO])}, X1{ld_ag(&ds->acc[DA_X1HI]), ld_ag(&ds->acc[DA_X1LO])};
-  const Fx SF = fx_add(fx_add(X0, X1), Fx{ld_ag(&ds->acc[DA_RHI]), ld_ag(&ds->acc[DA_RLO])});
-  const uint64_t c0 = ld_ag(&ds->acc[DA_C0]), c1 = ld_ag(&ds->acc[DA_C1]), tail = ld_ag(&ds->acc[DA_C2]);
-  const uint64_t cmax = a.info[row].cmax;  // (written by the main pass; used at the end)
-  const double Sd = fx_val(SF);
+  const Fx X0{sh.acc[DA_X0HI], sh.acc[DA_X0LO]}, X1{sh.acc[DA_X1HI], sh.acc[DA_X1LO]};
+  const Fx SF = fx_add(fx_add(X0, X1), Fx{sh.acc[DA_RHI], sh.acc[DA_RLO]});
+  const uint64_t c0 = sh.acc[DA_C0], c1 = sh.acc[DA_C1], tail = sh.acc[DA_C2];
+  const double Sd = fx_val(SF), q0 = 1.0 / Sd;
+  bool okd = Sd > 0.0 && Sd < INFINITY;  // (x / Sd >= t reads x >= least_ge(t, Sd))
+  const double ap = least_ge(topp, Sd, okd), am = minp > 0.0 ? least_ge(minp * q0, Sd, okd) : 0.0;
+  uint64_t th = 0, tl = 0;  // the list's total
   {
     const uint64_t ih = wave_incl_scan_u64(hi), il = wave_incl_scan_u64(lo);
     if (lane_id() == WAVE - 1) {
@@ -863,7 +985,7 @@ __device__ __noinline__ void finish_sorted(const FinArgs a, DeepSlot *ds, FinSha
       sh.wred2[w] = il;
     }
     __syncthreads();
-    uint64_t ph = ih - hi, pl = il - lo, th = 0, tl = 0;
+    uint64_t ph = ih - hi, pl = il - lo;
     for (int k = 0; k < NWV; ++k) {
       ph += k < w ? sh.wred[k] : 0ull;
       pl += k < w ? sh.wred2[k] : 0ull;
@@ -872,29 +994,28 @@ __device__ __noinline__ void finish_sorted(const FinArgs a, DeepSlot *ds, FinSha
     }
     hi = ph;  // (now the exclusive prefix at rank r0)
     lo = pl;
-    sh.pub[0] = th;  // (the same value from every thread)
-    sh.pub[1] = tl;
   }
-  const uint64_t K = P.top_k > 0 ? (uint64_t)P.top_k : ~0ull;
-  const double topp = P.top_p, minp = P.min_p, q0 = 1.0 / Sd;
-  // the first entry that is not kept (sampling.py:80, with min-p); the thread holding it publishes its exclusive prefix
-  // (the inclusive prefix of the last kept entry)
+  // The first entry that is not kept (sampling.py:80, with min-p); the thread holding it publishes its exclusive
+  // prefix (the inclusive prefix of the last kept entry). The thread's SP tests are independent (their prefixes are
+  // integer sums), so they overlap.
   {
-    Fx A = fx_add(X0, Fx{hi, lo});
+    Fx A = fx_add(X0, Fx{hi, lo}), Ah{0, 0};
     uint32_t fc = NONE;
-#pragma unroll 1
-    for (int s = 0; s < SP && r0 + s < n; ++s) {
+#pragma unroll 4
+    for (int s = 0; s < SP; ++s) {
       const uint32_t r = (uint32_t)(r0 + s);
       const bool g1 = r >= n0;
       const Fx Ar = g1 ? fx_add(A, X1) : A, f = fx_of(msr[r]);
-      if (c0 + r + (g1 ? c1 : 0ull) >= K || (minp > 0.0 && !(fx_val(f) / Sd >= minp * q0)) ||
-          fx_val(Ar) / Sd >= topp) {
+      const bool cut = (c0 + r + (g1 ? c1 : 0ull) >= K) | (minp > 0.0 && !(fx_val(f) >= am)) | (fx_val(Ar) >= ap);
+      if (r < (uint32_t)n && cut && fc == NONE) {
         fc = r;
-        sh.shi[tid] = Ar.hi;
-        sh.slo[tid] = Ar.lo;
-        break;
+        Ah = Ar;
       }
       A = fx_add(A, f);
+    }
+    if (fc != NONE) {
+      sh.shi[tid] = Ah.hi;
+      sh.slo[tid] = Ah.lo;
     }
     fc = wave_min_u32(fc);
     if (lane_id() == 0 && fc != NONE) atomicMin(&sh.q[0], fc);
@@ -903,13 +1024,13 @@ __device__ __noinline__ void finish_sorted(const FinArgs a, DeepSlot *ds, FinSha
   const uint32_t fc = sh.q[0];
   const int last = fc == NONE ? n - 1 : (int)fc - 1;  // the last kept entry
   const bool glast = last >= 0 && (uint32_t)last >= n0;
-  bool ok = n > 0 && Sd > 0.0 && last >= 0;
+  bool ok = n > 0 && okd && last >= 0;
   Fx Al{0, 0};  // c_last, unnormalized
   if (fc != NONE) {
     Al = Fx{sh.shi[fc / SP], sh.slo[fc / SP]};
     ok = ok && !(fc >= n0 && !glast && c1 > 0);  // (the first cut entry right after the gap: the cut may be inside it)
   } else {
-    Al = fx_add(fx_add(X0, Fx{sh.pub[0], sh.pub[1]}), glast ? X1 : Fx{0, 0});
+    Al = fx_add(fx_add(X0, Fx{th, tl}), glast ? X1 : Fx{0, 0});
     const uint64_t rl = c0 + (uint64_t)last + (glast ? c1 : 0ull);
     const uint64_t after = (!sep || glast) ? tail : c1 + tail;  // unlisted elements ranked after the list
     ok = ok && (after == 0 || rl + 1 >= K || fx_val(Al) / Sd >= topp);
@@ -918,37 +1039,36 @@ __device__ __noinline__ void finish_sorted(const FinArgs a, DeepSlot *ds, FinSha
   if (ok && a.mode == MODE_SAMPLE) {
     // the draw: the first kept entry whose inclusive prefix reaches u c_last; its exclusive prefix must lie below it
     // (else the draw falls in an unlisted region: before the list, or in the gap). Packed as rank << 1 | (not below).
-    const double thr = ds->u * clast;
+    bool okt = true;
+    const double at = least_ge(u * clast, Sd, okt);  // (the same value in every thread)
     Fx A = fx_add(X0, Fx{hi, lo});
     uint32_t fj = NONE;
-#pragma unroll 1
-    for (int s = 0; s < SP && r0 + s <= last; ++s) {
+#pragma unroll 4
+    for (int s = 0; s < SP; ++s) {
       const uint32_t r = (uint32_t)(r0 + s);
       const Fx Ar = r >= n0 ? fx_add(A, X1) : A, f = fx_of(msr[r]);
-      if (fx_val(fx_add(Ar, f)) / Sd >= thr) {
-        fj = r << 1 | (fx_val(Ar) / Sd < thr ? 0u : 1u);
-        break;
-      }
+      const bool hit = fx_val(fx_add(Ar, f)) >= at, below = !(fx_val(Ar) >= at);
+      if ((int)r <= last && hit && fj == NONE) fj = r << 1 | (below ? 0u : 1u);
       A = fx_add(A, f);
     }
     fj = wave_min_u32(fj);
     if (lane_id() == 0 && fj != NONE) atomicMin(&sh.q[1], fj);
     __syncthreads();
     fj = sh.q[1];
-    ok = fj != NONE && (fj & 1u) == 0u;
+    ok = okt && fj != NONE && (fj & 1u) == 0u;
   }
-  if (tid == 0 && ok) {
+  if (tid == 0 && ok) {  // (the main pass's cmax stays)
     const int32_t tok = a.mode == MODE_SAMPLE ? (int32_t)pk_id(sh.lc[sh.q[1] >> 1]) : -1;
-    RowInfo r = {};
-    r.cmax = cmax;
-    r.kkeep = sh.lc[last];
-    r.S = Sd;
-    r.Z = clast;
-    r.flags = R_DONE | R_BY_DEEP;
-    r.token = tok;
-    a.info[row] = r;
+    RowInfo *ri = a.info + row;
+    ri->kkeep = sh.lc[last];
+    ri->S = Sd;
+    ri->Z = clast;
+    ri->flags = R_DONE | R_BY_DEEP;
+    ri->ncert = 0;
+    ri->token = tok;
     if (a.mode == MODE_SAMPLE) a.tokens[row] = tok;
   }
+  return 0;
 }
 
 // The plan's tables lie past the history tables, so that the planning workgroup's pick item (the same slice) keeps
@@ -1010,9 +1130,10 @@ __device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slic
 }
 
 
+// Returns the slot to finish when this slice was the row's last (-2 - slot when the row was not planned), else -1.
 template <int DT, bool AL>
-__device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice, const DGeom &g, PickShared &ps,
-                                          const double *etab, bool keep) {
+__device__ __forceinline__ int pick_item(const ScanArgs &a, int slot, int slice, const DGeom &g, PickShared &ps,
+                                         const double *etab, bool keep) {
   DeepShared &sh = ps.d;
   const int tid = threadIdx.x;
   DeepSlot *ds = a.dslot + slot;
@@ -1079,18 +1200,29 @@ __device__ __forceinline__ void pick_item(const ScanArgs &a, int slot, int slice
       }
     }
   }
-  // Ticket: the row's last slice finishes it, then clears the row's records for the next call.
+  // Ticket: the row's last slice finishes it (finish_item, called by the kernel's loop).
   store_wait();
   __syncthreads();
   if (tid == 0) sh.ticket = ticket_add(&ds->pdone);
   __syncthreads();
-  if (sh.ticket != (uint32_t)(g.S - 1)) return;
+  if (sh.ticket != (uint32_t)(g.S - 1)) return -1;
+  return planned ? slot : -2 - slot;
+}
+
+// The finish of the row in slot fs (fs < -1: the row was not planned; its records are cleared all the same), then the
+// row's records cleared for the next call. Called at the kernel's top level, after the pick item: its registers are
+// allocated apart from the streaming code's, with no call in between.
+__device__ __forceinline__ void finish_item(const ScanArgs &a, int fs, PickShared &ps, const double *etab) {
+  const int tid = threadIdx.x;
+  const bool planned = fs >= 0;
+  const int slot = planned ? fs : -2 - fs;
+  DeepSlot *ds = a.dslot + slot;
   __builtin_amdgcn_s_setprio(3);  // (the finish is the row's critical path)
-  if (planned && ld_ag(&ds->spoil) == 0u) {
+  if (planned) {
     const FinArgs fa{a.dlist + (size_t)slot * DCAP, a.info, a.tokens, a.mode};
-    const uint32_t n = ld_ag(&ds->lcnt);
-    if (a.fin_sorted && n <= (uint32_t)LC) finish_sorted(fa, ds, ps.f, etab, (int)n);
-    else finish_row(fa, ds, ps.f, etab);
+    if (a.fin_sorted ? finish_sorted(fa, ds, ps.f, etab) != 0 : ld_ag(&ds->spoil) == 0u) {
+      finish_row(fa, ds, ps.f, etab);
+    }
   }
   __syncthreads();  // (every thread has read the row's sums)
   uint64_t *gh = a.dhist + (size_t)slot * 3 * DNB;
@@ -1116,7 +1248,10 @@ __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
   for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) count_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab);
   // one item per workgroup in each pass: the pick item is the count item's slice, whose history tables are still in LDS
   const bool keep = nd * g.S <= (int)gridDim.x;
-  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) pick_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab, keep);
+  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) {
+    const int fs = pick_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab, keep);
+    if (fs != -1) finish_item(a, fs, sh, etab);
+  }
 }
 
 template <int DT, bool AL>
