@@ -607,6 +607,24 @@ __device__ __forceinline__ void hist_words(const HistTab &h, int cb, int p0, int
   }
 }
 
+// The processed logits of one vector's VEC tokens (-inf where al does not allow a token) into p[0, VEC), skipping the
+// tokens whose bit in skip is set (history tokens: the side pass writes them). 16-byte stores when nothing is skipped
+// and p is 16-byte aligned (a whole vector per 4 tokens), else one store per token.
+template <int VEC>
+__device__ __forceinline__ void put_proc(float *p, bool p16, const float *x, uint32_t al, uint32_t skip) {
+  if (p16 && skip == 0u) {
+#pragma unroll
+    for (int q = 0; q < VEC; q += 4)
+      *reinterpret_cast<float4 *>(p + q) = make_float4(keep_or_ninf(x[q], al, q), keep_or_ninf(x[q + 1], al, q + 1),
+                                                       keep_or_ninf(x[q + 2], al, q + 2),
+                                                       keep_or_ninf(x[q + 3], al, q + 3));
+  } else {
+#pragma unroll
+    for (int k = 0; k < VEC; ++k)
+      if (!((skip >> k) & 1u)) p[k] = keep_or_ninf(x[k], al, k);
+  }
+}
+
 // x of a full chunk (every token below the stream end) of a sampled row in place: the keep bits of each vector, mask AND
 // NOT history, from the raw words with one bit-field extract; the NaN flag; -inf where a token is not kept (no select
 // when the whole wave's chunk keeps everything); the lane's chunk maximum. The same results as chunk_z for such a chunk,
@@ -628,14 +646,13 @@ __device__ __forceinline__ float chunk_x_full(const RowCtx &c, int cb, float (&x
     full = full && keep[v] == VMASK;
   }
   if (proc) {  // processed logits (after penalties and mask, before T) of the streamed (non-history) tokens
+    const bool p16 = ((uintptr_t)proc & 15u) == 0;
 #pragma unroll
     for (int v = 0; v < L::NV; ++v) {
       const int t0 = cb + v * L::STRIDE + l * L::VEC;
       const uint32_t al = MASKED ? __builtin_amdgcn_ubfe(mw[v], sh, (uint32_t)L::VEC) : VMASK;
       const uint32_t hx = c.pen ? __builtin_amdgcn_ubfe(hw[v], sh, (uint32_t)L::VEC) : 0u;
-#pragma unroll
-      for (int k = 0; k < L::VEC; ++k)
-        if (!((hx >> k) & 1u)) proc[t0 + k] = keep_or_ninf(xr[v * L::VEC + k], al, k);
+      put_proc<L::VEC>(proc + t0, p16, xr + v * L::VEC, al, hx);
     }
   }
 #pragma unroll
@@ -690,13 +707,12 @@ __device__ __forceinline__ float chunk_z(const RowCtx &c, int cb, int p0, int pv
     full = full && keep[v] == VMASK;
   }
   if (proc) {  // processed logits (after penalties and mask, before T) of the streamed tokens
+    const bool p16 = ((uintptr_t)proc & 15u) == 0;
 #pragma unroll
     for (int v = 0; v < L::NV; ++v) {
       const int t0 = cb + v * L::STRIDE + l * L::VEC;
       const uint32_t al = MASKED ? (mw[v] >> ((l * L::VEC) & 31)) & VMASK : VMASK;
-#pragma unroll
-      for (int k = 0; k < L::VEC; ++k)
-        if ((inr[v] >> k) & 1u) proc[t0 + k] = keep_or_ninf(xr[v * L::VEC + k], al, k);
+      put_proc<L::VEC>(proc + t0, p16, xr + v * L::VEC, al, ~inr[v] & VMASK);
     }
   }
 #pragma unroll
