@@ -124,3 +124,39 @@ def test_product_path_refuses_without_a_gpu(ge):
         ge.sampling.sample(x, [P()], [0], [0], [None])
     with pytest.raises(RuntimeError):
         ge.sampling.draw(np.ones(4) / 4, 0.5)
+
+
+def _least_ge_brute(t, S):
+    """The least float64 x >= 0 with x / S >= t, by stepping one ulp at a time from far below (plain Python floats)."""
+    import math
+    x = max(0.0, t * S * (1 - 1e-12))
+    while not (x / S >= t):
+        x = math.nextafter(x, math.inf)
+    while x > 0.0 and math.nextafter(x, 0.0) / S >= t:
+        x = math.nextafter(x, 0.0)
+    return x
+
+
+def test_division_threshold_lies_within_eight_ulps():
+    """The split-row finish replaces each test x / S >= t (x the exact fixed-point prefix as a double, S the row's mass,
+    t = top_p, min_p q_0 or u c_last) by x >= a, with a the least double for which the test holds: RN(x / S) is
+    non-decreasing in x, so that is the same test. The device finds a among the 16 doubles RN(t S) - 8 ulp ..
+    RN(t S) + 7 ulp (one per lane) and sends the row to the exact path when they do not bracket it. Brute force over
+    random and edge (t, S) here: a always lies in that window, and the window's first passing candidate is a."""
+    import math
+    rng = np.random.default_rng(11)
+    cases = [(0.0, 1.0), (1.0, 1.0), (1.0, 151936.0), (0.9, 3.0), (1e-300, 2.0), (0.5, 2.0 ** 18), (1.0, 1.0 + 2 ** -52)]
+    cases += [(float(rng.random()), float(1.0 + rng.random() * 2 ** 18)) for _ in range(3000)]
+    cases += [(float(rng.random() * 1e-6), float(1.0 + rng.random() * 10)) for _ in range(500)]
+    for t, S in cases:
+        want = _least_ge_brute(t, S)
+        x0 = t * S
+        bits0 = np.float64(x0).view(np.int64)
+        cand = [float(np.int64(max(b, 0)).view(np.float64)) if b > 0 else 0.0 for b in (bits0 + np.arange(-8, 8))]
+        ok = [c / S >= t for c in cand]
+        f = ok.index(True) if any(ok) else 16
+        assert f < 16 and (f > 0 or cand[f] == 0.0), (t, S)
+        assert cand[f] == want, (t, S, cand[f], want)
+        assert all(ok[f:]) and not any(ok[:f]), (t, S)
+        for x in (want, math.nextafter(want, 0.0), math.nextafter(want, math.inf)):
+            assert (x / S >= t) == (x >= want)
