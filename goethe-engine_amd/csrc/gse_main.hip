@@ -470,8 +470,23 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   const int n = ev.n;
   int st = EV_HARD;
   if (!((flags & (F_OVERFLOW | F_HOVER)) || nh_all > (uint32_t)NH || a.force_exact)) {
-    sort_head(sh, n, mk, kappa);
-    st = evaluate(ev, sh.r.head, sh);
+    // A keep prefix that surely runs past the head goes on without the sort and the evaluation, whose answer it
+    // already knows (EV_HARD): no logprobs, no top-k or min-p cut inside the head, an incomplete head, and the whole
+    // head's mass h below top_p (S - B) even with margins far above the roundings of h and of the evaluation's own sums
+    // (each within 2048 ulps). The rows of flat, hot nuclei that go to the split-row finish.
+    bool past = false;
+    if (!greedy && nlp == 0 && !complete && !(P.min_p > 0.0) && (P.top_k <= 0 || P.top_k > n)) {
+      double h = 0.0;
+      for (int i = tid; i < n; i += MT) h += exp_nonpos((double)fkey_inv(pk_key(sh.r.head[i])) - M, sh.etab);
+      h = block_sum_f64(h, sh.wred);
+      const double hhi = h * (1.0 + 1e-11), hlo = h * (1.0 - 1e-11);
+      const double B = ev.B + 2e-15 * (ev.S + hhi);
+      past = hhi < P.top_p * (ev.S + hlo - B);
+    }
+    if (!past) {
+      sort_head(sh, n, mk, kappa);
+      st = evaluate(ev, sh.r.head, sh);
+    }
   }
   if (st != EV_DONE) {
     __syncthreads();  // (sh.lpw)
