@@ -387,37 +387,50 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   auto batch = [&](const uint64_t(&pk)[GPT], const bool(&ok)[GPT]) __attribute__((always_inline)) {
 #pragma unroll
     for (int g = 0; g < GPT; ++g) sh.r.tmp[g * MT + tid] = ok[g] ? key_of_raw(pk[g], divide, Rd) : 0ull;
+    // the masses of the entries below the certified key, two at a time (independent exponentials overlap), and the
+    // head bits of the thread's GPT entries
+    uint32_t hb = 0;
 #pragma unroll 1
+    for (int g = 0; g < GPT; g += 2) {
+      const uint64_t v0 = sh.r.tmp[g * MT + tid], v1 = sh.r.tmp[(g + 1) * MT + tid];
+      const uint32_t k0 = pk_key(v0), k1 = pk_key(v1);
+      bestL = max(bestL, max(v0, v1));
+      const bool m0 = v0 && finite_max && k0 > KEY_NEGINF && k0 < kappa;
+      const bool m1 = v1 && finite_max && k1 > KEY_NEGINF && k1 < kappa;
+      const double e0 = exp_nonpos(m0 ? (double)fkey_inv(k0) - M : 0.0, sh.etab);
+      const double e1 = exp_nonpos(m1 ? (double)fkey_inv(k1) - M : 0.0, sh.etab);
+      scand += (m0 ? e0 : 0.0);
+      scand += (m1 ? e1 : 0.0);
+      hb |= (v0 && k0 >= kappa ? 1u : 0u) << g;
+      hb |= (v1 && k1 >= kappa ? 1u : 0u) << (g + 1);
+    }
+    // head appends: one LDS atomic per wave for all GPT rounds
+    uint32_t cnt = 0;
+    uint64_t bl[GPT];
+#pragma unroll
     for (int g = 0; g < GPT; ++g) {
-      const uint64_t v = sh.r.tmp[g * MT + tid];
-      const uint32_t k = pk_key(v);
-      bestL = v > bestL ? v : bestL;
-      if (v && finite_max && k > KEY_NEGINF && k < kappa) scand += exp_nonpos((double)fkey_inv(k) - M, sh.etab);
-      const bool h = v && k >= kappa;
-      const uint64_t bl = ballot64(h);
-      if (bl) {
-        uint32_t base = 0;
-        if (lane_id() == 0) base = atomicAdd(&sh.nh, (uint32_t)__popcll(bl));
-        base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
-        const uint32_t pos = base + lanes_below(bl);
-        if (h && pos < (uint32_t)NH) sh.r.head[pos] = v;
+      bl[g] = ballot64((hb >> g) & 1u);
+      cnt += (uint32_t)__popcll(bl[g]);
+    }
+    if (cnt) {
+      uint32_t base = 0;
+      if (lane_id() == 0) base = atomicAdd(&sh.nh, cnt);
+      base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+#pragma unroll
+      for (int g = 0; g < GPT; ++g) {
+        const uint32_t pos = base + lanes_below(bl[g]);
+        if (((hb >> g) & 1u) && pos < (uint32_t)NH) sh.r.head[pos] = sh.r.tmp[g * MT + tid];
+        base += (uint32_t)__popcll(bl[g]);
       }
     }
   };
-  {
-    bool ok[GPT];
-#pragma unroll
-    for (int g = 0; g < GPT; ++g) {
-      const int e = g * MT + tid, j = e / SPEC;
-      ok[g] = j < nsl && (uint32_t)(e - j * SPEC) < sh.loff[j];
-    }
-    batch(pks, ok);
-  }
-  // the slots past SPEC of the longer lists (flat index f over them; the list holding f: the last with prefix <= f)
+  // the slots past SPEC of the longer lists (flat index f over them; the list holding f: the last with prefix <= f),
+  // a round of MT GPT at a time; the first such round is loaded before the speculative batch is processed, so that its
+  // loads are in flight meanwhile
   const uint32_t rtot = sh.jcount;
-  for (uint32_t f0 = 0; f0 < rtot; f0 += MT * GPT) {
-    uint64_t pk[GPT];
-    bool ok[GPT];
+  uint64_t pk[GPT];
+  bool okr[GPT];
+  auto load_round = [&](uint32_t f0) __attribute__((always_inline)) {
 #pragma unroll
     for (int g = 0; g < GPT; ++g) {
       const uint32_t f = f0 + g * MT + tid;
@@ -427,11 +440,24 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
         const int m = lo + st;
         if (m < nsl && sh.lmax[m] <= f) lo = m;
       }
-      ok[g] = f < rtot;
-      pk[g] = ok[g] ? ld_ag(&cl0[(size_t)lo * CAPW + min((uint32_t)SPEC + f - sh.lmax[lo], (uint32_t)CAPW - 1u)])
-                    : 0ull;
+      okr[g] = f < rtot;
+      pk[g] = okr[g] ? ld_ag(&cl0[(size_t)lo * CAPW + min((uint32_t)SPEC + f - sh.lmax[lo], (uint32_t)CAPW - 1u)])
+                     : 0ull;
     }
-    batch(pk, ok);
+  };
+  if (rtot > 0) load_round(0);
+  {
+    bool ok[GPT];
+#pragma unroll
+    for (int g = 0; g < GPT; ++g) {
+      const int e = g * MT + tid, j = e / SPEC;
+      ok[g] = j < nsl && (uint32_t)(e - j * SPEC) < sh.loff[j];
+    }
+    batch(pks, ok);
+  }
+  for (uint32_t f0 = 0; f0 < rtot; f0 += MT * GPT) {
+    if (f0 > 0) load_round(f0);
+    batch(pk, okr);
   }
   bestL = wave_max_u64(bestL);
   if (lane_id() == 0) atomicMax((unsigned long long *)&sh.rtopL, (unsigned long long)bestL);
