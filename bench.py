@@ -330,8 +330,11 @@ def run_sample(args, ge, torch, batch):
         step(k, profile=True)
     torch.cuda.synchronize()
     calls, kms = h.profile()
-    kern = ["main_kernel", "deep_kernel", "exact_kernel"]
-    per = {kern[i]: kms[i] / calls * 1e3 for i in range(min(len(kern), len(kms)))}
+    # (the profile's interval per kernel slot: main, split-row, exact; a call launches the split-row kernel, which
+    # finishes every hard row itself, or, without it, the exact kernel)
+    slot = {"main_kernel": 0, "deep_kernel": 1, "exact_kernel": 2}
+    kern = ["main_kernel", "exact_kernel" if base_flags & lib.BATCH_NO_SPLIT else "deep_kernel"]
+    per = {k: kms[slot[k]] / calls * 1e3 for k in kern}
     log("[bench] per call (profiled) " + ", ".join(f"{k} {v:.2f} us" for k, v in per.items()))
     ceil = read_ceiling([s["x"] for s in sets], torch)
     thr = through_sample(args, ge, torch, batch, [s["x"] for s in sets], gpu_tokens) if args.through_sample else None

@@ -213,7 +213,9 @@ gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   a.dlist = h->dlist;
   a.dslots = (int)h->dslots;
   deep_grid(h, b.rows, &a.dslices, &a.dgrid);
-  if (b.flags & GSE_BATCH_NO_SPLIT) {  // (no slots: the resolve sends such rows to the exact path)
+  // Without the split-row launch the exact launch finishes the hard rows (the resolve sends them there: no slots);
+  // with it, that launch finishes every hard row itself. A forced exact call takes the 1024-thread exact launch.
+  if (b.flags & (GSE_BATCH_NO_SPLIT | GSE_BATCH_EXACT)) {
     a.dslices = 0;
     a.dgrid = 0;
   }
@@ -331,7 +333,7 @@ int sample_impl(gse_handle *h, const gse_batch &b, const gse_out &o) {
   if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return hip_fail(h, e, "event record");
   if (a.dgrid > 0 && (e = gse::launch_deep(a, s)) != hipSuccess) return hip_fail(h, e, "deep launch");
   if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return hip_fail(h, e, "event record");
-  if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
+  if (a.dgrid == 0 && (e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
   if (ev && (e = hipEventRecord(ev[3], s)) != hipSuccess) return hip_fail(h, e, "event record");
   return GSE_OK;
 }
@@ -433,7 +435,7 @@ GSE_API int gse_dist(gse_handle *h, const gse_batch *in, double *probs, int64_t 
   if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return hip_fail(h, e, "event record");
   if (a.dgrid > 0 && (e = gse::launch_deep(a, s)) != hipSuccess) return hip_fail(h, e, "deep launch");
   if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return hip_fail(h, e, "event record");
-  if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
+  if (a.dgrid == 0 && (e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
   if (ev && (e = hipEventRecord(ev[3], s)) != hipSuccess) return hip_fail(h, e, "event record");
   if ((e = gse::launch_dist_write(a, probs, probs_ld, s)) != hipSuccess) return hip_fail(h, e, "dist launch");
   if (ev && (e = hipEventRecord(ev[4], s)) != hipSuccess) return hip_fail(h, e, "event record");
@@ -508,7 +510,7 @@ GSE_API int gse_verify_tree(gse_handle *h, const gse_batch *in, const gse_tree *
     qdone = h->join;
   }
   if (a.dgrid > 0 && (e = gse::launch_deep(a, s)) != hipSuccess) return hip_fail(h, e, "deep launch");
-  if ((e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
+  if (a.dgrid == 0 && (e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
   if ((e = gse::launch_tree(L, s, qdone)) != hipSuccess) return hip_fail(h, e, "verify launch");
   return GSE_OK;
 }

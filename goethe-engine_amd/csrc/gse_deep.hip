@@ -396,6 +396,10 @@ struct FinShared {
   uint64_t acc[DA_N];           // the sorted finish: the plan's sums and counts
 };
 
+// Set by the finish's thread 0 when it has written the row's result (cleared by the same thread before the finish);
+// a row without it goes to the exact path, in the same workgroup.
+__shared__ uint32_t g_fin;
+
 // Exclusive prefix of two u64 values per thread, in thread order; ta, tb receive the totals.
 __device__ __forceinline__ void excl_scan2(uint64_t &a, uint64_t &b, uint64_t &ta, uint64_t &tb, FinShared &sh) {
   const uint64_t ia = wave_incl_scan_u64(a), ib = wave_incl_scan_u64(b);
@@ -714,6 +718,7 @@ __device__ __noinline__ void finish_row(const FinArgs a, DeepSlot *ds, FinShared
     r.flags = R_DONE | R_BY_DEEP;
     r.token = tok;
     *ri = r;
+    g_fin = 1u;
     if (a.mode == MODE_SAMPLE) a.tokens[row] = tok;
   }
 }
@@ -836,6 +841,7 @@ __device__ __forceinline__ void finish_wave(const FinArgs a, DeepSlot *ds, FinSh
     ri->ncert = 0;
     ri->token = tok;
     if (a.mode == MODE_SAMPLE) a.tokens[row] = tok;
+    g_fin = 1u;
   }
 }
 
@@ -1078,6 +1084,7 @@ __device__ __noinline__ int finish_sorted(const FinArgs a, DeepSlot *ds, FinShar
     ri->ncert = 0;
     ri->token = tok;
     if (a.mode == MODE_SAMPLE) a.tokens[row] = tok;
+    g_fin = 1u;
   }
   return 0;
 }
@@ -1092,6 +1099,90 @@ union PickShared {
   } p;
   FinShared f;
 };
+
+// ---- the exact path inside this launch ------------------------------------------------------------------------------
+// The hard rows this launch does not finish by the window lists (a finish that failed, a row that was not planned, and
+// the hard rows the main pass did not send here) are finished by the exact radix-select path, in this launch's
+// workgroup shape, so that no second launch follows. Its LDS is the pick items' (a union).
+namespace x256 {
+constexpr int XT = MT;      // threads
+constexpr int NB = 1024;    // histogram bins
+constexpr int LB = 10;      // key bits per histogram level
+constexpr int CAPS = 2048;  // collected elements
+constexpr int CHX = 2048;   // tokens per chunk
+#include "gse_exact_body.h"
+}  // namespace x256
+
+union DeepLds {
+  PickShared p;
+  x256::ExactShared x;
+};
+__shared__ DeepLds g_lds;
+__shared__ ScanArgs g_args;               // the exact path's copy of the kernel's arguments
+__shared__ uint64_t g_fail[DEEP_MAX / 64];  // slots whose finish failed in this workgroup (its exact rows)
+__shared__ uint64_t g_hb[NWV];            // the hard-row scan: one ballot per wave
+__shared__ uint32_t g_scan;               // hard rows that the main pass did not send to the split-row finish
+__shared__ uint64_t g_pl[DEEP_MAX / 64];  // thread 0: slots planned by this workgroup whose rows-planned ticket is due
+__shared__ uint32_t g_gs;                 // workgroups that share the hard-row scan (rows g, g + g_gs, ...)
+__shared__ uint32_t g_nd;                 // thread 0: the call's deep rows (read after the items, not kept in a register)
+
+// The call's counts (deep rows and other hard rows: one 64-bit word, read and cleared whole) and the rows-planned ticket
+// are cleared for the next call once every row is planned: every workgroup with items has then read the counts (its
+// first count item came before). A workgroup without items reads them before (deep rows, so it has no items) or after
+// (nothing to do): either way it does nothing.
+__device__ __forceinline__ void clear_counts(const ScanArgs &a) {
+  st_ag(reinterpret_cast<uint64_t *>(a.dctl), (uint64_t)0);
+  st_ag(&a.dctl[2], 0u);
+}
+
+namespace x256 {
+__device__ __forceinline__ ExactShared &xs() { return g_lds.x; }
+}  // namespace x256
+
+// Finishes one hard row by the exact path (every thread of the workgroup calls it; the LDS is free again when it
+// returns).
+__device__ __noinline__ void exact_hard(int row) { x256::exact_row(g_args, row, g_lds.x); }
+
+// The workgroup's exact rows, after its items: the rows whose finish failed here (their flags still read R_HARD |
+// R_DEEP), then, when the main pass counted any (scan), the hard rows it did not send to the split-row finish (R_HARD
+// without R_DEEP), workgroup g of the g_gs that scan taking rows g, g + g_gs, ... (A row that another workgroup is
+// finishing reads R_DEEP, then R_DONE: skipped.) Not inlined, reading the arguments from their LDS copy, so that the
+// kernel keeps nothing across it and its streaming code's registers are allocated apart from the exact path's.
+__device__ __noinline__ void exact_rows(bool scan) {
+  const ScanArgs &a = g_args;
+  const int G = (int)g_gs, tid = threadIdx.x;
+#pragma unroll 1
+  for (int k = 0; k < DEEP_MAX / 64; ++k) {
+    for (uint64_t m = g_fail[k]; m; m &= m - 1ull) {
+      exact_hard(a.dslot[k * 64 + (int)__builtin_ctzll(m)].row);
+      __syncthreads();  // (LDS of the row)
+    }
+  }
+  if (!scan) return;
+  for (int j0 = (int)blockIdx.x; j0 < a.rows; j0 += MT * G) {
+    const int r = j0 + tid * G;
+    const bool hard = r < a.rows && (a.info[r].flags & (R_HARD | R_DEEP)) == R_HARD;
+    const uint64_t bl = ballot64(hard);
+    if (lane_id() == 0) g_hb[tid / WAVE] = bl;
+    __syncthreads();
+    uint64_t hb[NWV];
+#pragma unroll
+    for (int k = 0; k < NWV; ++k) hb[k] = g_hb[k];
+    __syncthreads();  // (every thread has read the ballots)
+#pragma unroll 1
+    for (int k = 0; k < NWV; ++k) {
+      for (uint64_t m = hb[k]; m; m &= m - 1ull) {
+        exact_hard(j0 + (k * WAVE + (int)__builtin_ctzll(m)) * G);
+        __syncthreads();  // (LDS of the row)
+      }
+    }
+  }
+  // Without deep rows, every workgroup scans, and the last to end clears the count of other hard rows.
+  if (tid == 0 && g_nd == 0u && ticket_add(&a.dctl[3]) == gridDim.x - 1u) {
+    st_ag(reinterpret_cast<uint64_t *>(a.dctl), (uint64_t)0);
+    st_ag(&a.dctl[3], 0u);
+  }
+}
 
 template <int DT, bool AL>
 __device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slice, const DGeom &g, PickShared &ps,
@@ -1138,7 +1229,10 @@ __device__ __forceinline__ void count_item(const ScanArgs &a, int slot, int slic
   if (!lastc) return;
   __builtin_amdgcn_s_setprio(3);  // (the row's other slices wait for the plan)
   plan_block(gh, ds, a.mode, ps.p.pl);
-  if (tid == 0) ds->cdone = 0u;
+  if (tid == 0) {
+    ds->cdone = 0u;
+    g_pl[slot >> 6] |= 1ull << (slot & 63);  // (its pick item takes the rows-planned ticket)
+  }
 }
 
 
@@ -1213,10 +1307,20 @@ __device__ __forceinline__ int pick_item(const ScanArgs &a, int slot, int slice,
       }
     }
   }
-  // Ticket: the row's last slice finishes it (finish_item, called by the kernel's loop).
+  // Ticket: the row's last slice finishes it (finish_item, called by the kernel's loop). With it, for a row this
+  // workgroup planned, the rows-planned ticket (both in flight together).
   store_wait();
   __syncthreads();
-  if (tid == 0) sh.ticket = ticket_add(&ds->pdone);
+  if (tid == 0) {
+    uint32_t t = 0xFFFFFFFFu;
+    const uint64_t pb = 1ull << (slot & 63);
+    if (g_pl[slot >> 6] & pb) {
+      g_pl[slot >> 6] &= ~pb;
+      t = ticket_add(&a.dctl[2]);
+    }
+    sh.ticket = ticket_add(&ds->pdone);
+    if (t == g_nd - 1u) clear_counts(a);
+  }
   __syncthreads();
   if (sh.ticket != (uint32_t)(g.S - 1)) return -1;
   return planned ? slot : -2 - slot;
@@ -1231,6 +1335,7 @@ __device__ __forceinline__ void finish_item(const ScanArgs &a, int fs, PickShare
   const int slot = planned ? fs : -2 - fs;
   DeepSlot *ds = a.dslot + slot;
   __builtin_amdgcn_s_setprio(3);  // (the finish is the row's critical path)
+  if (tid == 0) g_fin = 0u;
   if (planned) {
     const FinArgs fa{a.dlist + (size_t)slot * DCAP, a.info, a.tokens, a.mode};
     if (a.fin_sorted ? finish_sorted(fa, ds, ps.f, etab) != 0 : ld_ag(&ds->spoil) == 0u) {
@@ -1245,6 +1350,7 @@ __device__ __forceinline__ void finish_item(const ScanArgs &a, int fs, PickShare
     ds->lcnt = 0;
     ds->pdone = 0;
     ds->spoil = 0;
+    if (g_fin == 0u) g_fail[slot >> 6] |= 1ull << (slot & 63);  // (the exact path takes the row after the items)
   }
 }
 
@@ -1252,18 +1358,46 @@ __device__ __forceinline__ void finish_item(const ScanArgs &a, int fs, PickShare
 // pick items, so a pick item only waits for count work that never waits itself.
 template <int DT, bool AL>
 __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void deep_kernel(ScanArgs a) {
-  __shared__ PickShared sh;
+  PickShared &sh = g_lds.p;
   __shared__ double etab[64];
-  const int nd = (int)min(a.dctl[0], (uint32_t)a.dslots);
-  if (nd == 0) return;
-  if (threadIdx.x < 64) etab[threadIdx.x] = EXP2_64[threadIdx.x];  // (published by the first barrier of an item)
-  const DGeom g = deep_geom(a, nd);
-  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) count_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab);
-  // one item per workgroup in each pass: the pick item is the count item's slice, whose history tables are still in LDS
-  const bool keep = nd * g.S <= (int)gridDim.x;
-  for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) {
-    const int fs = pick_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab, keep);
-    if (fs != -1) finish_item(a, fs, sh, etab);
+  const int tid = threadIdx.x;
+  const uint64_t cnt = *reinterpret_cast<const uint64_t *>(a.dctl);  // (one load: both counts of one moment)
+  const int nd = __builtin_amdgcn_readfirstlane((int)min((uint32_t)cnt, (uint32_t)a.dslots));  // (uniform)
+  if (tid < DEEP_MAX / 64) {
+    g_fail[tid] = 0ull;
+    g_pl[tid] = 0ull;
+  }
+  if (nd > 0) {
+    if (tid < 64) etab[tid] = EXP2_64[tid];  // (published by the first barrier of an item)
+    const DGeom g = deep_geom(a, nd);
+    if (tid == 0) {  // (kept in LDS, not in registers across the items)
+      g_nd = (uint32_t)nd;
+      g_scan = (uint32_t)(cnt >> 32);
+      g_gs = (uint32_t)min(nd * g.S, (int)gridDim.x);  // (the workgroups with items: every one of them reads the counts)
+    }
+    for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) count_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab);
+    // one item per workgroup in each pass: the pick item is the count item's slice, whose history tables are still in
+    // LDS
+    const bool keep = nd * g.S <= (int)gridDim.x;
+    for (int i = blockIdx.x; i < nd * g.S; i += gridDim.x) {
+      const int fs = pick_item<DT, AL>(a, i / g.S, i % g.S, g, sh, etab, keep);
+      if (fs != -1) finish_item(a, fs, sh, etab);
+    }
+  } else if (tid == 0) {
+    g_nd = 0u;
+    g_scan = (uint32_t)(cnt >> 32);
+    g_gs = gridDim.x;
+  }
+  // the exact rows: the arguments copied into LDS first (the argument segment pointer is the launch's only here, in the
+  // kernel; its one argument lies at the segment's start: a word per thread)
+  __syncthreads();  // (g_fail; LDS of the last item)
+  const bool scan = g_scan != 0u && (int)blockIdx.x < (int)g_gs;
+  if (__syncthreads_or(tid < DEEP_MAX / 64 && g_fail[tid] != 0ull) || scan) {
+    static_assert(sizeof(ScanArgs) % 4 == 0 && sizeof(ScanArgs) / 4 <= MT, "a word per thread");
+    const uint32_t *src = (const uint32_t *)__builtin_amdgcn_kernarg_segment_ptr();  // (an address space cast)
+    if (tid < (int)(sizeof(ScanArgs) / 4)) reinterpret_cast<uint32_t *>(&g_args)[tid] = src[tid];
+    __syncthreads();
+    exact_rows(scan);
   }
 }
 

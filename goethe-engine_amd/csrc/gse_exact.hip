@@ -1,14 +1,16 @@
-// Exact radix-select path: one 1024-thread workgroup per row that the scan marked hard. It finds the keep prefix and
-// the draw of goethe_engine/sampling.py:77-83 without sorting the row:
+// Exact radix-select path: one workgroup per row that the scan marked hard (1024 threads in the exact launch here, 256
+// inside the split-row launch: the same body, gse_exact_body.h, in two shapes). It finds the keep prefix and the draw
+// of goethe_engine/sampling.py:77-83 without sorting the row:
 //
 //   m   = min(top_k, #{q_i >= min_p * q_0}, first rank with cumsum(q)_i - q_i >= top_p)    (sampling.py:80)
 //   j   = first rank with cumsum(q)_i >= u * c_last, c_last = cumsum(q)_{m-1}             (sampling.py:81-83)
 //
 // The head of the row (at most HEADN top elements, cut at a bin of the key histogram that the max pass counts) is
 // collected into LDS and sorted once; a rank / mass query whose answer lies in it is a walk of that list. Any other
-// query walks a 4096-bin histogram of the 32-bit key (count and mass per bin), then collects the one bin that holds
-// the answer into LDS and sorts it; a bin too large to collect is refined with a histogram of its own key range
-// (12 bits per level), and a single key with more elements than fit is ordered by token id (the stable order).
+// query walks a histogram of the 32-bit key (4096 bins, 12 key bits per level; 1024 and 10 in the 256-thread shape;
+// count and mass per bin), then collects the one bin that holds the answer into LDS and sorts it; a bin too large to
+// collect is refined with a histogram of its own key range, and a single key with more elements than fit is ordered
+// by token id (the stable order).
 // Masses are exact sums of per-element fixed-point values (2^-64 resolution), so every prefix is deterministic and
 // the same whichever order the atomics land in.
 #include "gse_rowctx.h"
@@ -17,770 +19,32 @@ namespace gse {
 
 namespace {
 
-constexpr int XT = 1024;         // threads
-constexpr int XW = XT / WAVE;    // waves
-constexpr int NB = 4096;         // histogram bins
-constexpr int CAPS = 8192;       // collected elements
-constexpr int PER = CH / XT;     // tokens per thread per chunk (contiguous)
-
-struct ExactShared {
-  uint32_t cnt[CH];
-  union {
-    struct {
-      uint32_t c[NB];
-      uint64_t hi[NB];
-      uint64_t lo[NB];
-    } h;
-    struct {
-      uint64_t k[CAPS];
-      uint64_t phi[XT];
-      uint64_t plo[XT];
-    } col;
-  } u;
-  uint64_t wred[XW];
-  uint64_t wred2[XW];
-  double dred[XW];
-  uint64_t xs[4];
-  uint32_t n, found;
-};
-
-// Context of the row being finished.
-struct XCtx {
-  const int32_t *hist;
-  RowCtx c;
-  int row, nch;
-  double M, S;
-};
-
-// The logits of tokens t0 .. t0+PER-1 (a thread's run inside a chunk) as raw bits (bf16 zero-extended), loaded
-// together so that the PER loads are in flight at once, and converted only where used (raw_logit), so that a
-// prefetched run is not waited for early; indexes past the row end read its last element (the callers skip those
-// tokens). Returns the mask word of the run (its PER tokens share one: PER divides 32), all ones without a mask.
-// The pointers are global ones: loads through generic pointers would be flat loads, whose completion the compiler
-// cannot count, so that every later use waited for all loads in flight, the next run's included.
-__device__ __forceinline__ uint32_t load_run(const RowCtx &c, int t0, uint32_t (&v)[PER]) {
-  static_assert(32 % PER == 0, "a run shares one mask word");
-  typedef const __attribute__((address_space(1))) uint16_t g16;
-  typedef const __attribute__((address_space(1))) uint32_t g32;
-  if (c.dtype == GSE_BF16) {
-    g16 *p = (g16 *)c.base;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) v[i] = p[min(t0 + i, c.V - 1)];
-  } else {
-    g32 *p = (g32 *)c.base;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) v[i] = p[min(t0 + i, c.V - 1)];
-  }
-  return c.mw ? (t0 < c.V ? ((g32 *)c.mw)[t0 >> 5] : 0u) : 0xFFFFFFFFu;
-}
-
-__device__ __forceinline__ float raw_logit(const RowCtx &c, uint32_t r) {
-  return __uint_as_float(c.dtype == GSE_BF16 ? r << 16 : r);
-}
-
-// Calls f(t, key) for every token of the row, thread-contiguous inside each chunk (ids increase with (tid, i)).
-// The next chunk's run is loaded while the current one is processed (issued after the history counts, whose loads
-// are waited for).
-template <typename F>
-__device__ __forceinline__ void for_each_key(const RowCtx &c, const int32_t *hist, int nch, ExactShared &sh, F f) {
-  const int tid = threadIdx.x;
-  uint32_t v[PER];
-  uint32_t mword = load_run(c, tid * PER, v);
-  for (int ch = 0; ch < nch; ++ch) {
-    const int c0 = ch * CH;
-    const int t0 = c0 + tid * PER;
-    if (c.pen) build_counts(c, hist, c0, sh.cnt);
-    uint32_t vn[PER];
-    const uint32_t mn = load_run(c, ch + 1 < nch ? t0 + CH : t0, vn);
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int t = t0 + i;
-      if (t < c.V) {
-        const uint32_t ct = c.pen ? sh.cnt[t - c0] : 0u;
-        bool fn = false, ff = false;
-        float xm;
-        const uint32_t k = elem_key(c, raw_logit(c, v[i]), ct, (mword >> (t & 31)) & 1u, fn, ff, xm);
-        f(t, k);
-      }
-    }
-    if (c.pen) __syncthreads();
-#pragma unroll
-    for (int i = 0; i < PER; ++i) v[i] = vn[i];
-    mword = mn;
-  }
-}
-
-// The workgroup's LDS, at file scope so that the pass functions below address it as LDS without taking it as an
-// argument (a pointer argument would be a generic one).
+// The 1024-thread shape: the exact launch, for calls without the split-row launch (GSE_BATCH_NO_SPLIT, or a handle
+// without split-row slots). Otherwise the split-row launch finishes the hard rows itself (gse_deep.hip, 256 threads).
+namespace x1024 {
+constexpr int XT = 1024;   // threads
+constexpr int NB = 4096;   // histogram bins
+constexpr int LB = 12;     // key bits per histogram level
+constexpr int CAPS = 8192; // collected elements
+constexpr int CHX = CH;    // tokens per chunk
+#include "gse_exact_body.h"
 __shared__ ExactShared xsh;
-
-// ---- whole-row passes -----------------------------------------------------------------------------------------------
-// Each pass over the row is a function of its own, not inlined, taking the row context by value: its element loop is
-// then register-allocated apart from the finishing code around it. Inlined, the loop reloaded values of that code
-// from private memory (spill slots) inside every element, each reload waited for, at 150-700 us per pass over a
-// 128k-token row.
-
-enum { P_MAX = 0, P_SUM, P_COUNT, P_HIST, P_COLLECT, P_TOP, P_MAXH };
-
-struct PassIn {
-  double M;         // row maximum of z (P_SUM, P_HIST)
-  uint32_t lo, hi;  // key window (P_HIST, P_COLLECT); lo alone: the smallest key counted (P_COUNT)
-  int shift;        // bin width 2^shift keys (P_HIST, P_MAXH)
-  uint64_t pk;      // smallest packed key collected (P_TOP)
-};
-
-struct PassOut {
-  uint64_t u;  // P_MAX: the thread's largest packed key; P_COUNT: its count
-  double d;    // P_SUM: the thread's sum of exp(z - M), in token order
-};
-
-// Every thread of the workgroup calls it. P_HIST adds counts and fixed-point masses to the histogram bins (P_MAXH:
-// P_MAX that also counts every key into the bins, masses left alone), P_COLLECT
-// and P_TOP append packed keys at xsh.n (the callers clear the bins and the count first and synchronise afterwards).
-template <int OP>
-__device__ __noinline__ PassOut row_pass(const RowCtx c, const int32_t *hist, int nch, const PassIn in) {
-  ExactShared &sh = xsh;
-  uint64_t u = 0;
-  double d = 0.0;
-  for_each_key(c, hist, nch, sh, [&](int t, uint32_t k) {
-    if constexpr (OP == P_MAX || OP == P_MAXH) {
-      const uint64_t p = pack(k, (uint32_t)t);
-      u = p > u ? p : u;
-      if constexpr (OP == P_MAXH) atomicAdd(&sh.u.h.c[k >> in.shift], 1u);
-    } else if constexpr (OP == P_SUM) {
-      d += k > KEY_NEGINF ? exp((double)fkey_inv(k) - in.M) : 0.0;
-    } else if constexpr (OP == P_COUNT) {
-      u += k >= in.lo ? 1u : 0u;
-    } else if constexpr (OP == P_HIST) {
-      if (k >= in.lo && k <= in.hi) {
-        const int b = (int)((k - in.lo) >> in.shift);
-        atomicAdd(&sh.u.h.c[b], 1u);
-        if (k > KEY_NEGINF) {
-          const Fx f = fx_of(exp((double)fkey_inv(k) - in.M));
-          if (f.hi) atomicAdd((unsigned long long *)&sh.u.h.hi[b], (unsigned long long)f.hi);
-          if (f.lo) atomicAdd((unsigned long long *)&sh.u.h.lo[b], (unsigned long long)f.lo);
-        }
-      }
-    } else if constexpr (OP == P_COLLECT) {
-      if (k >= in.lo && k <= in.hi) {
-        const uint32_t pos = atomicAdd(&sh.n, 1u);
-        if (pos < (uint32_t)CAPS) sh.u.col.k[pos] = pack(k, (uint32_t)t);
-      }
-    } else {
-      const uint64_t p = pack(k, (uint32_t)t);
-      if (p >= in.pk) {
-        const uint32_t pos = atomicAdd(&sh.n, 1u);
-        if (pos < (uint32_t)CAPS) sh.u.col.k[pos] = p;
-      }
-    }
-  });
-  return PassOut{u, d};
-}
-
-template <int OP>
-__device__ __forceinline__ PassOut pass(const XCtx &x, const PassIn &in) {
-  return row_pass<OP>(x.c, x.hist, x.nch, in);
-}
-
-// ---- block reductions / scans (1024 threads) ------------------------------------------------------------------------
-
-__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, ExactShared &sh) {
-  v = wave_max_u64(v);
-  __syncthreads();
-  if (lane_id() == 0) sh.wred[threadIdx.x >> 6] = v;
-  __syncthreads();
-  uint64_t r = 0;
-  for (int w = 0; w < XW; ++w) r = sh.wred[w] > r ? sh.wred[w] : r;
-  __syncthreads();
-  return r;
-}
-
-
-__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, ExactShared &sh) {
-  v = wave_sum_u64(v);
-  __syncthreads();
-  if (lane_id() == 0) sh.wred[threadIdx.x >> 6] = v;
-  __syncthreads();
-  uint64_t r = 0;
-  for (int w = 0; w < XW; ++w) r += sh.wred[w];
-  __syncthreads();
-  return r;
-}
-
-// Deterministic block sum: wave tree, then waves in order.
-__device__ __forceinline__ double block_sum_f64(double v, ExactShared &sh) {
-  v = wave_sum_f64(v);
-  __syncthreads();
-  if (lane_id() == 0) sh.dred[threadIdx.x >> 6] = v;
-  __syncthreads();
-  double r = 0.0;
-  for (int w = 0; w < XW; ++w) r += sh.dred[w];
-  __syncthreads();
-  return r;
-}
-
-
-// Exclusive block scan of two u64 values per thread (in thread order).
-__device__ __forceinline__ void block_excl_scan2(uint64_t &a, uint64_t &b, ExactShared &sh) {
-  const uint64_t ia = wave_incl_scan_u64(a), ib = wave_incl_scan_u64(b);
-  __syncthreads();
-  if (lane_id() == WAVE - 1) {
-    sh.wred[threadIdx.x >> 6] = ia;
-    sh.wred2[threadIdx.x >> 6] = ib;
-  }
-  __syncthreads();
-  uint64_t pa = 0, pb = 0;
-  const int w = threadIdx.x >> 6;
-  for (int k = 0; k < w; ++k) {
-    pa += sh.wred[k];
-    pb += sh.wred2[k];
-  }
-  a = pa + ia - a;
-  b = pb + ib - b;
-  __syncthreads();
-}
-
-// ---- histogram over a key window --------------------------------------------------------------------------------------
-
-struct Win {
-  uint32_t lo, hi;   // key range of the window (inclusive)
-  int shift;         // bin width 2^shift keys
-  uint64_t above_n;  // elements with key above the window
-  Fx above_m;        // their mass
-};
-
-// Builds counts and masses of the keys inside the window.
-__device__ void build_hist(const XCtx &x, ExactShared &sh, const Win &w) {
-  for (int b = threadIdx.x; b < NB; b += XT) {
-    sh.u.h.c[b] = 0;
-    sh.u.h.hi[b] = 0;
-    sh.u.h.lo[b] = 0;
-  }
-  __syncthreads();
-  pass<P_HIST>(x, PassIn{x.M, w.lo, w.hi, w.shift, 0});
-  __syncthreads();
-}
-
-// Query kinds: rank (0-based) / first rank whose exclusive mass >= target / first rank whose inclusive mass >= target.
-enum { Q_RANK = 0, Q_EXCL = 1, Q_INCL = 2 };
-
-struct Hit {
-  int64_t rank;    // rank of the answer element (V when no element qualifies)
-  uint64_t pk;     // its packed key (0 when none)
-  Fx above;        // mass of all elements ranked before it
-  Fx self;         // its own mass
-};
-
-__device__ __forceinline__ bool q_pred(int kind, uint64_t r, int64_t n_before, Fx m_before, Fx m_incl, double S,
-                                       double tgt) {
-  if (kind == Q_RANK) return (int64_t)r < n_before;
-  if (kind == Q_EXCL) return fx_val(m_before) / S >= tgt;
-  return fx_val(m_incl) / S >= tgt;
-}
-
-// Finds, in the current histogram (descending bins), the first bin whose inclusive prefix satisfies the query.
-// Returns -1 when none does; fills the window-relative prefix before that bin.
-__device__ int find_bin(ExactShared &sh, const Win &w, int kind, uint64_t r, double S, double tgt, uint64_t &nb_out,
-                        Fx &mb_out) {
-  // thread t owns 4 consecutive bins in descending order: NB-1-4t ... NB-4-4t
-  const int tid = threadIdx.x;
-  uint64_t n4 = 0, h4 = 0, l4 = 0;
-  for (int i = 0; i < 4; ++i) {
-    const int b = NB - 1 - (4 * tid + i);
-    n4 += sh.u.h.c[b];
-    h4 += sh.u.h.hi[b];
-    l4 += sh.u.h.lo[b];
-  }
-  uint64_t pn = n4, ph = h4;
-  block_excl_scan2(pn, ph, sh);
-  uint64_t pl = l4, dummy = 0;
-  block_excl_scan2(pl, dummy, sh);
-  if (tid == 0) sh.found = 0xFFFFFFFFu;
-  __syncthreads();
-  uint64_t n = w.above_n + pn;
-  Fx m = fx_add(w.above_m, Fx{ph, pl});
-  for (int i = 0; i < 4; ++i) {
-    const int b = NB - 1 - (4 * tid + i);
-    const uint64_t cb = sh.u.h.c[b];
-    const Fx mb{sh.u.h.hi[b], sh.u.h.lo[b]};
-    const Fx mi = fx_add(m, mb);
-    bool hit;
-    if (kind == Q_RANK) hit = r < n + cb;
-    else if (kind == Q_EXCL) hit = cb > 0 && fx_val(mi) / S >= tgt;
-    else hit = cb > 0 && fx_val(mi) / S >= tgt;
-    if (hit) {
-      atomicMin(&sh.found, (uint32_t)(4 * tid + i));
-      break;
-    }
-    n += cb;
-    m = mi;
-  }
-  __syncthreads();
-  const uint32_t f = sh.found;
-  __syncthreads();
-  if (f == 0xFFFFFFFFu) return -1;
-  // recompute the prefix before bin index f (descending index) on one thread and broadcast
-  if (tid == (int)(f >> 2)) {
-    uint64_t nn = w.above_n + pn;
-    Fx mm = fx_add(w.above_m, Fx{ph, pl});
-    for (uint32_t i = 0; i < (f & 3u); ++i) {
-      const int b = NB - 1 - (int)(4 * (f >> 2) + i);
-      nn += sh.u.h.c[b];
-      mm = fx_add(mm, Fx{sh.u.h.hi[b], sh.u.h.lo[b]});
-    }
-    sh.xs[0] = nn;
-    sh.xs[1] = mm.hi;
-    sh.xs[2] = mm.lo;
-  }
-  __syncthreads();
-  nb_out = sh.xs[0];
-  mb_out = Fx{sh.xs[1], sh.xs[2]};
-  __syncthreads();
-  return NB - 1 - (int)f;
-}
-
-// Collects the packed keys of every element with key in [klo, khi] into LDS (sorted descending). Returns the count
-// (possibly above CAPS: then the list is partial).
-__device__ uint32_t collect(const XCtx &x, ExactShared &sh, uint32_t klo, uint32_t khi) {
-  if (threadIdx.x == 0) sh.n = 0;
-  __syncthreads();
-  pass<P_COLLECT>(x, PassIn{0.0, klo, khi, 0, 0});
-  __syncthreads();
-  const uint32_t n = sh.n;
-  if (n <= (uint32_t)CAPS) {
-    const int np2 = pow2_ceil(max((int)n, 2));
-    for (int i = (int)n + threadIdx.x; i < np2; i += XT) sh.u.col.k[i] = 0;
-    __syncthreads();
-    block_sort_desc_u64(sh.u.col.k, np2);
-  }
-  return n;
-}
-
-// Walks a collected, sorted list (n <= CAPS) for the query, with n_before / m_before the prefix above the list.
-// Returns the index inside the list (or n when no element qualifies) and fills the element's prefix mass.
-__device__ int walk_list(const XCtx &x, ExactShared &sh, int n, int kind, uint64_t r, uint64_t n_before, Fx m_before,
-                         double tgt, Fx &above, Fx &self) {
-  const int tid = threadIdx.x;
-  constexpr int PT = CAPS / XT;  // 8 elements per thread, consecutive
-  Fx ef[PT];
-  const double M = x.M;
-  uint64_t sh_hi = 0, sh_lo = 0;
-  for (int i = 0; i < PT; ++i) {
-    const int idx = tid * PT + i;
-    ef[i] = Fx{0, 0};
-    if (idx < n) {
-      const uint32_t k = pk_key(sh.u.col.k[idx]);
-      if (k > KEY_NEGINF) ef[i] = fx_of(exp((double)fkey_inv(k) - M));
-    }
-    sh_hi += ef[i].hi;
-    sh_lo += ef[i].lo;
-  }
-  block_excl_scan2(sh_hi, sh_lo, sh);
-  if (tid == 0) sh.found = 0xFFFFFFFFu;
-  __syncthreads();
-  Fx m = fx_add(m_before, Fx{sh_hi, sh_lo});
-  for (int i = 0; i < PT; ++i) {
-    const int idx = tid * PT + i;
-    if (idx >= n) break;
-    const Fx mi = fx_add(m, ef[i]);
-    if (q_pred(kind, r, (int64_t)n_before + idx + 1, m, mi, x.S, tgt)) {
-      atomicMin(&sh.found, (uint32_t)idx);
-      break;
-    }
-    m = mi;
-  }
-  __syncthreads();
-  const uint32_t f = sh.found;
-  __syncthreads();
-  if (f == 0xFFFFFFFFu) return n;
-  if (tid == (int)(f / PT)) {
-    Fx mm = fx_add(m_before, Fx{sh_hi, sh_lo});
-    for (uint32_t i = 0; i < f % PT; ++i) mm = fx_add(mm, ef[i]);
-    sh.xs[0] = mm.hi;
-    sh.xs[1] = mm.lo;
-    sh.xs[2] = ef[f % PT].hi;
-    sh.xs[3] = ef[f % PT].lo;
-  }
-  __syncthreads();
-  above = Fx{sh.xs[0], sh.xs[1]};
-  self = Fx{sh.xs[2], sh.xs[3]};
-  __syncthreads();
-  return (int)f;
-}
-
-// Elements sharing one key, taken in token-id order: the token at position p (0-based) among them.
-__device__ uint32_t nth_with_key(const XCtx &x, ExactShared &sh, uint32_t key, uint64_t p) {
-  const int tid = threadIdx.x;
-  uint64_t base = 0;
-  if (tid == 0) sh.found = 0xFFFFFFFFu;
-  __syncthreads();
-  const RowCtx c = x.c;
-  const int32_t *hist = x.hist;
-  const int nch = x.nch;
-  for (int ch = 0; ch < nch; ++ch) {
-    const int c0 = ch * CH;
-    if (c.pen) build_counts(c, hist, c0, sh.cnt);
-    const int t0 = c0 + tid * PER;
-    uint32_t v[PER];
-    const uint32_t mword = load_run(c, t0, v);
-    uint32_t match = 0;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int t = t0 + i;
-      if (t < c.V) {
-        const uint32_t ct = c.pen ? sh.cnt[t - c0] : 0u;
-        bool fn = false, ff = false;
-        float xm;
-        if (elem_key(c, raw_logit(c, v[i]), ct, (mword >> (t & 31)) & 1u, fn, ff, xm) == key) match |= 1u << i;
-      }
-    }
-    uint64_t cntm = (uint64_t)__popc(match), d = 0;
-    block_excl_scan2(cntm, d, sh);
-    const uint64_t total = block_sum_u64((uint64_t)__popc(match), sh);
-    const uint64_t mine = base + cntm;
-    if (p >= mine && p < mine + (uint64_t)__popc(match)) {
-      uint32_t left = (uint32_t)(p - mine), mm = match;
-      for (int i = 0; i < PER; ++i) {
-        if (mm & (1u << i)) {
-          if (left == 0) {
-            sh.found = (uint32_t)(t0 + i);
-            break;
-          }
-          --left;
-        }
-      }
-    }
-    base += total;
-    if (x.c.pen) __syncthreads();
-    __syncthreads();
-    if (sh.found != 0xFFFFFFFFu) break;
-  }
-  __syncthreads();
-  return sh.found;
-}
-
-// Runs one query to its element: histogram levels, collection, walk.
-__device__ Hit query(const XCtx &x, ExactShared &sh, int kind, uint64_t r, double tgt) {
-  Hit out;
-  Win w{0u, 0xFFFFFFFFu, 20, 0, Fx{0, 0}};
-  for (int level = 0; level < 3; ++level) {
-    build_hist(x, sh, w);
-    uint64_t nb = 0;
-    Fx mb{0, 0};
-    const int b = find_bin(sh, w, kind, r, x.S, tgt, nb, mb);
-    if (b < 0) {
-      out.rank = -1;
-      out.pk = 0;
-      return out;
-    }
-    const uint64_t cb = sh.u.h.c[b];
-    const uint32_t klo = w.lo + ((uint32_t)b << w.shift);
-    const uint32_t khi = w.shift == 0 ? klo : klo + ((1u << w.shift) - 1u);
-    __syncthreads();
-    if (cb <= (uint64_t)CAPS) {
-      const uint32_t n = collect(x, sh, klo, khi);
-      Fx above, self;
-      const int i = walk_list(x, sh, (int)n, kind, r, nb, mb, tgt, above, self);
-      if (i >= (int)n) {  // no element of the bin qualifies (exclusive mass): the answer is the next bin's first
-        out.rank = (int64_t)(nb + n);
-        out.pk = 0;
-        return out;
-      }
-      out.rank = (int64_t)(nb + i);
-      out.pk = sh.u.col.k[i];
-      out.above = above;
-      out.self = self;
-      __syncthreads();
-      return out;
-    }
-    if (w.shift == 0) {
-      // one key with more elements than fit: equal z, equal mass; the answer is positional in token-id order
-      const uint32_t k = klo;
-      const Fx e = k > KEY_NEGINF ? fx_of(exp((double)fkey_inv(k) - x.M)) : Fx{0, 0};
-      uint64_t pos;
-      if (kind == Q_RANK) {
-        pos = r - nb;
-      } else {
-        // smallest p with (before + p * e (+ e)) / S >= tgt; the bin holds the answer so p < cb
-        uint64_t lo = 0, hi = cb - 1;
-        while (lo < hi) {
-          const uint64_t mid = (lo + hi) / 2;
-          const Fx mp = fx_add(mb, Fx{e.hi * (mid + (kind == Q_INCL)), e.lo * (mid + (kind == Q_INCL))});
-          if (fx_val(mp) / x.S >= tgt) hi = mid;
-          else lo = mid + 1;
-        }
-        pos = lo;
-      }
-      const uint32_t t = nth_with_key(x, sh, k, pos);
-      out.rank = (int64_t)(nb + pos);
-      out.pk = pack(k, t);
-      out.above = fx_add(mb, Fx{e.hi * pos, e.lo * pos});
-      out.self = e;
-      return out;
-    }
-    w = Win{klo, khi, w.shift > 12 ? w.shift - 12 : 0, nb, mb};
-  }
-  out.rank = -1;
-  out.pk = 0;
-  return out;
-}
-
-// Level-0 bins (2^HS keys each) of the head's histogram, which the max pass counts.
-constexpr int HS = 20;
-// Elements of the head, at most: the cut is the level-0 bin that holds this rank. Smaller heads sort faster; a query
-// whose answer ranks below the head runs its own levels (forced exact, 16 rows: 2048 measured 12% faster than 8192
-// on C3 rows, 37% on C1 rows).
-constexpr int HEADN = 2048;
-static_assert(HEADN <= CAPS, "the head fits the list area");
-static_assert((0xFFFFFFFFu >> HS) < (uint32_t)NB, "the level-0 bins cover every key");
-
-// The head of the row: every element above the level-0 histogram bin that holds rank HEADN (every element when the row
-// has at most HEADN), collected and sorted descending in the list area; kcut receives the smallest key it covers
-// completely (every element with a key >= kcut is in the head). Returns its length, 0 when the top bin alone holds
-// more than HEADN elements. Expects the level-0 counts of every key in the histogram (the max pass, P_MAXH), masses
-// zero: the cut is a rank. A query answered inside the head is a walk of the list; query() reuses the LDS, after
-// which the head is gone.
-__device__ uint32_t collect_head(const XCtx &x, ExactShared &sh, uint32_t &kcut) {
-  const Win w{0u, 0xFFFFFFFFu, HS, 0, Fx{0, 0}};
-  uint64_t nb = 0;
-  Fx mb{0, 0};
-  const int b = find_bin(sh, w, Q_RANK, (uint64_t)HEADN, x.S, 0.0, nb, mb);
-  if (b == NB - 1) return 0;
-  kcut = b < 0 ? 0u : (uint32_t)(b + 1) << w.shift;
-  __syncthreads();
-  return collect(x, sh, kcut, 0xFFFFFFFFu);
-}
-
-// A query answered from the head of n elements: false when no element of the head satisfies it (the answer, if any,
-// ranks at n or below).
-__device__ bool head_query(const XCtx &x, ExactShared &sh, uint32_t n, int kind, uint64_t r, double tgt, Hit &h) {
-  Fx above, self;
-  const int i = walk_list(x, sh, (int)n, kind, r, 0, Fx{0, 0}, tgt, above, self);
-  if (i >= (int)n) return false;
-  h.rank = i;
-  h.pk = sh.u.col.k[i];
-  h.above = above;
-  h.self = self;
-  __syncthreads();
-  return true;
-}
-
-__device__ uint64_t count_ge(const XCtx &x, ExactShared &sh, uint32_t kmin) {
-  return block_sum_u64(pass<P_COUNT>(x, PassIn{0.0, kmin, 0, 0, 0}).u, sh);
-}
-
-// Collects the elements with packed key >= pk (the top ranks) and sorts them.
-__device__ uint32_t collect_top(const XCtx &x, ExactShared &sh, uint64_t pk) {
-  if (threadIdx.x == 0) sh.n = 0;
-  __syncthreads();
-  pass<P_TOP>(x, PassIn{0.0, 0, 0, 0, pk});
-  __syncthreads();
-  const uint32_t n = min(sh.n, (uint32_t)CAPS);
-  const int np2 = pow2_ceil(max((int)n, 2));
-  for (int i = (int)n + threadIdx.x; i < np2; i += XT) sh.u.col.k[i] = 0;
-  __syncthreads();
-  block_sort_desc_u64(sh.u.col.k, np2);
-  return n;
-}
-
-// Finishes one hard row (every thread of the workgroup calls it; its LDS is free again when it returns).
-__device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShared &sh) {
-  RowInfo *ri = a.info + row;
-  const int tid = threadIdx.x;
-  const gse_row P = a.params[row];
-  const bool greedy = is_greedy(a.mode, P);
-  XCtx x;
-  x.hist = a.hist;
-  x.row = row;
-  x.nch = a.nch;
-  x.c = make_ctx(a, row, P);
-  if (greedy) {  // logprobs of a greedy row are taken over z = x
-    x.c.greedy = false;
-    x.c.divide = false;
-  }
-  const int nlp = a.lp_ids ? min(min(P.logprobs, GSE_MAX_LOGPROBS), (int)a.lp_ld) : 0;
-  if (ri->flags & R_FULL) {
-    // the main pass could not count the history: recompute the row flags and, for a greedy row, the argmax
-    // (first maximum of nan_to_num of the masked logits, sampling.py:70-76)
-    RowCtx gc = make_ctx(a, row, P);
-    bool fnan = false, ffin = false;
-    uint64_t gb = 0;
-    const int nch = a.nch;
-    for (int ch = 0; ch < nch; ++ch) {
-      const int c0 = ch * CH;
-      if (gc.pen) build_counts(gc, a.hist, c0, sh.cnt);
-      const int t0 = c0 + tid * PER;
-      uint32_t v[PER];
-      const uint32_t mword = load_run(gc, t0, v);
-#pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const int t = t0 + i;
-        if (t < gc.V) {
-          float xm;
-          const uint32_t k =
-              elem_key(gc, raw_logit(gc, v[i]), gc.pen ? sh.cnt[t - c0] : 0u, (mword >> (t & 31)) & 1u, fnan, ffin, xm);
-          const uint64_t p = pack(k, (uint32_t)t);
-          gb = p > gb ? p : gb;
-        }
-      }
-      if (gc.pen) __syncthreads();
-    }
-    gb = block_max_u64(gb, sh);
-    const bool anynan = block_sum_u64(fnan ? 1u : 0u, sh) != 0;
-    const bool anyfin = block_sum_u64(ffin ? 1u : 0u, sh) != 0;
-    const bool bad = anynan || !anyfin;
-    if (a.mode == MODE_SAMPLE && (bad || greedy)) {
-      const int32_t tok = bad ? -1 : (int32_t)pk_id(gb);
-      if (tid == 0) a.tokens[row] = tok;
-      if (bad || !nlp) {
-        for (int i = tid; i < nlp; i += XT) {
-          a.lp_ids[(int64_t)row * a.lp_ld + i] = -1;
-          a.lps[(int64_t)row * a.lp_ld + i] = __builtin_nanf("");
-        }
-        if (tid == 0) ri->flags = R_DONE | R_BY_EXACT | (bad ? R_BAD : 0u) | (greedy ? R_GREEDY : 0u);
-        return;
-      }
-    } else if (anynan) {  // dist of a NaN row is NaN everywhere
-      if (tid == 0) ri->flags = R_DONE | R_BY_EXACT | R_SPECIAL;
-      return;
-    }
-  }
-  // pass 0: the row maximum of z
-  // (with the level-0 counts of the head when a query will need it)
-  const bool want_head = !greedy || nlp > 0;
-  if (want_head) {
-    for (int b = tid; b < NB; b += XT) {
-      sh.u.h.c[b] = 0;
-      sh.u.h.hi[b] = 0;
-      sh.u.h.lo[b] = 0;
-    }
-    __syncthreads();
-  }
-  const PassIn pin{0.0, 0u, 0xFFFFFFFFu, HS, 0};
-  uint64_t best = block_max_u64((want_head ? pass<P_MAXH>(x, pin) : pass<P_MAX>(x, pin)).u, sh);
-  const uint32_t mk = pk_key(best);
-  if (mk >= KEY_POSINF || mk <= KEY_NEGINF) {
-    for (int i = tid; i < nlp; i += XT) {
-      a.lp_ids[(int64_t)row * a.lp_ld + i] = -1;
-      a.lps[(int64_t)row * a.lp_ld + i] = __builtin_nanf("");
-    }
-    if (tid == 0) {
-      // z holds +inf or its maximum is -inf: token = order[0], the lowest id at the maximum key (sampling.py:82)
-      ri->cmax = best;
-      ri->flags = R_DONE | R_BY_EXACT | R_SPECIAL | (greedy ? R_GREEDY : 0u);
-      if (a.mode == MODE_SAMPLE && !greedy) a.tokens[row] = (int32_t)pk_id(best);
-    }
-    return;
-  }
-  x.M = (double)fkey_inv(mk);
-  // pass A: S (fixed thread order, deterministic)
-  x.S = block_sum_f64(pass<P_SUM>(x, PassIn{x.M, 0, 0, 0, 0}).d, sh);
-  const double S = x.S;
-  const int64_t V = a.V;
-
-  // The head serves the queries below whose answers rank inside it; nh = 0 once a query has run its own levels.
-  uint32_t kcut = 0, nh = 0;
-  if (want_head) nh = collect_head(x, sh, kcut);
-  if (!greedy) {
-    const double q0 = 1.0 / S;
-    int64_t m = V;
-    if (P.top_k > 0 && P.top_k < m) m = P.top_k;
-    if (P.min_p > 0.0) {
-      // smallest key whose q passes q >= min_p * q_0 (monotone in the key), then count the keys above it
-      const double thr = P.min_p * q0;
-      uint32_t lo = KEY_NEGINF + 1u, hi = mk;
-      while (lo < hi) {
-        const uint32_t mid = lo + (hi - lo) / 2;
-        if (exp((double)fkey_inv(mid) - x.M) / S >= thr) hi = mid;
-        else lo = mid + 1;
-      }
-      int64_t mm;
-      if (nh > 0 && lo >= kcut) {  // every key >= lo is in the head
-        uint64_t c = 0;
-        for (int i = tid; i < (int)nh; i += XT) c += pk_key(sh.u.col.k[i]) >= lo ? 1u : 0u;
-        mm = (int64_t)block_sum_u64(c, sh);
-      } else {
-        mm = (int64_t)count_ge(x, sh, lo);
-      }
-      if (mm < m) m = mm;
-    }
-    {
-      // An answer at rank m or below leaves m as it is: with m <= nh, one not in the head needs no search.
-      Hit hp;
-      if (nh > 0 && head_query(x, sh, nh, Q_EXCL, 0, P.top_p, hp)) {
-        if (hp.rank < m) m = hp.rank;
-      } else if (!(nh > 0 && m <= (int64_t)nh)) {
-        nh = 0;
-        hp = query(x, sh, Q_EXCL, 0, P.top_p);
-        if (hp.rank >= 0 && hp.rank < m) m = hp.rank;
-      }
-    }
-    if (m < 1) m = 1;
-    Hit hl;
-    if (!(m <= (int64_t)nh && head_query(x, sh, nh, Q_RANK, (uint64_t)(m - 1), 0.0, hl))) {
-      nh = 0;
-      hl = query(x, sh, Q_RANK, (uint64_t)(m - 1), 0.0);
-    }
-    const double clast = fx_val(fx_add(hl.above, hl.self)) / S;
-    int32_t tok = -1;
-    if (a.mode == MODE_SAMPLE) {
-      const double u = a.uni ? a.uni[row] : uniform64(P.seed, P.idx);
-      const double thr = u * clast;
-      Hit hj;
-      if (!(nh > 0 && head_query(x, sh, nh, Q_INCL, 0, thr, hj))) {
-        nh = 0;
-        hj = query(x, sh, Q_INCL, 0, thr);
-      }
-      if (hj.rank < 0 || hj.rank > m - 1) hj = hl;  // j = min(count, keep.sum() - 1)
-      tok = (int32_t)pk_id(hj.pk);
-    }
-    if (tid == 0) {
-      RowInfo r = {};
-      r.cmax = best;
-      r.kkeep = hl.pk;
-      r.S = S;
-      r.Z = clast;
-      r.flags = R_DONE | R_BY_EXACT;
-      r.token = tok;
-      if (a.mode == MODE_SAMPLE) a.tokens[row] = tok;
-      *ri = r;
-    }
-  } else if (tid == 0) {
-    ri->flags = R_DONE | R_BY_EXACT | R_GREEDY;
-  }
-  if (nlp > 0) {
-    const int n_top = (int)min((int64_t)nlp, V);
-    uint32_t n = (uint32_t)n_top;  // the first n_top elements of the head, when it holds them
-    if (n_top > (int)nh) {
-      const Hit hn = query(x, sh, Q_RANK, (uint64_t)(n_top - 1), 0.0);
-      n = collect_top(x, sh, hn.pk);
-    }
-    const double lS = log(S);
-    for (int i = tid; i < nlp; i += XT) {
-      int32_t id = -1;
-      float lp = __builtin_nanf("");
-      if (i < (int)n) {
-        const uint64_t pk = sh.u.col.k[i];
-        id = (int32_t)pk_id(pk);
-        const uint32_t k = pk_key(pk);
-        lp = k > KEY_NEGINF ? (float)(((double)fkey_inv(k) - x.M) - lS) : -INFINITY;
-      }
-      a.lp_ids[(int64_t)row * a.lp_ld + i] = id;
-      a.lps[(int64_t)row * a.lp_ld + i] = lp;
-    }
-  }
-}
+__device__ __forceinline__ ExactShared &xs() { return xsh; }
+}  // namespace x1024
+using namespace x1024;
 
 constexpr int XGRID = 256;  // workgroups of the exact pass, at most (one per CU; every row when all are forced)
 
-// The exact pass: with GSE_BATCH_EXACT one workgroup per row; otherwise a small grid, workgroup g owning the rows
-// r = g (mod grid): it finds its hard ones (those the main pass and the split-row finish left: one scan of their flags,
-// compacted in row order) and finishes them, so that a call with no hard row costs a launch and one round of loads.
+// The exact pass, launched when the split-row launch is not (GSE_BATCH_NO_SPLIT, GSE_BATCH_EXACT): with
+// GSE_BATCH_EXACT one workgroup per row; otherwise a small grid, workgroup g owning the rows r = g (mod grid): it finds
+// its hard ones (one scan of their flags, compacted in row order) and finishes them, so that a call with no hard row
+// costs a launch and one round of loads.
 __global__ __launch_bounds__(XT) void exact_kernel(ScanArgs a) {
   ExactShared &sh = xsh;
   __shared__ uint32_t wn[XT / WAVE];
   __shared__ int hrow[XT];
-  if (blockIdx.x == 0 && threadIdx.x == 0) a.dctl[0] = 0u;  // the deep rows of this call are finished
+  // (the call's counts, deep rows and other hard rows, cleared for the next call)
+  if (blockIdx.x == 0 && threadIdx.x == 0) *reinterpret_cast<uint64_t *>(a.dctl) = 0ull;
   const int G = (int)gridDim.x, w = threadIdx.x / WAVE;
   // A workgroup with no hard row ends here, before the set-up of the row code (its registers and spill slots).
   bool any = false;

@@ -134,7 +134,7 @@ struct ScanArgs {
   RowInfo *info;
   uint32_t *done;   // [rows] slice tickets, zero between calls
   // split-row finish
-  uint32_t *dctl;    // [0]: deep rows taken by this call (reset by the exact pass)
+  uint32_t *dctl;    // [0..1]: the call's counts, one 64-bit word (low: deep rows; high: other hard rows); [2], [3]: tickets
   DeepSlot *dslot;   // [DEEP_MAX]
   uint64_t *dhist;   // [DEEP_MAX][3][DNB]: per bin, element count and exact mass (2^-40 and 2^-64 parts), atomic adds
   uint64_t *dlist;   // [DEEP_MAX][DCAP]: packed keys of the window elements

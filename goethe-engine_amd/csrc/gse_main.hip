@@ -105,6 +105,14 @@ __device__ __forceinline__ void set_info(RowInfo *ri, uint64_t cmax, uint64_t kk
   *ri = r;
 }
 
+// A hard row's info; a row that the split-row finish does not take (no R_DEEP) is also counted, so that the split-row
+// launch looks for such rows (its exact rows).
+__device__ __forceinline__ void set_hard(const ScanArgs &a, RowInfo *ri, uint64_t cmax, double S, uint32_t flags,
+                                         int32_t token) {
+  set_info(ri, cmax, 0, S, 0.0, flags, token);
+  if (!(flags & R_DEEP)) atomicAdd(reinterpret_cast<unsigned long long *>(a.dctl), 1ull << 32);
+}
+
 // ---------------------------------------------------------------------------------------------------------------------
 // Row resolve, run by the last workgroup of the row.
 
@@ -334,7 +342,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
       (((flags & F_PINF) || (divide && !(flags & F_FINITE))) && !(flags & F_NAN))) {
     // more distinct history ids than a part can count, or a maximum of z that is not finite (the parts do not know
     // whether a finite x exists): the exact path redoes the whole row (flags, argmax, logprobs)
-    if (tid == 0) set_info(ri, gtop, 0, 0.0, 0.0, R_HARD | R_FULL | (greedy ? R_GREEDY : 0u), -1);
+    if (tid == 0) set_hard(a, ri, gtop, 0.0, R_HARD | R_FULL | (greedy ? R_GREEDY : 0u), -1);
     return;
   }
   if (a.mode == MODE_SAMPLE && (greedy || bad)) {
@@ -366,7 +374,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
     // maximum that is not finite) the exact path redoes the row
     if (tid == 0) {
       if (finite_max && !(flags & F_HOVER)) set_info(ri, pack(mk, 0u), 0ull, 0.0, 0.0, R_DONE, -1);
-      else set_info(ri, gtop, 0, 0.0, 0.0, R_HARD | R_FULL, -1);
+      else set_hard(a, ri, gtop, 0.0, R_HARD | R_FULL, -1);
     }
     return;
   }
@@ -468,7 +476,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
     const bool hard = (flags & (F_OVERFLOW | F_HOVER)) || a.force_exact;
     if (tid == 0) {
       if (hard) {
-        set_info(ri, t, 0, 0.0, 0.0, R_HARD | (greedy ? R_GREEDY : 0u), -1);
+        set_hard(a, ri, t, 0.0, R_HARD | (greedy ? R_GREEDY : 0u), -1);
       } else {
         set_info(ri, t, 0, 0.0, 0.0, R_DONE | R_SPECIAL | (greedy ? R_GREEDY : 0u), (int32_t)pk_id(t));
         if (a.mode == MODE_SAMPLE && !greedy) a.tokens[row] = (int32_t)pk_id(t);
@@ -523,7 +531,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
       // (the split-row finish recomputes z and every mass itself: overflowing wave lists do not matter to it)
       const bool deep = a.dslices > 0 && !greedy && !(flags & F_HOVER) && !a.force_exact && (nlp == 0 || sh.lpw);
       if (deep) {
-        const uint32_t slot = atomicAdd(a.dctl, 1u);
+        const uint32_t slot = (uint32_t)atomicAdd(reinterpret_cast<unsigned long long *>(a.dctl), 1ull);
         if (slot < (uint32_t)a.dslots) {
           DeepSlot *ds = a.dslot + slot;
           ds->P = P;
@@ -536,7 +544,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
       }
       // cmax: the greedy argmax, or the packed maximum of z (always listed) that the split-row finish reads
       const uint64_t zmax = pk_key(sh.rtopL) == mk ? sh.rtopL : pack(mk, 0u);  // (a list overflow may drop it)
-      set_info(ri, greedy ? gtop : zmax, 0, ev.S, 0.0, fl, greedy ? (int32_t)pk_id(gtop) : -1);
+      set_hard(a, ri, greedy ? gtop : zmax, ev.S, fl, greedy ? (int32_t)pk_id(gtop) : -1);
     }
   }
 }

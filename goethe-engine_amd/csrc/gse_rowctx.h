@@ -48,13 +48,15 @@ __device__ __forceinline__ float load_one(const RowCtx &c, int t) {
   return ((const float *)c.base)[t];
 }
 
-// Rebuilds the LDS count table cnt[0, CH) for tokens [c0, c0 + CH) from the row's history. Ends with a barrier.
+// Rebuilds the LDS count table cnt[0, N) for tokens [c0, c0 + N) from the row's history. Ends with a barrier.
+template <int N = CH>
 __device__ __forceinline__ void build_counts(const RowCtx &c, const int32_t *hist, int c0, uint32_t *cnt) {
-  for (int i = threadIdx.x; i < CH / 4; i += blockDim.x) reinterpret_cast<uint4 *>(cnt)[i] = make_uint4(0, 0, 0, 0);
+  static_assert(N % 4 == 0, "");
+  for (int i = threadIdx.x; i < N / 4; i += blockDim.x) reinterpret_cast<uint4 *>(cnt)[i] = make_uint4(0, 0, 0, 0);
   __syncthreads();
   for (int j = c.hb + (int)threadIdx.x; j < c.he; j += blockDim.x) {
     int t = hist[j];
-    if (t >= c0 && t < c0 + CH && t < c.V) atomicAdd(&cnt[t - c0], 1u);
+    if (t >= c0 && t < c0 + N && t < c.V) atomicAdd(&cnt[t - c0], 1u);
   }
   __syncthreads();
 }

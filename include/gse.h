@@ -279,9 +279,11 @@ GSE_API int gse_pack_mask(gse_handle *h, const uint8_t *bools, int64_t bool_ld, 
 
 /* Replaces: nothing (measurement; the reference has no profiler). Calls made with GSE_BATCH_PROFILE record HIP events
  * around each of their kernels on their stream (no synchronisation), for up to GSE_PROFILE_CALLS calls. gse_profile
- * waits for the last recorded event, writes into ms[i] the total milliseconds of kernel i (launch order: main, deep
- * (the split-row finish), exact[, dist]) over the recorded calls and into *calls their number, then clears the
- * record. Returns the number of kernels per call (<= n are written) or a negative GSE_E_* code. */
+ * waits for the last recorded event, writes into ms[i] the total milliseconds of kernel slot i (launch order: main,
+ * deep (the split-row finish), exact[, dist]) over the recorded calls and into *calls their number, then clears the
+ * record. A call launches the split-row kernel, which then finishes every hard row itself, or, without it
+ * (GSE_BATCH_NO_SPLIT, GSE_BATCH_EXACT), the exact kernel: the other one's slot holds only its two events. Returns the
+ * number of kernel slots per call (<= n are written) or a negative GSE_E_* code. */
 #define GSE_PROFILE_CALLS 512
 GSE_API int gse_profile(gse_handle *h, float *ms, uint32_t n, uint32_t *calls);
 

@@ -424,6 +424,44 @@ def test_deep_rows_plan_wait_off(ge, gpu):
 
 
 @pytest.mark.gpu
+def test_hard_rows_in_the_split_row_launch(ge, gpu):
+    """With the split-row launch, it finishes every hard row itself (no exact launch follows it): rows whose part holds
+    more distinct penalty-history ids than it can count (3000 of 8192; hard, not sent to the split-row finish) beside
+    deep rows, such rows alone (the launch without deep rows), deep rows whose finish gives up (GSE_BATCH_NO_PLAN_WAIT)
+    beside them, and deep rows alone, in turn on one handle, twice over: every token equals the oracle's, so each call
+    left the counts it used cleared for the next."""
+    n, v = 16, 8192
+    rng = np.random.default_rng(5)
+    x = rng.normal(0.0, 1.0, size=(n, v)).astype(np.float32)
+    P = ge.sampling.SamplingParams
+    params = [P(temperature=[1.0, 1.3][r % 2], top_p=[0.95, 0.99, 0.999][r % 3], frequency_penalty=0.05)
+              for r in range(n)]
+    big = [rng.permutation(v)[:3000] for _ in range(n)]
+    small = [rng.integers(0, v, size=20) for _ in range(n)]
+    mixed = [big[r] if r % 4 == 0 else small[r] for r in range(n)]
+    u = np.array([ora.uniform(3000 + r, 2) for r in range(n)], np.float64)
+    xt = torch.from_numpy(x).to(gpu)
+    lib = ge._lib
+    cases = [("mixed", mixed, 0), ("overflow only", big, 0), ("no plan wait", mixed, lib.BATCH_NO_PLAN_WAIT),
+             ("deep only", small, 0)]
+    for rep in range(2):
+        for name, hist, flags in cases:
+            print(f"[hard rows] {name}, pass {rep}", flush=True)
+            got = ge.sampling.sample_ex(xt, params, None, None, None, history=hist, uniforms=u, flags=flags).tolist()
+            paths = lib.handle(gpu.index, n, v).row_paths(n)
+            assert got == ora.sample(x, params, None, None, None, history=hist, uniforms=u), (rep, name)
+            deep, exact = (paths == lib.PATH_DEEP).sum(), (paths == lib.PATH_EXACT).sum()
+            if name == "mixed":
+                assert deep >= 1 and exact >= n // 4, (name, paths)
+            elif name == "overflow only":
+                assert deep == 0 and exact >= n // 2, (name, paths)
+            elif name == "no plan wait":
+                assert exact >= n // 4 + 1, (name, paths)
+            else:
+                assert deep >= n // 2, (name, paths)
+
+
+@pytest.mark.gpu
 def test_deep_slots_overflow_to_exact(ge, gpu):
     """More deep rows than the split-row finish has slots (1024 per call at most): the rows past the slots take the
     exact path, and every token still equals the oracle's."""
