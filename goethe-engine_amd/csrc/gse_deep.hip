@@ -43,7 +43,8 @@ struct DeepShared {
     } c;
     uint64_t wl[WLC];           // pick pass: the slice's window elements
   };
-  uint32_t hover, ticket, nwl, wbase, pstat;
+  uint64_t pplan;
+  uint32_t hover, ticket, nwl, wbase;
   uint32_t wsum[NWV];
   uint64_t wred[NWV], wred2[NWV];
   double dred[NWV];
@@ -99,8 +100,12 @@ __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c,
   float xa[EPL], xb[EPL];
   uint32_t ma[L::NV], mb[L::NV];
   const int wu = __builtin_amdgcn_readfirstlane(w);  // (the wave index as a scalar: the chunk loop stays uniform)
-  int ck = wu;
-  if (nfull > 0) load_full<DT, AL>(c, p0 + ck * CHK, ck < nfull, xa, ma);
+  int ck = wu, cn = wu + NWV;
+  // both buffers' chunks go out before the history build (a slice of a few chunks per wave then loads at once)
+  if (nfull > 0) {
+    load_full<DT, AL>(c, p0 + ck * CHK, ck < nfull, xa, ma);
+    load_full<DT, AL>(c, p0 + cn * CHK, cn < nfull, xb, mb);
+  }
   if (build) {
     if (tid == 0) sh.hover = 0;
     build_history(c, a.hist, hid, p0, p1, sh.h, sh.wsum, sh.hover);
@@ -119,7 +124,7 @@ __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c,
   ln.fid = 0xFFFFFFFFu;
   ln.fnan = false;
   ln.ffin = false;
-  int nxt = wu + NWV;  // wave w takes chunks w, w + 4, w + 8, ... (scalar arithmetic)
+  int nxt = wu + 2 * NWV;  // wave w takes chunks w, w + 4, w + 8, ... (scalar arithmetic)
   auto grab = [&]() -> int {
     const int n = nxt;
     nxt += NWV;
@@ -145,14 +150,14 @@ __device__ __forceinline__ void stream_slice(const ScanArgs &a, const RowCtx &c,
   };
   if (nfull > 0) {
     while (true) {
-      const int cn = grab();
-      load_full<DT, AL>(c, p0 + cn * CHK, cn < nfull, xb, mb);
       if (ck >= nfull) break;
       body(ck, xa, ma);
       ck = grab();
       load_full<DT, AL>(c, p0 + ck * CHK, ck < nfull, xa, ma);
       if (cn >= nfull) break;
       body(cn, xb, mb);
+      cn = grab();
+      load_full<DT, AL>(c, p0 + cn * CHK, cn < nfull, xb, mb);
     }
   }
   if (nfull * CHK < p1 - p0 && w == 0) {  // the partial last chunk (uniform in wave 0)
@@ -350,17 +355,13 @@ __device__ __forceinline__ void plan_block(const uint64_t *gh, DeepSlot *ds, int
     const uint64_t xm[6] = {x0h, x0o, x1h, x1o, htot - x0h - x1h, otot - x0o - x1o};
     const uint32_t status =
         (inw > 0 && inw <= (uint64_t)DCAP && S > 0.0 && fabsf(M) < INFINITY) ? DS_PLANNED : DS_FAIL;
-    // the plan, then (once it is stored) its status, which the row's pick slices wait for
-    st_ag(&ds->w2lo, w2lo);
-    st_ag(&ds->w2hi, w2hi);
-    st_ag(&ds->w1lo, w1lo);
-    st_ag(&ds->w1hi, w1hi);
+    // the region counts and sums (read by the finish, which comes after this workgroup's pick ticket and so after
+    // these stores), then the status and windows in one word, which the row's pick slices wait for
     st_ag(&ds->acc[DA_C0], n0);  // (the element counts of the regions the pick pass sums without listing)
     st_ag(&ds->acc[DA_C1], n1);
     st_ag(&ds->acc[DA_C2], n2);
     for (int k = 0; k < 6; ++k) st_ag(&ds->acc[DA_X0HI + k], xm[k]);
-    store_wait();
-    st_ag(&ds->status, status);
+    st_ag(&ds->plan, plan_word(status, w2lo, w2hi, w1lo, w1hi));
   }
 }
 
@@ -476,7 +477,8 @@ __device__ __noinline__ void finish_row(const FinArgs a, DeepSlot *ds, FinShared
   const int row = ds->row;
   const float Mf = ds->M;
   const double M = (double)Mf;
-  const uint32_t w2hi = ld_ag(&ds->w2hi), w1lo = ld_ag(&ds->w1lo);
+  const uint64_t pw = ld_ag(&ds->plan);
+  const uint32_t w2hi = plan_win(pw, 1), w1lo = plan_win(pw, 2);
   const bool sep = w1lo > w2hi;  // an unlisted gap (region 1) between the draw window and the cut window
   const Fx X0{ld_ag(&ds->acc[DA_X0HI]), ld_ag(&ds->acc[DA_X0LO])}, X1{ld_ag(&ds->acc[DA_X1HI]), ld_ag(&ds->acc[DA_X1LO])};
   const Fx SF = fx_add(fx_add(X0, X1), Fx{ld_ag(&ds->acc[DA_RHI]), ld_ag(&ds->acc[DA_RLO])});
@@ -851,7 +853,8 @@ __device__ __noinline__ int finish_sorted(const FinArgs a, DeepSlot *ds, FinShar
   // every load the finish makes, issued together: the list's first LC entries (entries past its end are stale and
   // never used), the plan's windows, sums and counts (lanes of wave 0, into LDS), the row's parameters
   const uint32_t nraw = ld_ag(&ds->lcnt), spoil = ld_ag(&ds->spoil);
-  const uint32_t w2hi = ld_ag(&ds->w2hi), w1lo = ld_ag(&ds->w1lo);
+  const uint64_t pw = ld_ag(&ds->plan);
+  const uint32_t w2hi = plan_win(pw, 1), w1lo = plan_win(pw, 2);
   uint64_t v[SP];
 #pragma unroll
   for (int j = 0; j < SP; ++j) v[j] = ld_ag(&a.lst[j * MT + tid]);
@@ -1257,10 +1260,10 @@ __device__ __forceinline__ int pick_item(const ScanArgs &a, int slot, int slice,
   auto wait_plan = [&]() __attribute__((always_inline)) {
     if (tid == 0) {
       sh.nwl = 0;
-      uint32_t st = ld_ag(&ds->status);
-      if (st == DS_PENDING) {
+      uint64_t st = ld_ag(&ds->plan);
+      if (plan_status(st) == DS_PENDING) {
         const uint64_t t0 = wall_clock64();
-        while ((st = ld_ag(&ds->status)) == DS_PENDING) {
+        while (plan_status(st = ld_ag(&ds->plan)) == DS_PENDING) {
           // (every slice of the grid is resident at once and a plan takes microseconds: the limit, a.plan_wait, only
           // ends the wait when the device could not hold the whole grid)
           if (wall_clock64() - t0 >= a.plan_wait) {
@@ -1271,15 +1274,16 @@ __device__ __forceinline__ int pick_item(const ScanArgs &a, int slot, int slice,
           __builtin_amdgcn_s_sleep(16);  // (about 1000 clocks between polls)
         }
       }
-      sh.pstat = st;
+      sh.pplan = st;
     }
     __syncthreads();
-    planned = sh.pstat == DS_PLANNED;
+    const uint64_t pw = sh.pplan;
+    planned = plan_status(pw) == DS_PLANNED;
     if (planned) {
-      w2lo = ld_ag(&ds->w2lo);
-      w2hi = ld_ag(&ds->w2hi);
-      w1lo = ld_ag(&ds->w1lo);
-      w1hi = ld_ag(&ds->w1hi);
+      w2lo = plan_win(pw, 0);
+      w2hi = plan_win(pw, 1);
+      w1lo = plan_win(pw, 2);
+      w1hi = plan_win(pw, 3);
     }
   };
   stream_slice<DT, AL>(a, c, row, p0, p1, sh, keep, wait_plan, [&](float z, int t, bool ok) __attribute__((always_inline)) {

@@ -75,6 +75,16 @@ constexpr int DCAP = 8192;     // window elements listed per deep row
 
 enum : uint32_t { DS_PENDING = 0u, DS_PLANNED = 1u, DS_FAIL = 2u };
 
+// DeepSlot::plan: the status in bits 0-7, then the windows w2lo, w2hi, w1lo, w1hi (inclusive bins, 12 bits each).
+__host__ __device__ constexpr uint64_t plan_word(uint32_t st, uint32_t w2lo, uint32_t w2hi, uint32_t w1lo,
+                                                 uint32_t w1hi) {
+  return (uint64_t)st | (uint64_t)w2lo << 8 | (uint64_t)w2hi << 20 | (uint64_t)w1lo << 32 | (uint64_t)w1hi << 44;
+}
+__host__ __device__ constexpr uint32_t plan_status(uint64_t p) { return (uint32_t)(p & 0xFFu); }
+__host__ __device__ constexpr uint32_t plan_win(uint64_t p, int i) {  // 0: w2lo, 1: w2hi, 2: w1lo, 3: w1hi
+  return (uint32_t)(p >> (8 + 12 * i)) & 0xFFFu;
+}
+
 enum {  // DeepSlot.acc: exact fixed-point masses of the plan's regions (hi: 2^-40 units, lo: 2^-64 units) and counts
   DA_X0HI, DA_X0LO,  // bins before the draw window
   DA_X1HI, DA_X1LO,  // bins strictly between the two windows
@@ -89,14 +99,15 @@ struct DeepSlot {    // 256 bytes, one per deep row of a call
   int32_t row;
   float M;           // maximum of z
   double u;          // the draw's uniform
-  uint32_t status;   // DS_*, written by the planner
-  uint32_t w2lo, w2hi, w1lo, w1hi;  // bin windows holding the draw and the last kept element (inclusive)
+  uint64_t plan;     // the planner's word (plan_word): DS_* status and the bin windows holding the draw and the last
+                     // kept element, stored whole, so that a slice that sees the status also has the windows
   uint32_t lcnt;                    // listed window elements
   uint32_t cdone, pdone;            // slice tickets of the two passes (zero between calls)
+  uint32_t pad0;
   uint64_t acc[DA_N];               // the plan's region sums and counts
   uint32_t spoil;                   // a slice gave up waiting for the plan: the exact path takes the row (zero between calls)
   uint32_t pad32;
-  uint64_t pad[7];
+  uint64_t pad[8];
 };
 static_assert(sizeof(DeepSlot) == 256, "");
 

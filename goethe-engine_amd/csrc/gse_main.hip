@@ -538,7 +538,7 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
           ds->row = row;
           ds->M = M;
           ds->u = a.mode == MODE_SAMPLE ? (a.uni ? a.uni[row] : uniform64(P.seed, P.idx)) : 0.0;
-          ds->status = DS_PENDING;
+          ds->plan = plan_word(DS_PENDING, 0, 0, 0, 0);
           fl |= R_DEEP;
         }
       }
