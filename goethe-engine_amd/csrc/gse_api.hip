@@ -44,8 +44,6 @@ struct gse_handle {
   uint32_t *ptick = nullptr;
   uint32_t *plist = nullptr;          // [GSE_MAX_KIDS + 1][max_rows] nodes of each verify residual pass
   uint32_t *pcnt = nullptr;           // [GSE_MAX_KIDS + 1]          // [max_rows]
-  hipStream_t side = nullptr;       // verify rounds: the q rows' statistics run here, beside the selection pass
-  hipEvent_t fork = nullptr, join = nullptr;
   hipEvent_t (*ring)[5] = nullptr;  // kernel boundaries of up to GSE_PROFILE_CALLS profiled calls
   int nring = 0;                    // calls recorded
   int nprof = 0;                    // kernels per recorded call
@@ -378,15 +376,6 @@ GSE_API int gse_open(const gse_open_params *p, gse_handle **out) {
   }
   h->owned = true;
   carve(h, block, L, true);
-  // the verify rounds' side stream (default priority) and its fork / join events, made here so that no call creates
-  // them (a call may be under graph capture)
-  if ((e = hipStreamCreateWithFlags(&h->side, hipStreamNonBlocking)) != hipSuccess ||
-      (e = hipEventCreateWithFlags(&h->fork, hipEventDisableTiming)) != hipSuccess ||
-      (e = hipEventCreateWithFlags(&h->join, hipEventDisableTiming)) != hipSuccess) {
-    fail(nullptr, GSE_E_DEVICE, "side stream: %s", hipGetErrorString(e));
-    gse_close(h);
-    return GSE_E_DEVICE;
-  }
   *out = h;
   return GSE_OK;
 }
@@ -494,24 +483,12 @@ GSE_API int gse_verify_tree(gse_handle *h, const gse_batch *in, const gse_tree *
   L.qpart = h->qpart;
   L.qfin = h->qfin;
   L.out = o;
-  // The drafter rows' statistics need only the inputs: they run on the handle's side stream (forked from the caller's
-  // stream after its earlier work, joined before the kid tests), so that their workgroups fill the slots the selection
-  // pass leaves idle. They are queued after the main pass, whose workgroups then take the device first. Streams keep
-  // the default priority.
-  hipEvent_t qdone = nullptr;
-  const bool side = gse::tree_has_qstats(L);
-  if (side && !h->side) return fail(h, GSE_E_DEVICE, "the handle has no side stream");
-  if (side && (e = hipEventRecord(h->fork, s)) != hipSuccess) return hip_fail(h, e, "side stream fork");
+  // (the drafter rows' statistics run in the verify launch's statistics kernel, after the selection pass: on a second
+  // stream beside it they slowed the split-row pass by more than they saved, C4 315.4 -> 312.1 us per call without it)
   if ((e = gse::launch_main(a, s)) != hipSuccess) return hip_fail(h, e, "main launch");
-  if (side) {
-    if ((e = hipStreamWaitEvent(h->side, h->fork, 0)) != hipSuccess) return hip_fail(h, e, "side stream fork");
-    if ((e = gse::launch_qstats(L, h->side)) != hipSuccess) return hip_fail(h, e, "q statistics launch");
-    if ((e = hipEventRecord(h->join, h->side)) != hipSuccess) return hip_fail(h, e, "side stream join");
-    qdone = h->join;
-  }
   if (a.dgrid > 0 && (e = gse::launch_deep(a, s)) != hipSuccess) return hip_fail(h, e, "deep launch");
   if (a.dgrid == 0 && (e = gse::launch_exact(a, s)) != hipSuccess) return hip_fail(h, e, "exact launch");
-  if ((e = gse::launch_tree(L, s, qdone)) != hipSuccess) return hip_fail(h, e, "verify launch");
+  if ((e = gse::launch_tree(L, s)) != hipSuccess) return hip_fail(h, e, "verify launch");
   return GSE_OK;
 }
 
@@ -638,9 +615,6 @@ GSE_API void gse_close(gse_handle *h) {
     DeviceGuard g(h->device);
     (void)hipDeviceSynchronize();
     if (h->owned && h->block) (void)hipFree(h->block);
-    if (h->fork) (void)hipEventDestroy(h->fork);
-    if (h->join) (void)hipEventDestroy(h->join);
-    if (h->side) (void)hipStreamDestroy(h->side);
     if (h->ring) {
       for (int c = 0; c < GSE_PROFILE_CALLS; ++c)
         for (int i = 0; i < 5; ++i)

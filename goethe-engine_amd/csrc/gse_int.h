@@ -258,12 +258,8 @@ hipError_t launch_exact(const ScanArgs &a, hipStream_t s);
 hipError_t launch_dist_write(const ScanArgs &a, double *probs, int64_t probs_ld, hipStream_t s);
 hipError_t launch_draw(const double *q, int64_t ld, int rows, int V, const double *u, int32_t *out, hipStream_t s);
 hipError_t launch_mss(const gse_mss_batch &b, hipStream_t s);
-// The q rows' statistics of a verify round (drafter logits only; they read the inputs only), and whether the round has
-// any; then the round after the selection pass: with qdone, the statistics ran by launch_qstats and qdone marks their
-// end on their stream, else launch_tree computes them too.
-bool tree_has_qstats(const TreeLaunch &L);
-hipError_t launch_qstats(const TreeLaunch &L, hipStream_t s);
-hipError_t launch_tree(const TreeLaunch &L, hipStream_t s, hipEvent_t qdone);
+// The verify round after the selection pass (the statistics of the q rows given as drafter logits included).
+hipError_t launch_tree(const TreeLaunch &L, hipStream_t s);
 hipError_t launch_pick(const PickLaunch &L, hipStream_t s);
 hipError_t launch_zero(void *p, size_t bytes, hipStream_t s);
 hipError_t launch_qprob(const gse_qrows &q, int V, double *out, int64_t ld, hipStream_t s);

@@ -697,12 +697,11 @@ __device__ __forceinline__ Tgt tgt_of(const TreeArgs &a, int u, const gse_row &P
 
 // Per MSS node: the exact kept mass per slice (the last slice forms C). Per logits q row: the slice maximum m of z and
 // the slice mass exp(z - m) (the last slice forms M = max m and E = sum over slices of mass * exp(m - M), in slice
-// order: within a few ulp of the sum of exp(z - M) over the row). Row y = blockIdx.y + ybase: node y, or q row
-// y - nodes (the q rows depend on the inputs only, so they may run in a launch of their own).
+// order: within a few ulp of the sum of exp(z - M) over the row). Row y = blockIdx.y: node y, or q row y - nodes.
 template <int DTK, int QKK>
-__global__ __launch_bounds__(TT) void tstats_kernel(TreeArgs a, int ybase) {
+__global__ __launch_bounds__(TT) void tstats_kernel(TreeArgs a) {
   __shared__ TreeShared sh;
-  const int s = blockIdx.x, y = (int)blockIdx.y + ybase, tid = threadIdx.x;
+  const int s = blockIdx.x, y = (int)blockIdx.y, tid = threadIdx.x;
   if (s == 0 && y == 0 && tid <= GSE_MAX_KIDS) a.pcnt[tid] = 0u;  // (the residual passes' lists of this call)
   const int V = a.s.V, s0 = s * TS, s1 = min(V, s0 + TS);
   if (y < a.nodes) {
@@ -1402,27 +1401,14 @@ void by_instance(const TreeLaunch &L, F f) {
 
 }  // namespace
 
-bool tree_has_qstats(const TreeLaunch &L) { return L.q.rows > 0 && L.q.kind != GSE_Q_PROB; }
-
-hipError_t launch_qstats(const TreeLaunch &L, hipStream_t s) {
+hipError_t launch_tree(const TreeLaunch &L, hipStream_t s) {
   const TreeArgs a = tree_args(L);
-  if (!tree_has_qstats(L)) return hipSuccess;
-  by_instance(L, [&](auto dtc, auto qkc) {
-    constexpr int DT = decltype(dtc)::value, QK = decltype(qkc)::value;
-    hipLaunchKernelGGL((tstats_kernel<DT, QK>), dim3(a.nsl, L.q.rows), dim3(TT), 0, s, a, a.nodes);
-  });
-  return hipGetLastError();
-}
-
-hipError_t launch_tree(const TreeLaunch &L, hipStream_t s, hipEvent_t qdone) {
-  const TreeArgs a = tree_args(L);
-  // the q rows' statistics in this launch too, unless they ran on their own (qdone: their launch's end)
-  const int yq = tree_has_qstats(L) && !qdone ? (int)L.q.rows : 0;
+  // the statistics of the q rows given as drafter logits in the same launch (grid rows past the nodes)
+  const int yq = L.q.rows > 0 && L.q.kind != GSE_Q_PROB ? (int)L.q.rows : 0;
   // the instances for the call's logits type and q kind
   auto go = [&](auto dtc, auto qkc) {
     constexpr int DT = decltype(dtc)::value, QK = decltype(qkc)::value;
-    hipLaunchKernelGGL((tstats_kernel<DT, QK>), dim3(a.nsl, a.nodes + yq), dim3(TT), 0, s, a, 0);
-    if (qdone) (void)hipStreamWaitEvent(s, qdone, 0);
+    hipLaunchKernelGGL((tstats_kernel<DT, QK>), dim3(a.nsl, a.nodes + yq), dim3(TT), 0, s, a);
     hipLaunchKernelGGL(tkid0_kernel, dim3(a.nodes), dim3(TT), 0, s, a);
     // pass r: kid r - 1 rejected -> res_r; a node with k kids needs passes 1..k (one without kids draws in pass 1)
     // pass 1 takes most live nodes: one resident round; later passes only nodes with more kids (a quarter round,

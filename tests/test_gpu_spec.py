@@ -232,9 +232,9 @@ def test_verify_passes_with_more_items_than_workgroups(ge, gpu):
 
 
 def test_verify_rounds_back_to_back_on_a_stream(ge, gpu):
-    """Two verify rounds with drafter logits (their q-row statistics run on the library's side stream, forked from and
-    joined to the caller's stream), launched alternately four times each on a non-default stream without any
-    synchronisation: every launch's output equals a synchronised launch's, which equals the oracle walk's."""
+    """Two verify rounds with drafter logits (their q-row statistics included), launched alternately four times each on
+    a non-default stream without any synchronisation: every launch's output equals a synchronised launch's, which
+    equals the oracle walk's."""
     reqs = ge.workloads.c4()
     other = [dict(r, seed=(r["seed"] * 7 + 3) % (1 << 62)) for r in reqs[:12]]
 
@@ -256,7 +256,7 @@ def test_verify_rounds_back_to_back_on_a_stream(ge, gpu):
                                    r["params"], r["seed"])
             assert got[a] == want, (a, got[a], want)
         refs.append(snap(c))
-    print("[verify] back-to-back rounds on a side stream", flush=True)
+    print("[verify] back-to-back rounds on a non-default stream", flush=True)
     st = torch.cuda.Stream(gpu)  # (default priority)
     snaps = []
     with torch.cuda.stream(st):
@@ -349,7 +349,7 @@ def test_draft_pick_bf16_matches_oracle(ge, gpu, t):
 
 
 def test_verify_round_in_a_captured_graph(ge, gpu):
-    """A verify round with drafter logits (its fork to the handle's side stream and the join back) captured in a graph
+    """A verify round with drafter logits (its q-row statistics included) captured in a graph
     on the stream it ran on before (so its handle exists: opening one allocates), replayed three times with eager work
     between the replays; every replay's walks equal the eager round's, which equal the oracle's."""
     reqs = ge.workloads.c4()[:8]
