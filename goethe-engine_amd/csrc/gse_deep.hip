@@ -383,7 +383,7 @@ static_assert(LC <= DCAP && LC % MT == 0, "");
 constexpr uint32_t NONE = 0xFFFFFFFFu;
 
 struct FinShared {
-  uint64_t lc[LC];              // the first LC window entries
+  alignas(16) uint64_t lc[LC];  // the first LC window entries (16-byte aligned: pairs are read as one)
   uint64_t sub[SUBC];           // the collected entries of one sub-bin, sorted
   uint32_t scnt[NSB];           // sub-bin counts, then their exclusive prefix
   uint32_t stop[NSB];           // sub-bin head keys (largest key)
@@ -847,6 +847,122 @@ __device__ __forceinline__ void finish_wave(const FinArgs a, DeepSlot *ds, FinSh
   }
 }
 
+// Longest list the block finish takes (its ranking pass grows with the list; the bucketed finish below is as fast
+// from about 200 entries on: C3 lists of 87-150 entries 8.7-10.8 -> 6.0-7.6 us, of about 230 entries 9-10 us either way).
+constexpr int FBN = 192;
+static_assert(FBN <= MT, "");
+
+// The sorted finish of a list of at most FBN entries (finish_wave's steps, a workgroup wide): thread t holds entry t,
+// ranks it by the count of greater entries (a pass over the list in LDS), and then holds rank t; one block scan of the
+// fixed-point masses gives every rank's exclusive prefix, and the cut and the draw are block minima. Five barriers.
+__device__ __forceinline__ void finish_block(const FinArgs a, DeepSlot *ds, FinShared &sh, const double *etab, int n,
+                                          uint64_t e, int row, float Mf, double u, uint64_t K, double topp,
+                                          double minp, bool sep, uint32_t w1lo) {
+  const int tid = threadIdx.x, l = lane_id(), w = tid >> 6;
+  const bool val = tid < n;
+  const double M = (double)Mf;
+  const bool g1o = val && sep && dbin(fkey_inv(pk_key(e)), Mf) >= w1lo;
+  if (val) sh.lc[tid] = e;
+  const uint64_t dw = ballot64(val && !g1o);  // (every lane takes part in the ballot)
+  if (l == 0) sh.wsum[w] = (uint32_t)__popcll(dw);
+  if (tid < 2) sh.q[tid] = NONE;
+  __syncthreads();  // 1: the list, the draw window's counts
+  uint32_t n0 = 0;
+#pragma unroll
+  for (int k = 0; k < NWV; ++k) n0 += sh.wsum[k];  // entries of the draw window (they rank first)
+  if (val) {  // (entries past n in lc are stale: the pairs loop reads whole pairs below n only)
+    uint32_t r = 0;
+    int m = 0;
+    const ulonglong2 *lp = reinterpret_cast<const ulonglong2 *>(sh.lc);
+#pragma unroll 1
+    for (; m + 4 <= n; m += 4) {
+      const ulonglong2 p = lp[m >> 1], q = lp[(m >> 1) + 1];
+      r += (p.x > e ? 1u : 0u) + (p.y > e ? 1u : 0u) + (q.x > e ? 1u : 0u) + (q.y > e ? 1u : 0u);
+    }
+#pragma unroll 1
+    for (; m < n; ++m) r += sh.lc[m] > e ? 1u : 0u;
+    sh.sub[r] = e;
+  }
+  __syncthreads();  // 2: the entries in rank order
+  const uint64_t es = val ? sh.sub[tid] : 0ull;  // rank tid
+  const Fx f = val ? fx_of(exp_nonpos((double)fkey_inv(pk_key(es)) - M, etab)) : Fx{0, 0};
+  const Fx X0{sh.acc[DA_X0HI], sh.acc[DA_X0LO]}, X1{sh.acc[DA_X1HI], sh.acc[DA_X1LO]};
+  const Fx SF = fx_add(fx_add(X0, X1), Fx{sh.acc[DA_RHI], sh.acc[DA_RLO]});
+  const uint64_t c0 = sh.acc[DA_C0], c1 = sh.acc[DA_C1], tail = sh.acc[DA_C2];
+  const double Sd = fx_val(SF), q0 = 1.0 / Sd;
+  bool okd = Sd > 0.0 && Sd < INFINITY;  // (x / Sd >= t reads x >= least_ge(t, Sd))
+  const double ap = least_ge(topp, Sd, okd), am = minp > 0.0 ? least_ge(minp * q0, Sd, okd) : 0.0;
+  // exclusive prefix of rank tid: the wave scan, then the earlier waves' totals
+  const uint64_t ih = wave_incl_scan_u64(f.hi), il = wave_incl_scan_u64(f.lo);
+  if (l == WAVE - 1) {
+    sh.wred[w] = ih;
+    sh.wred2[w] = il;
+  }
+  __syncthreads();  // 3: the wave totals
+  uint64_t ph = ih - f.hi, pl = il - f.lo, th = 0, tl = 0;
+#pragma unroll
+  for (int k = 0; k < NWV; ++k) {
+    ph += k < w ? sh.wred[k] : 0ull;
+    pl += k < w ? sh.wred2[k] : 0ull;
+    th += sh.wred[k];
+    tl += sh.wred2[k];
+  }
+  const bool g1 = (uint32_t)tid >= n0;
+  const Fx Ar = fx_add(fx_add(X0, Fx{ph, pl}), g1 ? X1 : Fx{0, 0});
+  // the first entry that is not kept (sampling.py:80, with min-p); it publishes its exclusive prefix
+  const bool cut = val && ((c0 + (uint64_t)tid + (g1 ? c1 : 0ull) >= K) | (minp > 0.0 && !(fx_val(f) >= am)) |
+                           (fx_val(Ar) >= ap));
+  if (cut) {
+    sh.shi[tid] = Ar.hi;
+    sh.slo[tid] = Ar.lo;
+  }
+  {
+    const uint64_t cb = ballot64(cut);
+    if (l == 0 && cb) atomicMin(&sh.q[0], (uint32_t)(w * WAVE + (int)__builtin_ctzll(cb)));
+  }
+  __syncthreads();  // 4: the first cut
+  const uint32_t fc = sh.q[0];
+  const int last = fc == NONE ? n - 1 : (int)fc - 1;  // the last kept entry
+  const bool glast = last >= 0 && (uint32_t)last >= n0;
+  bool ok = n > 0 && okd && last >= 0;
+  Fx Al{0, 0};  // c_last, unnormalized
+  if (fc != NONE) {
+    Al = Fx{sh.shi[fc], sh.slo[fc]};
+    ok = ok && !(fc >= n0 && !glast && c1 > 0);  // (the first cut entry right after the gap: the cut may be inside it)
+  } else {
+    Al = fx_add(fx_add(X0, Fx{th, tl}), glast ? X1 : Fx{0, 0});
+    const uint64_t rl = c0 + (uint64_t)last + (glast ? c1 : 0ull);
+    const uint64_t after = (!sep || glast) ? tail : c1 + tail;  // unlisted elements ranked after the list
+    ok = ok && (after == 0 || rl + 1 >= K || fx_val(Al) / Sd >= topp);
+  }
+  const double clast = fx_val(Al) / Sd;
+  if (ok && a.mode == MODE_SAMPLE) {
+    // the draw: the first kept entry whose inclusive prefix reaches u c_last; its exclusive prefix must lie below it.
+    // Packed as rank << 1 | (not below).
+    bool okt = true;
+    const double at = least_ge(u * clast, Sd, okt);  // (the same value in every thread)
+    const bool hit = tid <= last && fx_val(fx_add(Ar, f)) >= at, below = !(fx_val(Ar) >= at);
+    uint32_t fj = hit ? (uint32_t)tid << 1 | (below ? 0u : 1u) : NONE;
+    fj = wave_min_u32(fj);
+    if (l == 0 && fj != NONE) atomicMin(&sh.q[1], fj);
+    __syncthreads();  // 5: the draw
+    fj = sh.q[1];
+    ok = okt && fj != NONE && (fj & 1u) == 0u;
+  }
+  if (tid == 0 && ok) {  // (the main pass's cmax stays)
+    const int32_t tok = a.mode == MODE_SAMPLE ? (int32_t)pk_id(sh.sub[sh.q[1] >> 1]) : -1;
+    RowInfo *ri = a.info + row;
+    ri->kkeep = sh.sub[last];
+    ri->S = Sd;
+    ri->Z = clast;
+    ri->flags = R_DONE | R_BY_DEEP;
+    ri->ncert = 0;
+    ri->token = tok;
+    if (a.mode == MODE_SAMPLE) a.tokens[row] = tok;
+    g_fin = 1u;
+  }
+}
+
 __device__ __noinline__ int finish_sorted(const FinArgs a, DeepSlot *ds, FinShared &sh, const double *etab) {
   constexpr int SP = LC / MT;  // entries (and ranks) per thread
   const int tid = threadIdx.x, w = tid >> 6;
@@ -872,7 +988,11 @@ __device__ __noinline__ int finish_sorted(const FinArgs a, DeepSlot *ds, FinShar
     if (tid < WAVE) finish_wave(a, ds, sh, etab, n, v[0], accv, row, Mf, u, K, topp, minp, sep, w1lo);
     return 0;
   }
-  if (tid < DA_N) sh.acc[tid] = accv;
+  if (tid < DA_N) sh.acc[tid] = accv;  // (published by the first barrier of either path)
+  if (n <= FBN) {
+    finish_block(a, ds, sh, etab, n, v[0], row, Mf, u, K, topp, minp, sep, w1lo);
+    return 0;
+  }
   uint32_t *bcnt = reinterpret_cast<uint32_t *>(sh.sub), *bofs = bcnt + 2 * FB;
   double *msr = reinterpret_cast<double *>(sh.sub);  // (after the ranks: the masses by rank)
   for (int b = tid; b < 2 * FB; b += MT) bcnt[b] = 0;
