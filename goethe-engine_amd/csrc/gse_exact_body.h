@@ -9,6 +9,9 @@ constexpr int PER = CHX / XT;    // tokens per thread per chunk (contiguous)
 constexpr int HS = 32 - LB;      // level-0 bins (2^HS keys each) of the head's histogram, which the max pass counts
 static_assert(NB == 4 * XT && (1 << LB) == NB && CAPS == 8 * XT && PER == 8, "the shape the body is written for");
 
+constexpr int HIDC = 2048;                // history ids a row keeps in LDS for its chunks' count tables
+constexpr uint32_t NHID_GLOBAL = 0xFFFFFFFFu;
+
 struct ExactShared {
   uint32_t cnt[CHX];
   union {
@@ -28,6 +31,8 @@ struct ExactShared {
   double dred[XW];
   uint64_t xs[4];
   uint32_t n, found;
+  int32_t hid[HIDC];  // the row's history ids, when they fit (nhid of them; nhid = NHID_GLOBAL: read from memory)
+  uint32_t nhid;
 };
 
 // Context of the row being finished.
@@ -64,6 +69,23 @@ __device__ __forceinline__ float raw_logit(const RowCtx &c, uint32_t r) {
   return __uint_as_float(c.dtype == GSE_BF16 ? r << 16 : r);
 }
 
+// The count table sh.cnt of the chunk [c0, c0 + CHX) from the row's history: from its LDS copy when the row's history
+// fits, else from memory (a round trip per chunk). Ends with a barrier.
+__device__ __forceinline__ void chunk_counts(const RowCtx &c, const int32_t *hist, int c0, ExactShared &sh) {
+  const uint32_t nh = sh.nhid;
+  if (nh == NHID_GLOBAL) {
+    build_counts<CHX>(c, hist, c0, &sh.cnt[0]);
+    return;
+  }
+  for (int i = threadIdx.x; i < CHX / 4; i += XT) reinterpret_cast<uint4 *>(sh.cnt)[i] = make_uint4(0, 0, 0, 0);
+  __syncthreads();
+  for (int j = threadIdx.x; j < (int)nh; j += XT) {
+    const int t = sh.hid[j];
+    if (t >= c0 && t < c0 + CHX && t < c.V) atomicAdd(&sh.cnt[t - c0], 1u);
+  }
+  __syncthreads();
+}
+
 // Calls f(t, key) for every token of the row, thread-contiguous inside each chunk (ids increase with (tid, i)).
 // The next chunk's run is loaded while the current one is processed (issued after the history counts, whose loads
 // are waited for).
@@ -75,7 +97,7 @@ __device__ __forceinline__ void for_each_key(const RowCtx &c, const int32_t *his
   for (int ch = 0; ch < nch; ++ch) {
     const int c0 = ch * CHX;
     const int t0 = c0 + tid * PER;
-    if (c.pen) build_counts<CHX>(c, hist, c0, sh.cnt);
+    if (c.pen) chunk_counts(c, hist, c0, sh);
     uint32_t vn[PER];
     const uint32_t mn = load_run(c, ch + 1 < nch ? t0 + CHX : t0, vn);
 #pragma unroll
@@ -236,7 +258,8 @@ struct Win {
 };
 
 // Builds counts and masses of the keys inside the window.
-__device__ void build_hist(const XCtx &x, ExactShared &sh, const Win &w) {
+__device__ __noinline__ void build_hist(const XCtx &x, ExactShared &, const Win &w) {
+  ExactShared &sh = xs();  // (the LDS object itself: a reference argument is a generic pointer)
   for (int b = threadIdx.x; b < NB; b += XT) {
     sh.u.h.c[b] = 0;
     sh.u.h.hi[b] = 0;
@@ -266,8 +289,9 @@ __device__ __forceinline__ bool q_pred(int kind, uint64_t r, int64_t n_before, F
 
 // Finds, in the current histogram (descending bins), the first bin whose inclusive prefix satisfies the query.
 // Returns -1 when none does; fills the window-relative prefix before that bin.
-__device__ int find_bin(ExactShared &sh, const Win &w, int kind, uint64_t r, double S, double tgt, uint64_t &nb_out,
+__device__ __noinline__ int find_bin(ExactShared &, const Win &w, int kind, uint64_t r, double S, double tgt, uint64_t &nb_out,
                         Fx &mb_out) {
+  ExactShared &sh = xs();  // (the LDS object itself: a reference argument is a generic pointer)
   // thread t owns 4 consecutive bins in descending order: NB-1-4t ... NB-4-4t
   const int tid = threadIdx.x;
   uint64_t n4 = 0, h4 = 0, l4 = 0;
@@ -327,7 +351,8 @@ __device__ int find_bin(ExactShared &sh, const Win &w, int kind, uint64_t r, dou
 
 // Collects the packed keys of every element with key in [klo, khi] into LDS (sorted descending). Returns the count
 // (possibly above CAPS: then the list is partial).
-__device__ uint32_t collect(const XCtx &x, ExactShared &sh, uint32_t klo, uint32_t khi) {
+__device__ __noinline__ uint32_t collect(const XCtx &x, ExactShared &, uint32_t klo, uint32_t khi) {
+  ExactShared &sh = xs();  // (the LDS object itself: a reference argument is a generic pointer)
   if (threadIdx.x == 0) sh.n = 0;
   __syncthreads();
   pass<P_COLLECT>(x, PassIn{0.0, klo, khi, 0, 0});
@@ -344,8 +369,9 @@ __device__ uint32_t collect(const XCtx &x, ExactShared &sh, uint32_t klo, uint32
 
 // Walks a collected, sorted list (n <= CAPS) for the query, with n_before / m_before the prefix above the list.
 // Returns the index inside the list (or n when no element qualifies) and fills the element's prefix mass.
-__device__ int walk_list(const XCtx &x, ExactShared &sh, int n, int kind, uint64_t r, uint64_t n_before, Fx m_before,
+__device__ __noinline__ int walk_list(const XCtx &x, ExactShared &, int n, int kind, uint64_t r, uint64_t n_before, Fx m_before,
                          double tgt, Fx &above, Fx &self) {
+  ExactShared &sh = xs();  // (the LDS object itself: a reference argument is a generic pointer)
   const int tid = threadIdx.x;
   constexpr int PT = CAPS / XT;  // 8 elements per thread, consecutive
   Fx ef[PT];
@@ -395,7 +421,8 @@ __device__ int walk_list(const XCtx &x, ExactShared &sh, int n, int kind, uint64
 }
 
 // Elements sharing one key, taken in token-id order: the token at position p (0-based) among them.
-__device__ uint32_t nth_with_key(const XCtx &x, ExactShared &sh, uint32_t key, uint64_t p) {
+__device__ __noinline__ uint32_t nth_with_key(const XCtx &x, ExactShared &, uint32_t key, uint64_t p) {
+  ExactShared &sh = xs();  // (the LDS object itself: a reference argument is a generic pointer)
   const int tid = threadIdx.x;
   uint64_t base = 0;
   if (tid == 0) sh.found = 0xFFFFFFFFu;
@@ -405,7 +432,7 @@ __device__ uint32_t nth_with_key(const XCtx &x, ExactShared &sh, uint32_t key, u
   const int nch = x.nch;
   for (int ch = 0; ch < nch; ++ch) {
     const int c0 = ch * CHX;
-    if (c.pen) build_counts<CHX>(c, hist, c0, sh.cnt);
+    if (c.pen) chunk_counts(c, hist, c0, sh);
     const int t0 = c0 + tid * PER;
     uint32_t v[PER];
     const uint32_t mword = load_run(c, t0, v);
@@ -446,7 +473,8 @@ __device__ uint32_t nth_with_key(const XCtx &x, ExactShared &sh, uint32_t key, u
 }
 
 // Runs one query to its element: histogram levels, collection, walk.
-__device__ Hit query(const XCtx &x, ExactShared &sh, int kind, uint64_t r, double tgt) {
+__device__ __noinline__ Hit query(const XCtx &x, ExactShared &, int kind, uint64_t r, double tgt) {
+  ExactShared &sh = xs();  // (the LDS object itself: a reference argument is a generic pointer)
   Hit out;
   Win w{0u, 0xFFFFFFFFu, HS, 0, Fx{0, 0}};
   for (int level = 0; level < (32 + LB - 1) / LB; ++level) {
@@ -525,7 +553,8 @@ static_assert((0xFFFFFFFFu >> HS) < (uint32_t)NB, "the level-0 bins cover every 
 // more than HEADN elements. Expects the level-0 counts of every key in the histogram (the max pass, P_MAXH), masses
 // zero: the cut is a rank. A query answered inside the head is a walk of the list; query() reuses the LDS, after
 // which the head is gone.
-__device__ uint32_t collect_head(const XCtx &x, ExactShared &sh, uint32_t &kcut) {
+__device__ __noinline__ uint32_t collect_head(const XCtx &x, ExactShared &, uint32_t &kcut) {
+  ExactShared &sh = xs();  // (the LDS object itself: a reference argument is a generic pointer)
   const Win w{0u, 0xFFFFFFFFu, HS, 0, Fx{0, 0}};
   uint64_t nb = 0;
   Fx mb{0, 0};
@@ -538,7 +567,8 @@ __device__ uint32_t collect_head(const XCtx &x, ExactShared &sh, uint32_t &kcut)
 
 // A query answered from the head of n elements: false when no element of the head satisfies it (the answer, if any,
 // ranks at n or below).
-__device__ bool head_query(const XCtx &x, ExactShared &sh, uint32_t n, int kind, uint64_t r, double tgt, Hit &h) {
+__device__ __noinline__ bool head_query(const XCtx &x, ExactShared &, uint32_t n, int kind, uint64_t r, double tgt, Hit &h) {
+  ExactShared &sh = xs();  // (the LDS object itself: a reference argument is a generic pointer)
   Fx above, self;
   const int i = walk_list(x, sh, (int)n, kind, r, 0, Fx{0, 0}, tgt, above, self);
   if (i >= (int)n) return false;
@@ -550,12 +580,14 @@ __device__ bool head_query(const XCtx &x, ExactShared &sh, uint32_t n, int kind,
   return true;
 }
 
-__device__ uint64_t count_ge(const XCtx &x, ExactShared &sh, uint32_t kmin) {
+__device__ __noinline__ uint64_t count_ge(const XCtx &x, ExactShared &, uint32_t kmin) {
+  ExactShared &sh = xs();  // (the LDS object itself: a reference argument is a generic pointer)
   return block_sum_u64(pass<P_COUNT>(x, PassIn{0.0, kmin, 0, 0, 0}).u, sh);
 }
 
 // Collects the elements with packed key >= pk (the top ranks) and sorts them.
-__device__ uint32_t collect_top(const XCtx &x, ExactShared &sh, uint64_t pk) {
+__device__ __noinline__ uint32_t collect_top(const XCtx &x, ExactShared &, uint64_t pk) {
+  ExactShared &sh = xs();  // (the LDS object itself: a reference argument is a generic pointer)
   if (threadIdx.x == 0) sh.n = 0;
   __syncthreads();
   pass<P_TOP>(x, PassIn{0.0, 0, 0, 0, pk});
@@ -579,6 +611,14 @@ __device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShare
   x.row = row;
   x.nch = (a.V + CHX - 1) / CHX;
   x.c = make_ctx(a, row, P);
+  {  // the row's history ids into LDS when they fit (every chunk of every pass counts its tokens from them)
+    const int nh = x.c.pen ? x.c.he - x.c.hb : 0;
+    const bool fits = nh <= HIDC;
+    if (fits)
+      for (int j = tid; j < nh; j += XT) sh.hid[j] = a.hist[x.c.hb + j];
+    if (tid == 0) sh.nhid = fits ? (uint32_t)nh : NHID_GLOBAL;
+    __syncthreads();
+  }
   if (greedy) {  // logprobs of a greedy row are taken over z = x
     x.c.greedy = false;
     x.c.divide = false;
@@ -593,7 +633,7 @@ __device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShare
     const int nch = (a.V + CHX - 1) / CHX;
     for (int ch = 0; ch < nch; ++ch) {
       const int c0 = ch * CHX;
-      if (gc.pen) build_counts<CHX>(gc, a.hist, c0, sh.cnt);
+      if (gc.pen) chunk_counts(gc, a.hist, c0, sh);
       const int t0 = c0 + tid * PER;
       uint32_t v[PER];
       const uint32_t mword = load_run(gc, t0, v);
