@@ -43,17 +43,22 @@ struct XCtx {
   double M, S;
 };
 
+// The all-ones mask word that a run of a row without a mask reads (so that the mask word's load has no branch).
+__device__ const uint32_t XONES[1] = {0xFFFFFFFFu};
+
 // The logits of tokens t0 .. t0+PER-1 (a thread's run inside a chunk) as raw bits (bf16 zero-extended), loaded
 // together so that the PER loads are in flight at once, and converted only where used (raw_logit), so that a
 // prefetched run is not waited for early; indexes past the row end read its last element (the callers skip those
 // tokens). Returns the mask word of the run (its PER tokens share one: PER divides 32), all ones without a mask.
-// The pointers are global ones: loads through generic pointers would be flat loads, whose completion the compiler
-// cannot count, so that every later use waited for all loads in flight, the next run's included.
+// The pointers are global ones and no load sits behind a branch (the logits type is a template argument, the mask
+// word's address a select): loads through generic pointers, or behind a branch, make later uses wait for every load
+// in flight, the next runs' included.
+template <int DT>
 __device__ __forceinline__ uint32_t load_run(const RowCtx &c, int t0, uint32_t (&v)[PER]) {
   static_assert(32 % PER == 0, "a run shares one mask word");
   typedef const __attribute__((address_space(1))) uint16_t g16;
   typedef const __attribute__((address_space(1))) uint32_t g32;
-  if (c.dtype == GSE_BF16) {
+  if constexpr (DT == GSE_BF16) {
     g16 *p = (g16 *)c.base;
 #pragma unroll
     for (int i = 0; i < PER; ++i) v[i] = p[min(t0 + i, c.V - 1)];
@@ -62,7 +67,11 @@ __device__ __forceinline__ uint32_t load_run(const RowCtx &c, int t0, uint32_t (
 #pragma unroll
     for (int i = 0; i < PER; ++i) v[i] = p[min(t0 + i, c.V - 1)];
   }
-  return c.mw ? (t0 < c.V ? ((g32 *)c.mw)[t0 >> 5] : 0u) : 0xFFFFFFFFu;
+  g32 *mp = c.mw ? (g32 *)c.mw : (g32 *)XONES;
+  return mp[c.mw ? (min(t0, c.V - 1) >> 5) : 0];
+}
+__device__ __forceinline__ uint32_t load_run_any(const RowCtx &c, int t0, uint32_t (&v)[PER]) {
+  return c.dtype == GSE_BF16 ? load_run<GSE_BF16>(c, t0, v) : load_run<GSE_F32>(c, t0, v);
 }
 
 __device__ __forceinline__ float raw_logit(const RowCtx &c, uint32_t r) {
@@ -87,19 +96,21 @@ __device__ __forceinline__ void chunk_counts(const RowCtx &c, const int32_t *his
 }
 
 // Calls f(t, key) for every token of the row, thread-contiguous inside each chunk (ids increase with (tid, i)).
-// The next chunk's run is loaded while the current one is processed (issued after the history counts, whose loads
-// are waited for).
-template <typename F>
+// The runs of the next two chunks are loading while the current one is processed (a pass is a chain of chunks, each
+// waiting for its loads: with 256 threads a row is about 75 chunks of 2048 tokens). A load past the row reads its last
+// chunk again, so every step issues the same loads.
+template <int DT, typename F>
 __device__ __forceinline__ void for_each_key(const RowCtx &c, const int32_t *hist, int nch, ExactShared &sh, F f) {
   const int tid = threadIdx.x;
-  uint32_t v[PER];
-  uint32_t mword = load_run(c, tid * PER, v);
+  uint32_t v[PER], vn[PER];
+  uint32_t mword = load_run<DT>(c, tid * PER, v);
+  uint32_t mn = load_run<DT>(c, (nch > 1 ? CHX : 0) + tid * PER, vn);
   for (int ch = 0; ch < nch; ++ch) {
     const int c0 = ch * CHX;
     const int t0 = c0 + tid * PER;
     if (c.pen) chunk_counts(c, hist, c0, sh);
-    uint32_t vn[PER];
-    const uint32_t mn = load_run(c, ch + 1 < nch ? t0 + CHX : t0, vn);
+    uint32_t vm[PER];
+    const uint32_t mm = load_run<DT>(c, ch + 2 < nch ? t0 + 2 * CHX : t0, vm);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int t = t0 + i;
@@ -113,8 +124,12 @@ __device__ __forceinline__ void for_each_key(const RowCtx &c, const int32_t *his
     }
     if (c.pen) __syncthreads();
 #pragma unroll
-    for (int i = 0; i < PER; ++i) v[i] = vn[i];
+    for (int i = 0; i < PER; ++i) {
+      v[i] = vn[i];
+      vn[i] = vm[i];
+    }
     mword = mn;
+    mn = mm;
   }
 }
 
@@ -145,12 +160,12 @@ struct PassOut {
 // Every thread of the workgroup calls it. P_HIST adds counts and fixed-point masses to the histogram bins (P_MAXH:
 // P_MAX that also counts every key into the bins, masses left alone), P_COLLECT
 // and P_TOP append packed keys at xsh.n (the callers clear the bins and the count first and synchronise afterwards).
-template <int OP>
+template <int OP, int DT>
 __device__ __noinline__ PassOut row_pass(const RowCtx c, const int32_t *hist, int nch, const PassIn in) {
   ExactShared &sh = xs();
   uint64_t u = 0;
   double d = 0.0;
-  for_each_key(c, hist, nch, sh, [&](int t, uint32_t k) {
+  for_each_key<DT>(c, hist, nch, sh, [&](int t, uint32_t k) {
     if constexpr (OP == P_MAX || OP == P_MAXH) {
       const uint64_t p = pack(k, (uint32_t)t);
       u = p > u ? p : u;
@@ -187,7 +202,8 @@ __device__ __noinline__ PassOut row_pass(const RowCtx c, const int32_t *hist, in
 
 template <int OP>
 __device__ __forceinline__ PassOut pass(const XCtx &x, const PassIn &in) {
-  return row_pass<OP>(x.c, x.hist, x.nch, in);
+  return x.c.dtype == GSE_BF16 ? row_pass<OP, GSE_BF16>(x.c, x.hist, x.nch, in)
+                               : row_pass<OP, GSE_F32>(x.c, x.hist, x.nch, in);
 }
 
 // ---- block reductions / scans (1024 threads) ------------------------------------------------------------------------
@@ -435,7 +451,7 @@ __device__ __noinline__ uint32_t nth_with_key(const XCtx &x, ExactShared &, uint
     if (c.pen) chunk_counts(c, hist, c0, sh);
     const int t0 = c0 + tid * PER;
     uint32_t v[PER];
-    const uint32_t mword = load_run(c, t0, v);
+    const uint32_t mword = load_run_any(c, t0, v);
     uint32_t match = 0;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -636,7 +652,7 @@ __device__ __forceinline__ void exact_row(const ScanArgs &a, int row, ExactShare
       if (gc.pen) chunk_counts(gc, a.hist, c0, sh);
       const int t0 = c0 + tid * PER;
       uint32_t v[PER];
-      const uint32_t mword = load_run(gc, t0, v);
+      const uint32_t mword = load_run_any(gc, t0, v);
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int t = t0 + i;
