@@ -128,12 +128,12 @@ int check_batch(gse_handle *h, const gse_batch &b) {
   return GSE_OK;
 }
 
-// Parts per row for the main pass: each at most PTOK tokens, a multiple of PCHUNK long, and enough of them over the
-// batch to give every CU about four workgroups, as long as a part keeps at least PMIN tokens.
+// Parts per row for the main pass: each at most ptok tokens (PTOK, or PTOK_PLAIN), a multiple of PCHUNK long, and
+// enough of them over the batch to give every CU about four workgroups, as long as a part keeps at least PMIN tokens.
 // rows * parts <= rows * (ceil(vocab / PTOK) + 1) + target.
-void parts(const gse_handle *h, uint32_t rows, uint32_t vocab, int *nparts, int *plen) {
+void parts(const gse_handle *h, uint32_t rows, uint32_t vocab, uint32_t ptok, int *nparts, int *plen) {
   const uint32_t nck = (vocab + gse::PCHUNK - 1) / gse::PCHUNK;
-  uint32_t np = (vocab + gse::PTOK - 1) / gse::PTOK;
+  uint32_t np = (vocab + ptok - 1) / ptok;
   uint32_t want = (h->target + rows - 1) / rows;
   const uint32_t cap = vocab / gse::PMIN > 1u ? vocab / gse::PMIN : 1u;
   if (want > cap) want = cap;
@@ -190,7 +190,12 @@ gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   a.V = (int)b.vocab;
   a.rows = (int)b.rows;
   a.nch = (int)((b.vocab + gse::CH - 1) / gse::CH);
-  parts(h, b.rows, b.vocab, &a.nparts, &a.plen);
+  // A call with no histories and no masks keeps no part-sized tables in LDS: its parts may be twice as long (a large
+  // batch then streams its rows in half the workgroups, each with one prologue and one first-chunk latency for twice
+  // the tokens), and a part's listing target and valve grow with its length, so that a row lists as many candidates.
+  parts(h, b.rows, b.vocab, (!b.hist && !b.mask) ? (uint32_t)gse::PTOK_PLAIN : (uint32_t)gse::PTOK, &a.nparts, &a.plen);
+  a.kt = a.plen > gse::PTOK ? (int)(((int64_t)gse::KT * a.plen + gse::PTOK - 1) / gse::PTOK) : gse::KT;
+  a.vfirst = (int)((int64_t)gse::CAPW / 4 * a.kt / gse::KT) + 1;
   a.mode = mode;
   a.xcd_map = 1;
   a.force_exact = (b.flags & GSE_BATCH_EXACT) ? 1 : 0;

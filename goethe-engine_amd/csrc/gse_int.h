@@ -37,16 +37,19 @@ enum : uint32_t {
 
 enum { MODE_SAMPLE = 0, MODE_DIST = 1 };
 
-constexpr int CH = 8192;
+constexpr int CH = 8192;  // tokens per slice (the exact path, dist, and the verify and pick passes walk rows in these)
 // gse_sample_noalloc's static workspace: batches of at most this many rows of at most this many tokens.
 constexpr uint32_t NOALLOC_ROWS = 32;
 constexpr uint32_t NOALLOC_VOCAB = 163840;
-static_assert(NOALLOC_ROWS == GSE_NOALLOC_ROWS && NOALLOC_VOCAB == GSE_NOALLOC_VOCAB, "gse.h states the limits");  // tokens per slice (the exact path, dist, and the verify and pick passes walk rows in these)
+static_assert(NOALLOC_ROWS == GSE_NOALLOC_ROWS && NOALLOC_VOCAB == GSE_NOALLOC_VOCAB, "gse.h states the limits");
 
 constexpr int CAPW = 512;   // candidates listed per wave per part
 constexpr int PWAVES = 4;   // waves per part workgroup
 constexpr int MAXP = 64;    // parts per row
 constexpr int PTOK = 65536; // tokens per part, at most
+constexpr int PTOK_PLAIN = 131072;  // tokens per part, at most, in a call with no histories and no masks (no part-sized
+                                    // LDS tables: the parts are twice as long and the listing targets twice as high)
+constexpr int KT = 222;       // tokens of a part of at most PTOK tokens its listing threshold aims to leave above it
 constexpr int PCHUNK = 1024;  // part lengths are multiples of this (one wave chunk)
 constexpr int PMIN = 8192;    // tokens per part, at least, when a small batch is split to fill the device: every part
                               // lists its own candidates, so more parts make a longer row resolve
@@ -128,6 +131,7 @@ struct ScanArgs {
   int64_t ld;
   int dtype, V, rows, nch, mode, force_exact, xcd_map;
   int nparts, plen;  // the main pass: parts per row, tokens per part (a multiple of 1024; the last part may be shorter)
+  int kt, vfirst;    // tokens of a part its listing threshold aims to leave above it; list length that first opens the valve
   int pmajor;        // workgroup L streams part L / rows8 of row L % rows8 (else the parts of a row are consecutive)
   const gse_row *params;
   const int32_t *mask;

@@ -15,9 +15,9 @@
 // wave does not list, from v_exp_f32 with a rigorous error bound (rescaled in fp64 when a lane's maximum rises). The
 // row history's tokens of the part (penalties: counts from an LDS table indexed by rank) take a side pass with the same
 // arithmetic. The part's listing threshold is the kp-th largest of the 256 lane maxima of its waves' first chunks (to
-// 16 key bits; kp aims at KT tokens of the part above it, scaled by the exact counts of allowed tokens in the sample and
-// in the part); a wave whose list passes a quarter of its capacity raises its own to the KV-th largest of its running
-// lane maxima. Every element at or above the threshold in force when it is processed is listed (z bits, id);
+// 16 key bits; kp aims at a.kt tokens of the part above it (KT, or more in proportion for a part longer than PTOK),
+// scaled by the exact counts of allowed tokens in the sample and in the part); a wave whose list passes a.vfirst
+// (a quarter of its capacity at KT) raises its own to the KV-th largest of its running lane maxima. Every element at or above the threshold in force when it is processed is listed (z bits, id);
 // thresholds only rise, so a wave's list certifies its top elements down to its final threshold.
 //
 // Row resolve: the union of the waves' lists cut at the largest certified key is the row's certified head: exactly its
@@ -35,9 +35,8 @@ namespace {
 
 using namespace strm;
 
-constexpr int KT = 222;                // tokens of a part its listing threshold aims to leave above it
 constexpr int KV = 32;                 // rank, among a wave's running lane maxima, of its raised threshold (when its
-                                       // list passes a quarter of its capacity)
+                                       // list passes a.vfirst entries)
 constexpr int NH = 2048;               // certified head capacity of the row resolve
 constexpr int NBK = 512;               // key buckets of the head sort
 constexpr int BKT = 64;                // largest bucket the head sort ranks by counting (else: bitonic)
@@ -555,9 +554,9 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
 // The stream carries every token of the part below pv (the part end, rounded down to a whole vector for aligned rows)
 // except the tokens of the row's history: those (at most a few hundred per part) and the ragged tokens [pv, p1) are
 // penalized and masked by a side pass with exactly the same arithmetic, and enter the same running state out of order.
-// Every chunk issues the same loads (a vector past pv loads the row's next tokens, or zeros past the row's end, and is
-// ignored), so the compiler can count the loads in flight: each wave keeps two chunks loading while it works on a
-// third. The stream needs no per-element branch: the mask and the history exclusion are one bit select per element,
+// Every chunk issues the same loads (a vector past pv loads the part's next tokens, or zeros past the part's end, and is
+// ignored), so the compiler can count the loads in flight: each wave keeps three or five chunks loading while it works
+// on one. The stream needs no per-element branch: the mask and the history exclusion are one bit select per element,
 // the listing is skipped for a whole chunk when the lane maxima lie below the threshold, and the unlisted terms are
 // summed in fp32 per chunk.
 
@@ -576,6 +575,8 @@ struct Run {
   float R;         // z(xt): every unlisted element has z <= R
   float c1, c0;    // the exponent of an unlisted term: t = fma(x, c1, c0), (x / T - R) log2(e) rounded
   double bR;       // the part of a term's error bound that grows with |R| (the roundings of z, c1 and c0)
+  float kb;        // a stream chunk's bound factor on its sum (EPL terms a lane): (2.4e-7 + 3 6e-8 + 5e-8 + bR), raised
+                   // by 2^-20 relative to cover the fp32 rounding of the chunk's bound (uniform)
   uint32_t kcert;  // certified key of z: every element with key >= kcert is listed (fkey(R) + 1)
   bool ovf;        // c0 out of the fp32 range: the part's sums cannot be trusted
   uint32_t woff;   // elements the wave has listed (uniform)
@@ -583,6 +584,7 @@ struct Run {
   float g;         // greedy rows: largest nan_to_num(x) so far, at the lowest token gid holding it
   uint32_t gid;
   uint32_t fid;    // lowest token of this lane with x not NaN (found in the lane's first chunk)
+  bool fid_all;    // every lane of the wave has found its fid (uniform): the stream's chunks skip the search
   uint64_t nanm;   // lanes that saw a NaN before the mask (wave-uniform)
 };
 
@@ -594,52 +596,94 @@ __device__ __forceinline__ float keep_or_ninf(float x, uint32_t keep, int k) {
   return __uint_as_float((__float_as_uint(x) & sel) | (0xFF800000u & ~sel));
 }
 
-// Buffer resources of the row's logits and mask words: 32-bit offsets from a scalar base (no per-lane 64-bit address
-// arithmetic), and a load at or past the end of the row returns zeros instead of reading past it.
-struct RowBufs {
-  __amdgpu_buffer_rsrc_t x, m;
+// The wave's next chunk for the aligned loads: its first byte and the bytes left in the part, of the logits and of the
+// mask words, stepped by one wave stride per chunk (scalar arithmetic). Each load goes through a buffer resource based
+// at the chunk, so a lane's offsets are the same in every chunk (no per-chunk vector arithmetic), and a load at or past
+// the part's end returns zeros without a memory access (a chunk past the part has an empty range).
+struct Cursor {
+  const char *x, *m;
+  int xn, mn;
 };
-__device__ __forceinline__ RowBufs row_bufs(const RowCtx &c) {
-  constexpr int FMT = 0x00020000;  // raw 32-bit buffer (GFX9 resource word 3)
-  RowBufs r;
-  r.x = __builtin_amdgcn_make_buffer_rsrc((void *)c.base, (short)0, c.V * (c.dtype == GSE_BF16 ? 2 : 4), FMT);
-  r.m = __builtin_amdgcn_make_buffer_rsrc((void *)c.mw, (short)0, c.mw ? (c.V + 31) / 32 * 4 : 0, FMT);
+template <int DT>
+__device__ __forceinline__ Cursor cursor(const RowCtx &c, int cb, int p1) {
+  constexpr int ES = DT == GSE_F32 ? 4 : 2;
+  Cursor r;
+  r.x = c.base + (size_t)cb * ES;
+  r.xn = (p1 - cb) * ES;
+  r.m = c.mw ? (const char *)c.mw + (cb >> 5) * 4 : nullptr;  // (aligned rows: cb is a multiple of 32)
+  r.mn = (((p1 + 31) >> 5) - (cb >> 5)) * 4;
   return r;
 }
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rsrc(const char *base, int bytes) {
+  constexpr int FMT = 0x00020000;  // raw 32-bit buffer (GFX9 resource word 3)
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, max(bytes, 0), FMT);
+}
 
-// One chunk's logits and mask words, the same loads for every chunk. Aligned rows: one 16-byte buffer load per vector
-// (a vector past the stream end pv loads the row's next tokens, or zeros past the row, and is ignored: its tokens are
-// not in the chunk's in-range bits); unaligned rows load element by element, clamped to the part.
+// One chunk's logits and mask words, the same loads for every chunk, as raw words: a lane's EPL logits of the chunk
+// (fp32 bits, or bf16 pairs, token 2i in the low half of word i) stay packed until the chunk is processed, so that no
+// arithmetic on a loaded value sits between the loads in flight and the loop's back edge (bf16 rows unpacked at load
+// time made every iteration wait for all three chunks ahead). Aligned rows: one 16-byte buffer load per vector (a vector
+// past the stream end pv loads the part's next tokens, or zeros past the part, and is ignored: its tokens are not in the
+// chunk's in-range bits); unaligned rows load element by element, clamped to the part.
+template <int DT>
+constexpr int RAW = Lay<DT>::NV * 4;  // raw words of a lane's chunk
+// Aligned rows read chunk cur and step cur to the wave's next chunk; unaligned rows read chunk cb.
 template <int DT, bool AL, bool MASKED>
-__device__ __forceinline__ void load_u(const RowCtx &c, const RowBufs &rb, int cb, int pv, int p1, float (&x)[EPL],
+__device__ __forceinline__ void load_u(const RowCtx &c, Cursor &cur, int cb, int pv, int p1, uint32_t (&r)[RAW<DT>],
                                        uint32_t (&mw)[Lay<DT>::NV]) {
   using L = Lay<DT>;
+  constexpr int ES = DT == GSE_F32 ? 4 : 2;
+  constexpr int DX = NWV * CHK * ES, DM = NWV * CHK / 8;  // one wave stride, in logit and mask bytes
   const int l = lane_id();
+  __amdgpu_buffer_rsrc_t rx, rm;
+  if constexpr (AL) {
+    rx = chunk_rsrc(cur.x, cur.xn);
+    cur.x += DX;
+    cur.xn -= DX;
+    if constexpr (MASKED) {
+      rm = chunk_rsrc(cur.m, cur.mn);
+      cur.m += DM;
+      cur.mn -= DM;
+    }
+  }
 #pragma unroll
   for (int v = 0; v < L::NV; ++v) {
     const int t0 = cb + v * L::STRIDE + l * L::VEC;
+    const int o = v * L::STRIDE + l * L::VEC;  // t0 - cb
     if constexpr (MASKED) {
-      if constexpr (AL) mw[v] = __builtin_amdgcn_raw_buffer_load_b32(rb.m, (t0 >> 5) * 4, 0, 0);
+      if constexpr (AL) mw[v] = __builtin_amdgcn_raw_buffer_load_b32(rm, (o >> 5) * 4, 0, 0);
       else mw[v] = c.mw[min(t0, p1 - 1) >> 5];
     }
     if constexpr (AL) {
-      const auto u = __builtin_amdgcn_raw_buffer_load_b128(rb.x, t0 * (DT == GSE_F32 ? 4 : 2), 0, 0);
-      if constexpr (DT == GSE_F32) {
+      const auto u = __builtin_amdgcn_raw_buffer_load_b128(rx, o * ES, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[4 * v + i] = __uint_as_float(u[i]);
-      } else {
+      for (int i = 0; i < 4; ++i) r[4 * v + i] = u[i];
+    } else if constexpr (DT == GSE_F32) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          x[8 * v + 2 * i] = __uint_as_float(u[i] << 16);
-          x[8 * v + 2 * i + 1] = __uint_as_float(u[i] & 0xFFFF0000u);
-        }
-      }
+      for (int k = 0; k < L::VEC; ++k) r[v * L::VEC + k] = __float_as_uint(load_one(c, min(t0 + k, p1 - 1)));
     } else {
+      const uint16_t *b = (const uint16_t *)c.base;
 #pragma unroll
-      for (int k = 0; k < L::VEC; ++k) x[v * L::VEC + k] = load_one(c, min(t0 + k, p1 - 1));
+      for (int k = 0; k < L::VEC / 2; ++k)
+        r[4 * v + k] = (uint32_t)b[min(t0 + 2 * k, p1 - 1)] | ((uint32_t)b[min(t0 + 2 * k + 1, p1 - 1)] << 16);
     }
   }
   (void)pv;
+}
+
+// The chunk's logits from its raw words (bf16: the value's bits in the high half of an fp32)
+template <int DT>
+__device__ __forceinline__ void unpack(const uint32_t (&r)[RAW<DT>], float (&x)[EPL]) {
+  if constexpr (DT == GSE_F32) {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) x[i] = __uint_as_float(r[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < RAW<DT>; ++i) {
+      x[2 * i] = __uint_as_float(r[i] << 16);
+      x[2 * i + 1] = __uint_as_float(r[i] & 0xFFFF0000u);
+    }
+  }
 }
 
 // The history words of a chunk's vectors (bit o of the part's history bitset = token p0 + o is in the row's history),
@@ -677,11 +721,13 @@ __device__ __forceinline__ void put_proc(float *p, bool p16, const float *x, uin
 // x of a full chunk (every token below the stream end) of a sampled row in place: the keep bits of each vector, mask AND
 // NOT history, from the raw words with one bit-field extract; the NaN flag; -inf where a token is not kept (no select
 // when the whole wave's chunk keeps everything); the lane's chunk maximum. The same results as chunk_z for such a chunk,
-// with the range tests and shifts of the general chunk left out.
-template <int DT, bool MASKED>
+// with the range tests and shifts of the general chunk left out. PLAIN: a row with no mask and no penalties, whose
+// tokens the stream all keeps (no keep bits, no select).
+template <int DT, bool MASKED, bool PLAIN>
 __device__ __forceinline__ float chunk_x_full(const RowCtx &c, int cb, float (&xr)[EPL], const uint32_t (&mw)[Lay<DT>::NV],
                                               const uint32_t (&hw)[Lay<DT>::NV], Run &rn, float *proc) {
   using L = Lay<DT>;
+  static_assert(!(PLAIN && MASKED), "");
   constexpr uint32_t VMASK = (1u << L::VEC) - 1u;
   const int l = lane_id();
   const uint32_t sh = (uint32_t)(l * L::VEC) & 31u;
@@ -689,10 +735,14 @@ __device__ __forceinline__ float chunk_x_full(const RowCtx &c, int cb, float (&x
   bool full = true;
 #pragma unroll
   for (int v = 0; v < L::NV; ++v) {
-    uint32_t w = MASKED ? mw[v] : 0xFFFFFFFFu;
-    if (c.pen) w &= ~hw[v];
-    keep[v] = __builtin_amdgcn_ubfe(w, sh, (uint32_t)L::VEC);
-    full = full && keep[v] == VMASK;
+    if constexpr (PLAIN) {
+      keep[v] = VMASK;
+    } else {
+      uint32_t w = MASKED ? mw[v] : 0xFFFFFFFFu;
+      if (c.pen) w &= ~hw[v];
+      keep[v] = __builtin_amdgcn_ubfe(w, sh, (uint32_t)L::VEC);
+      full = full && keep[v] == VMASK;
+    }
   }
   if (proc) {  // processed logits (after penalties and mask, before T) of the streamed (non-history) tokens
     const bool p16 = ((uintptr_t)proc & 15u) == 0;
@@ -700,14 +750,14 @@ __device__ __forceinline__ float chunk_x_full(const RowCtx &c, int cb, float (&x
     for (int v = 0; v < L::NV; ++v) {
       const int t0 = cb + v * L::STRIDE + l * L::VEC;
       const uint32_t al = MASKED ? __builtin_amdgcn_ubfe(mw[v], sh, (uint32_t)L::VEC) : VMASK;
-      const uint32_t hx = c.pen ? __builtin_amdgcn_ubfe(hw[v], sh, (uint32_t)L::VEC) : 0u;
+      const uint32_t hx = !PLAIN && c.pen ? __builtin_amdgcn_ubfe(hw[v], sh, (uint32_t)L::VEC) : 0u;
       put_proc<L::VEC>(proc + t0, p16, xr + v * L::VEC, al, hx);
     }
   }
 #pragma unroll
   for (int i = 0; i < EPL; i += 2) rn.nanm |= ballot64(__builtin_isunordered(xr[i], xr[i + 1]));  // (a NaN in either)
   float cmax = -INFINITY;
-  if (ballot64(!full) == 0ull) {
+  if (PLAIN || ballot64(!full) == 0ull) {
 #pragma unroll
     for (int i = 0; i < EPL; ++i) cmax = fmaxf(cmax, xr[i]);
   } else {
@@ -721,12 +771,15 @@ __device__ __forceinline__ float chunk_x_full(const RowCtx &c, int cb, float (&x
       }
     }
   }
-  if (rn.fid == 0xFFFFFFFFu) {  // (only until the lane has seen a value that is not NaN)
+  if (!rn.fid_all) {  // (only until every lane has seen a value that is not NaN)
+    if (rn.fid == 0xFFFFFFFFu) {
 #pragma unroll
-    for (int i = EPL - 1; i >= 0; --i) {
-      const int t = cb + (i / L::VEC) * L::STRIDE + l * L::VEC + (i % L::VEC);
-      if (xr[i] == xr[i]) rn.fid = (uint32_t)t;
+      for (int i = EPL - 1; i >= 0; --i) {
+        const int t = cb + (i / L::VEC) * L::STRIDE + l * L::VEC + (i % L::VEC);
+        if (xr[i] == xr[i]) rn.fid = (uint32_t)t;
+      }
     }
+    rn.fid_all = ballot64(rn.fid == 0xFFFFFFFFu) == 0ull;
   }
   return cmax;
 }
@@ -790,12 +843,15 @@ __device__ __forceinline__ float chunk_z(const RowCtx &c, int cb, int p0, int pv
       }
     }
   }
-  if (rn.fid == 0xFFFFFFFFu) {  // the lane's first chunk: its lowest token whose value is not NaN
+  if (!rn.fid_all) {  // the lane's first chunk: its lowest token whose value is not NaN
+    if (rn.fid == 0xFFFFFFFFu) {
 #pragma unroll
-    for (int i = EPL - 1; i >= 0; --i) {
-      const int t = cb + (i / L::VEC) * L::STRIDE + l * L::VEC + (i % L::VEC);
-      if (t < p1 && xr[i] == xr[i]) rn.fid = (uint32_t)t;
+      for (int i = EPL - 1; i >= 0; --i) {
+        const int t = cb + (i / L::VEC) * L::STRIDE + l * L::VEC + (i % L::VEC);
+        if (t < p1 && xr[i] == xr[i]) rn.fid = (uint32_t)t;
+      }
     }
+    rn.fid_all = ballot64(rn.fid == 0xFFFFFFFFu) == 0ull;
   }
   return cmax;
 }
@@ -812,6 +868,20 @@ __device__ __forceinline__ float pairwise(F &f) {
     const float y = pairwise<MID, HI>(f);
     return x + y;
   }
+}
+
+// The bound factor of a stream chunk's sum (EPL = 8 terms a lane: three levels of pairwise additions), raised by 2^-20
+// relative so that the fp32 arithmetic of the chunk's bound (two fmas of non-negative terms, 2^-23 relative at most)
+// stays inside it.
+__device__ __forceinline__ float chunk_bound_factor(double bR) {
+  return (float)((2.4e-7 + 3.0 * 6.0e-8 + 5e-8 + bR) * (1.0 + 0x1p-20));
+}
+
+// max(a, b) of two values that are never signaling NaNs, one v_max_f32 (fmaxf first quiets both operands)
+__device__ __forceinline__ float fmax_q(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
 }
 
 // Raises the wave's listing threshold to the x key k (uniform): xt = the value of k, R = z(xt), and the lanes' sums
@@ -831,6 +901,7 @@ __device__ __forceinline__ void set_threshold(Run &rn, uint32_t k, bool divide, 
   rn.ovf = rn.ovf || (fin && !(fabs(cr) <= 3.4028234663852886e38));
   rn.c0 = fin && fabs(cr) <= 3.4028234663852886e38 ? (float)cr : -INFINITY;
   rn.bR = fin ? 1.8e-7 * fabs((double)R) : 0.0;
+  rn.kb = chunk_bound_factor(rn.bR);
   rn.xkey = k;
   rn.xt = xt;
   rn.R = R;
@@ -844,7 +915,7 @@ template <int N, typename Tok>
 __device__ __forceinline__ void chunk_sum(const ScanArgs &a, int row, int wl, float cmax, const float (&xr)[N],
                                           Run &rn, Tok tok, bool divide, double Rd) {
   static_assert((N & (N - 1)) == 0 && N <= 256, "");
-  rn.m = fmaxf(rn.m, cmax);
+  rn.m = fmax_q(rn.m, cmax);
   if (rn.woff >= rn.vnext) {  // (again after every KV / 2 more listed elements)
     const uint32_t k = max(rn.xkey, wave_kth_largest_u16(fkey(rn.m) >> 16, KV) << 16);
     if (k > rn.xkey) set_threshold(rn, k, divide, Rd);
@@ -888,7 +959,12 @@ __device__ __forceinline__ void chunk_sum(const ScanArgs &a, int row, int wl, fl
   // own rounding (2^-24 |t|): times ln 2, 1.8e-7 |R| (bR) + 1.25e-7 |t| (mom = -sum e |t|)
   constexpr double LV = N >= 16 ? 4.0 : N >= 8 ? 3.0 : N >= 4 ? 2.0 : 1.0;
   rn.s += (double)s;
-  rn.b += (double)s * (2.4e-7 + LV * 6.0e-8 + 5e-8 + rn.bR) - (double)mom * 1.25e-7 + 1e-36;
+  if constexpr (N == EPL) {  // a stream chunk: its bound in fp32 (kb: the factor above, raised to cover this rounding)
+    static_assert(EPL == 8, "kb is the factor of three pairwise levels");
+    rn.b += (double)fmaf(s, rn.kb, fmaf(-mom, 1.2500012e-7f, 1e-36f));
+  } else {
+    rn.b += (double)s * (2.4e-7 + LV * 6.0e-8 + 5e-8 + rn.bR) - (double)mom * 1.25e-7 + 1e-36;
+  }
 }
 
 // Tokens outside the stream (history tokens with their counts, ragged tokens with count 0; tok < 0: empty slot), with
@@ -928,7 +1004,8 @@ __device__ __forceinline__ void side_tokens(const ScanArgs &a, const RowCtx &c, 
 }
 
 // One part [p0, p1) of the row. Returns true in the workgroup that finished the row last (it then resolves the row).
-template <int DT, bool AL, bool MASKED, bool GREEDY, bool DIV>
+// PC: a call with no histories and no masks (its own kernel: every row takes the plain stream).
+template <int DT, bool AL, bool MASKED, bool GREEDY, bool DIV, bool PC>
 __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, const RowCtx &c, int row, int part,
                                           Shared &sh) {
   using L = Lay<DT>;
@@ -951,15 +1028,21 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
       hid[k] = j < c.he ? a.hist[j] : -1;
     }
   }
-  const RowBufs rbuf = row_bufs(c);
-  float xa[EPL], xb[EPL], xc[EPL], xd[EPL];
-  uint32_t ma[L::NV], mb[L::NV], mcw[L::NV], md[L::NV];
-  uint32_t ha[L::NV] = {}, hb[L::NV] = {}, hc[L::NV] = {}, hd[L::NV] = {};  // history words (penalized rows)
+  Cursor cur = cursor<DT>(c, p0 + __builtin_amdgcn_readfirstlane(w) * CHK, p1);
+  // A ring of NB chunk buffers: chunk j of the wave (token chunk wu + j NWV) in slot j % NB, NB - 1 chunks loading while
+  // the wave works on one. bf16 rows of the plain kernel keep six (4 registers a chunk, 1 KB a wave: five in flight
+  // carry 80 KB a CU, where three left the stream short of bytes in flight to cover the memory latency); the others four
+  // (no registers to spare).
+  constexpr int NB = (DT == GSE_BF16 && PC) ? 6 : 4;
+  uint32_t xr[NB][RAW<DT>];
+  uint32_t mk[NB][L::NV];
+  uint32_t hk[NB][L::NV] = {};  // history words (penalized rows)
   const int wu = __builtin_amdgcn_readfirstlane(w);  // (the wave index as a scalar: the chunk loop stays uniform)
-  int c0 = wu, c1 = wu + NWV, c3 = wu + 2 * NWV;  // wave w takes chunks w, w + 4, w + 8, ...
-  // First token of chunk ck for its loads. A chunk past the stream gets a start far past the row (vocabularies are at
-  // most 2^21 tokens): its buffer loads fail the range check and return zeros without a memory access (unaligned rows
-  // clamp to the part instead), so the loads a wave issues ahead of its last chunk fetch nothing.
+  const int c0 = wu;  // wave w takes chunks w, w + 4, w + 8, ...
+  // First token of chunk ck (unaligned rows' loads, the history words). A chunk past the stream gets a start far past
+  // the row (vocabularies are at most 2^21 tokens); the loads of unaligned rows clamp to the part, and aligned rows read
+  // through the cursor, whose range ends at the part's end: the loads a wave issues ahead of its last chunk fetch
+  // nothing.
   const auto cst = [&](int ck) -> int { return ck < nck ? p0 + ck * CHK : (1 << 28); };
   // allowed tokens of the part's stream range (masked rows: popcounts of its mask words, every load issued before the
   // first is used; the sum comes after the history build)
@@ -980,9 +1063,8 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   if (c.pen) asm volatile("" ::"v"(hid[0]), "v"(hid[1]), "v"(hid[2]), "v"(hid[3]), "v"(hid[4]), "v"(hid[5]),
                           "v"(hid[6]), "v"(hid[7]));
   static_assert(HPT == 8, "");
-  load_u<DT, AL, MASKED>(c, rbuf, cst(c0), pv, p1, xa, ma);
-  load_u<DT, AL, MASKED>(c, rbuf, cst(c1), pv, p1, xb, mb);
-  load_u<DT, AL, MASKED>(c, rbuf, cst(c3), pv, p1, xd, md);
+#pragma unroll
+  for (int j = 0; j < 3; ++j) load_u<DT, AL, MASKED>(c, cur, cst(wu + j * NWV), pv, p1, xr[j], mk[j]);
   if (tid == 0) sh.hover = 0;
   if (c.pen) build_history(c, a.hist, hid, p0, p1, sh.h, sh.wcnt, sh.hover);
   else __syncthreads();
@@ -1017,10 +1099,9 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     }
   }
 
-  if (c.pen) {  // (the first two chunks were loaded before the history tables existed)
-    hist_words<DT>(sh.h, cst(c0), p0, p1, ha);
-    hist_words<DT>(sh.h, cst(c1), p0, p1, hb);
-    hist_words<DT>(sh.h, cst(c3), p0, p1, hd);
+  if (c.pen) {  // (the first three chunks were loaded before the history tables existed)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) hist_words<DT>(sh.h, cst(wu + j * NWV), p0, p1, hk[j]);
   }
   Run rn;
   rn.m = -INFINITY;
@@ -1032,35 +1113,33 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   rn.c1 = DIV ? (float)(1.4426950408889634 * c.Rd) : LOG2E;  // RN(log2(e) / T)
   rn.c0 = -INFINITY;
   rn.bR = 0.0;
+  rn.kb = chunk_bound_factor(0.0);
   rn.kcert = 0;
   rn.ovf = false;
   rn.woff = 0;
-  rn.vnext = CAPW / 4 + 1;
+  rn.vnext = (uint32_t)a.vfirst;
   rn.g = -INFINITY;
   rn.gid = 0xFFFFFFFFu;
   rn.fid = 0xFFFFFFFFu;
+  rn.fid_all = false;
   rn.nanm = 0;
-  // the next chunks (scalar arithmetic: no LDS round trip and no vector temporary between a chunk's loads and its use)
-  int nxt = wu + 3 * NWV;
-  auto grab = [&]() -> int {
-    const int n = nxt;
-    nxt += NWV;
-    return n;
-  };
   auto tok_of = [&](int cb) {
     return [=](int i) { return (uint32_t)(cb + (i / L::VEC) * L::STRIDE + lane * L::VEC + (i % L::VEC)); };
   };
   // First chunk of each wave; the part's listing threshold from the 256 lane maxima.
   float cmax = -INFINITY;
-  if (c0 < nck) cmax = chunk_z<DT, AL, MASKED, GREEDY>(c, p0 + c0 * CHK, p0, pv, p1, xa, ma, ha, rn, proc);
+  float x0[EPL];
+  unpack<DT>(xr[0], x0);
+  if (c0 < nck) cmax = chunk_z<DT, AL, MASKED, GREEDY>(c, p0 + c0 * CHK, p0, pv, p1, x0, mk[0], hk[0], rn, proc);
   if (listing) {
     // The listing threshold: the rank-kp largest of the 256 lane maxima of the waves' first chunks (a 2048-token
     // sample). kp is scaled so that about T tokens of the part lie above it: kp = T * (allowed tokens in the sample) /
     // (allowed tokens in the part), counted exactly, so that a mask whose allowed tokens cluster in runs does not skew
-    // it. T = 222, or 3 top_k + 32 (at most 444) for rows that keep at most top_k elements.
+    // it. T = a.kt (222 for a part of at most PTOK tokens), or 3 top_k + 32 (at most 2 a.kt) for rows that keep at
+    // most top_k elements.
     uint32_t as = 0;
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) as += xa[i] > -INFINITY ? 1u : 0u;
+    for (int i = 0; i < EPL; ++i) as += x0[i] > -INFINITY ? 1u : 0u;
     if (c0 >= nck) as = 0;
     as = wave_sum_u32(as);
     apc = wave_sum_u32(apc);
@@ -1077,9 +1156,10 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
       As += sh.wkap[q];
       Ap += sh.wflags[q];
     }
-    const uint32_t T = P.top_k > 0 ? min(2u * KT, (uint32_t)(3 * max(P.top_k, nlp_of(a, P)) + 32)) : (uint32_t)KT;
+    const uint32_t kt = (uint32_t)a.kt;
+    const uint32_t T = P.top_k > 0 ? min(2u * kt, (uint32_t)(3 * max(P.top_k, nlp_of(a, P)) + 32)) : kt;
     // (a sample with few allowed tokens estimates nothing: then the lowest lane maximum, and the valve bounds the lists)
-    const uint32_t kp = As < 16u ? max(act, 1u) : max(1u, min(act, (T * As + Ap - 1) / max(Ap, 1u)));  // (T As < 2^20)
+    const uint32_t kp = As < 16u ? max(act, 1u) : max(1u, min(act, (T * As + Ap - 1) / max(Ap, 1u)));  // (T As < 2^22)
     uint32_t r = 0;
 #pragma unroll
     for (int b = 15; b >= 0; --b) {
@@ -1091,10 +1171,12 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     }
     set_threshold(rn, max(r << 16, KEY_NEGINF + 1u), DIV, c.Rd);
   }
-  int c2 = grab();
-  load_u<DT, AL, MASKED>(c, rbuf, cst(c2), pv, p1, xc, mcw);
+#pragma unroll
+  for (int j = 3; j < NB; ++j) {
+    load_u<DT, AL, MASKED>(c, cur, cst(wu + j * NWV), pv, p1, xr[j], mk[j]);
+    if (c.pen) hist_words<DT>(sh.h, cst(wu + j * NWV), p0, p1, hk[j]);
+  }
   if (c.pen) {
-    hist_words<DT>(sh.h, cst(c2), p0, p1, hc);
     const uint32_t nd = sh.h.nd;
 #pragma unroll
     for (int k = 0; k < KHP; ++k) {  // (rank r is this thread's in the side pass too: no barrier)
@@ -1106,45 +1188,56 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     }
   }
   if (c0 < nck) {
-    if (listing) chunk_sum<EPL>(a, row, wl, cmax, xa, rn, tok_of(p0 + c0 * CHK), DIV, c.Rd);
-    else rn.m = fmaxf(rn.m, cmax);
+    if (listing) chunk_sum<EPL>(a, row, wl, cmax, x0, rn, tok_of(p0 + c0 * CHK), DIV, c.Rd);
+    else rn.m = fmax_q(rn.m, cmax);
   }
-  // Steady state: three chunks loading while the wave works on a fourth (chunk indices rise, so the first past the end
-  // ends the wave's stream). In processing order: b, d, c, a, b, d, ... (a was processed above).
-  auto step = [&](int ck, float(&x)[EPL], const uint32_t(&mw)[L::NV], const uint32_t(&hw)[L::NV])
-                  __attribute__((always_inline)) {
-    float cm;
-    if (!GREEDY && AL && p0 + (ck + 1) * CHK <= pv) {  // a full chunk (uniform): the lean path
-      cm = chunk_x_full<DT, MASKED>(c, p0 + ck * CHK, x, mw, hw, rn, proc);
-    } else {
-      cm = chunk_z<DT, AL, MASKED, GREEDY>(c, p0 + ck * CHK, p0, pv, p1, x, mw, hw, rn, proc);
+  // Steady state: chunk j of the wave is wu + j NWV (scalar arithmetic: no LDS round trip and no vector temporary
+  // between a chunk's loads and its use); chunks 1 .. NB - 1 are loading and each step issues the load of the chunk
+  // NB - 1 ahead into the slot the previous step freed. The loop runs whole rounds of NB steps (the loads past the wave's
+  // last chunk fetch nothing, their steps are skipped) with one back edge and the loads issued in the same order before
+  // it and in it: the wait before each step then leaves the newer loads in flight (a loop with an exit in every step,
+  // or loads issued in another order before it, made the first step of every round wait for all of them). The kernel of a call with no masks and no histories streams with the keep bits compiled out.
+  const int nw = wu < nck ? (nck - wu + NWV - 1) / NWV : 0;  // the wave's chunks (uniform)
+  auto stream = [&](auto plain) __attribute__((always_inline)) {
+    constexpr bool PLAIN = decltype(plain)::value;
+    const bool pen = !PLAIN && c.pen;
+    auto step = [&](int ck, const uint32_t(&raw)[RAW<DT>], const uint32_t(&mw)[L::NV], const uint32_t(&hw)[L::NV])
+                    __attribute__((always_inline)) {
+      float x[EPL];
+      unpack<DT>(raw, x);
+      const bool full = !GREEDY && AL && p0 + (ck + 1) * CHK <= pv;  // a full chunk (uniform): the lean path
+      if constexpr (PLAIN) {  // (each path ends with its own sum: the two do not join with x in different registers)
+        if (full) {
+          const float cm = chunk_x_full<DT, MASKED, PLAIN>(c, p0 + ck * CHK, x, mw, hw, rn, proc);
+          if (listing) chunk_sum<EPL>(a, row, wl, cm, x, rn, tok_of(p0 + ck * CHK), DIV, c.Rd);
+          else rn.m = fmax_q(rn.m, cm);
+        } else {
+          const float cm = chunk_z<DT, AL, MASKED, GREEDY>(c, p0 + ck * CHK, p0, pv, p1, x, mw, hw, rn, proc);
+          if (listing) chunk_sum<EPL>(a, row, wl, cm, x, rn, tok_of(p0 + ck * CHK), DIV, c.Rd);
+          else rn.m = fmax_q(rn.m, cm);
+        }
+      } else {  // (one sum: the general kernel holds no registers to spare for a second copy)
+        const float cm = full ? chunk_x_full<DT, MASKED, PLAIN>(c, p0 + ck * CHK, x, mw, hw, rn, proc)
+                              : chunk_z<DT, AL, MASKED, GREEDY>(c, p0 + ck * CHK, p0, pv, p1, x, mw, hw, rn, proc);
+        if (listing) chunk_sum<EPL>(a, row, wl, cm, x, rn, tok_of(p0 + ck * CHK), DIV, c.Rd);
+        else rn.m = fmax_q(rn.m, cm);
+      }
+    };
+    auto fetch = [&](int j, uint32_t(&raw)[RAW<DT>], uint32_t(&mw)[L::NV], uint32_t(&hw)[L::NV])
+                     __attribute__((always_inline)) {
+      const int ck = wu + j * NWV;
+      load_u<DT, AL, MASKED>(c, cur, cst(ck), pv, p1, raw, mw);
+      if (pen) hist_words<DT>(sh.h, cst(ck), p0, p1, hw);
+    };
+    for (int j = 1; j < nw; j += NB) {  // (j % NB == 1: step s works on slot (s + 1) % NB, and refills slot s)
+#pragma unroll
+      for (int q = 0; q < NB; ++q) {
+        fetch(j + q + NB - 1, xr[q], mk[q], hk[q]);
+        if (q == 0 || j + q < nw) step(wu + (j + q) * NWV, xr[(q + 1) % NB], mk[(q + 1) % NB], hk[(q + 1) % NB]);
+      }
     }
-    if (listing) chunk_sum<EPL>(a, row, wl, cm, x, rn, tok_of(p0 + ck * CHK), DIV, c.Rd);
-    else rn.m = fmaxf(rn.m, cm);
   };
-  // (c2 was issued above; c3 before the history build: processing order c1, c3, c2, then the next grabs)
-  while (true) {
-    c0 = grab();
-    load_u<DT, AL, MASKED>(c, rbuf, cst(c0), pv, p1, xa, ma);
-    if (c.pen) hist_words<DT>(sh.h, cst(c0), p0, p1, ha);
-    if (c1 >= nck) break;
-    step(c1, xb, mb, hb);
-    c1 = grab();
-    load_u<DT, AL, MASKED>(c, rbuf, cst(c1), pv, p1, xb, mb);
-    if (c.pen) hist_words<DT>(sh.h, cst(c1), p0, p1, hb);
-    if (c3 >= nck) break;
-    step(c3, xd, md, hd);
-    c3 = grab();
-    load_u<DT, AL, MASKED>(c, rbuf, cst(c3), pv, p1, xd, md);
-    if (c.pen) hist_words<DT>(sh.h, cst(c3), p0, p1, hd);
-    if (c2 >= nck) break;
-    step(c2, xc, mcw, hc);
-    c2 = grab();
-    load_u<DT, AL, MASKED>(c, rbuf, cst(c2), pv, p1, xc, mcw);
-    if (c.pen) hist_words<DT>(sh.h, cst(c2), p0, p1, hc);
-    if (c0 >= nck) break;
-    step(c0, xa, ma, ha);
-  }
+  stream(std::integral_constant<bool, PC>{});
   // the history tokens of the part (the tables are still in LDS: the resolve has not started), then the ragged ones
   if (c.pen) {
     const uint32_t nd = sh.h.nd;
@@ -1244,8 +1337,9 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
   return sh.ticket == (uint32_t)(a.nparts - 1);
 }
 
-// Four waves per SIMD: every workgroup of a 256-row batch is resident at once (4 per CU).
-template <int DT>
+// Four waves per SIMD: every workgroup of a 256-row batch is resident at once (4 per CU). PC: the kernel of a call with
+// no histories and no masks.
+template <int DT, bool PC>
 __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void main_kernel(ScanArgs a) {
   __shared__ Shared sh;
   const int L = blockIdx.x;
@@ -1265,38 +1359,32 @@ __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
   if (row >= a.rows) return;
   if (threadIdx.x < 64) sh.etab[threadIdx.x] = EXP2_64[threadIdx.x];  // (published by the first barrier)
   const gse_row P = a.params[row];
-  const RowCtx c = make_ctx(a, row, P);
+  RowCtx c = make_ctx(a, row, P);
+  if constexpr (PC) {
+    c.mw = nullptr;
+    c.pen = false;
+  }
   // 16-byte vector loads: the row start is 16-byte aligned and the row holds a whole vector (a vector past the stream's
   // end loads the row's first one)
   const bool aligned = (((uintptr_t)c.base) & 15u) == 0 && a.V >= Lay<DT>::VEC;
   // variants: alignment (16-byte vector loads), mask, greedy (no division), division by T (T != 1)
-  bool last;
   // (MASKED variants read the row's mask words unconditionally: only rows with a mask take them)
-  if (c.greedy) {
-    if (c.mw) {
-      last = aligned ? part_body<DT, true, true, true, false>(a, P, c, row, part, sh)
-                     : part_body<DT, false, true, true, false>(a, P, c, row, part, sh);
+  auto run = [&](auto masked) __attribute__((always_inline)) -> bool {
+    constexpr bool M = decltype(masked)::value;
+    if (c.greedy) {
+      return aligned ? part_body<DT, true, M, true, false, PC>(a, P, c, row, part, sh)
+                     : part_body<DT, false, M, true, false, PC>(a, P, c, row, part, sh);
+    } else if (c.divide) {
+      return aligned ? part_body<DT, true, M, false, true, PC>(a, P, c, row, part, sh)
+                     : part_body<DT, false, M, false, true, PC>(a, P, c, row, part, sh);
     } else {
-      last = aligned ? part_body<DT, true, false, true, false>(a, P, c, row, part, sh)
-                     : part_body<DT, false, false, true, false>(a, P, c, row, part, sh);
+      return aligned ? part_body<DT, true, M, false, false, PC>(a, P, c, row, part, sh)
+                     : part_body<DT, false, M, false, false, PC>(a, P, c, row, part, sh);
     }
-  } else if (c.mw) {
-    if (c.divide) {
-      last = aligned ? part_body<DT, true, true, false, true>(a, P, c, row, part, sh)
-                     : part_body<DT, false, true, false, true>(a, P, c, row, part, sh);
-    } else {
-      last = aligned ? part_body<DT, true, true, false, false>(a, P, c, row, part, sh)
-                     : part_body<DT, false, true, false, false>(a, P, c, row, part, sh);
-    }
-  } else {
-    if (c.divide) {
-      last = aligned ? part_body<DT, true, false, false, true>(a, P, c, row, part, sh)
-                     : part_body<DT, false, false, false, true>(a, P, c, row, part, sh);
-    } else {
-      last = aligned ? part_body<DT, true, false, false, false>(a, P, c, row, part, sh)
-                     : part_body<DT, false, false, false, false>(a, P, c, row, part, sh);
-    }
-  }
+  };
+  bool last;
+  if constexpr (PC) last = run(std::false_type{});
+  else last = c.mw ? run(std::true_type{}) : run(std::false_type{});
   if (!last) return;
   // the row resolve is a chain of short dependent steps: give its waves issue priority over the streaming waves of the
   // other workgroups on this CU
@@ -1310,10 +1398,13 @@ __global__ __launch_bounds__(MT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 hipError_t launch_main(const ScanArgs &a, hipStream_t s) {
   const int rows = a.xcd_map ? (a.rows + 7) / 8 * 8 : a.rows;
   dim3 grid((unsigned)(rows * a.nparts)), block(MT);
+  const bool pc = a.hist == nullptr && a.mask == nullptr;
   if (a.dtype == GSE_BF16) {
-    hipLaunchKernelGGL(main_kernel<GSE_BF16>, grid, block, 0, s, a);
+    if (pc) hipLaunchKernelGGL((main_kernel<GSE_BF16, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((main_kernel<GSE_BF16, false>), grid, block, 0, s, a);
   } else {
-    hipLaunchKernelGGL(main_kernel<GSE_F32>, grid, block, 0, s, a);
+    if (pc) hipLaunchKernelGGL((main_kernel<GSE_F32, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((main_kernel<GSE_F32, false>), grid, block, 0, s, a);
   }
   return hipGetLastError();
 }
