@@ -232,12 +232,28 @@ __device__ __forceinline__ void sort_regs(uint64_t (&v)[S], uint64_t *buf) {
   }
 }
 
+// a[0, n) (n <= MT * S, in LDS) sorted descending by sort_regs, tmp (MT * S entries) its buffer; zero pads sort last.
+// Out of line: inlined, its unrolled network held the registers of the code around it (the main pass spilled).
+template <int S>
+__device__ __noinline__ void sort_lds_regs(uint64_t *a, uint64_t *tmp, int n) {
+  const int tid = threadIdx.x;
+  uint64_t v[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) v[s] = tid * S + s < n ? a[tid * S + s] : 0ull;
+  sort_regs<S>(v, tmp);
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+    if (tid * S + s < n) a[tid * S + s] = v[s];
+  __syncthreads();
+}
+
 // Sorts a[0, n) (packed keys, descending: key desc, then token id asc) in place, every key in [klo, khi], by the whole
 // workgroup (MT threads): a counting sort over NB buckets of equal key width (count, scan, scatter into tmp), then each
-// element's rank inside its bucket by counting; a bucket larger than BK (many equal or close keys) makes the whole array
-// take a bitonic sort instead. a and tmp hold at least pow2_ceil(n) entries, bcnt and bofs NB; wsum NWV words, bmax one
-// word of scratch. Rolled loops: compact code (this runs once per row, from a cold instruction cache). Ends with a
-// barrier.
+// element's rank inside its bucket by counting; a bucket larger than BK (many equal or close keys: bf16 logits tie
+// often) makes the whole array take a bitonic sort instead, in registers (sort_regs: four or eight elements a thread,
+// only its three widest steps through LDS) for n <= 8 MT. a and tmp hold at least pow2_ceil(n) entries, bcnt and bofs
+// NB; wsum NWV words, bmax one word of scratch. Rolled loops elsewhere: compact code (this runs once per row, from a
+// cold instruction cache). Ends with a barrier.
 template <int NB, int BK>
 __device__ __forceinline__ void sort_desc_counting(uint64_t *a, uint64_t *tmp, uint32_t *bcnt, uint32_t *bofs,
                                                    uint32_t *wsum, uint32_t *bmax, int n, uint32_t khi, uint32_t klo) {
@@ -287,12 +303,26 @@ __device__ __forceinline__ void sort_desc_counting(uint64_t *a, uint64_t *tmp, u
       const uint64_t v = tmp[i];
       const uint32_t b = (khi - pk_key(v)) >> shift;
       const uint32_t b0 = bofs[b], b1 = bcnt[b];
-      uint32_t r = b0;
+      uint32_t r = b0, q = b0;
+      // (eight reads in flight per round: a bucket of dozens of tied keys, common with bf16 logits, costs a few LDS
+      // round trips instead of one per member)
 #pragma unroll 1
-      for (uint32_t q = b0; q < b1; ++q) r += tmp[q] > v ? 1u : 0u;
+      for (; q + 8 <= b1; q += 8) {
+        uint64_t t[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) t[k] = tmp[q + k];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r += t[k] > v ? 1u : 0u;
+      }
+#pragma unroll 1
+      for (; q < b1; ++q) r += tmp[q] > v ? 1u : 0u;
       a[r] = v;
     }
     __syncthreads();
+  } else if (n <= 4 * MT) {
+    sort_lds_regs<4>(a, tmp, n);
+  } else if (n <= 8 * MT) {
+    sort_lds_regs<8>(a, tmp, n);
   } else {
     int N = 2;
     while (N < n) N <<= 1;
