@@ -285,9 +285,9 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   const int SPEC = max(1, (MT * GPT) / nsl);
   uint64_t pks[GPT];
 #pragma unroll
-  for (int g = 0; g < GPT; ++g) {
-    const int e = g * MT + tid, j = e / SPEC;
-    pks[g] = j < nsl ? ld_ag(&cl0[(size_t)j * CAPW + (e - j * SPEC)]) : 0ull;
+  for (int g = 0; g < GPT; ++g) {  // (unconditional loads, clamped into the row's lists: the batch drops the extra)
+    const int e = g * MT + tid, j = min(e / SPEC, nsl - 1);
+    pks[g] = ld_ag(&cl0[(size_t)j * CAPW + min(e - j * SPEC, CAPW - 1)]);
   }
   const int prt = tid / PWAVES;
   uint32_t r_nc = 0, r_mkey = 0, r_kap = 0, r_fl = 0;
@@ -437,19 +437,34 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   const uint32_t rtot = sh.jcount;
   uint64_t pk[GPT];
   bool okr[GPT];
+  // (the searches of the GPT slots advance together, one step of each per LDS round trip, over the log2(nsl) + 1 steps
+  // the row's lists need: 16 lists at C3 take five round trips, where searches of NSL done one slot after the other
+  // took up to 64)
+  int top = 1;
+  while (2 * top <= nsl) top *= 2;
   auto load_round = [&](uint32_t f0) __attribute__((always_inline)) {
+    int lo[GPT];
+#pragma unroll
+    for (int g = 0; g < GPT; ++g) lo[g] = 0;
+#pragma unroll 1
+    for (int st = top; st > 0; st >>= 1) {
+      uint32_t lv[GPT];  // (every read issued, in range, before any is used: one LDS round trip per step)
+#pragma unroll
+      for (int g = 0; g < GPT; ++g) lv[g] = sh.lmax[min(lo[g] + st, nsl - 1)];
+#pragma unroll
+      for (int g = 0; g < GPT; ++g) {
+        const uint32_t f = f0 + g * MT + tid;
+        const int m = lo[g] + st;
+        lo[g] = (m < nsl && lv[g] <= f) ? m : lo[g];
+      }
+    }
+    // (every load issued, into the row's lists: a load under a condition is waited for where the condition joins,
+    // and the slots of one round then came in one after the other; the batch drops the slots past rtot)
 #pragma unroll
     for (int g = 0; g < GPT; ++g) {
       const uint32_t f = f0 + g * MT + tid;
-      int lo = 0;
-#pragma unroll
-      for (int st = NSL / 2; st > 0; st >>= 1) {
-        const int m = lo + st;
-        if (m < nsl && sh.lmax[m] <= f) lo = m;
-      }
       okr[g] = f < rtot;
-      pk[g] = okr[g] ? ld_ag(&cl0[(size_t)lo * CAPW + min((uint32_t)SPEC + f - sh.lmax[lo], (uint32_t)CAPW - 1u)])
-                     : 0ull;
+      pk[g] = ld_ag(&cl0[(size_t)lo[g] * CAPW + min((uint32_t)SPEC + f - sh.lmax[lo[g]], (uint32_t)CAPW - 1u)]);
     }
   };
   if (rtot > 0) load_round(0);
