@@ -150,8 +150,16 @@ __device__ __forceinline__ int evaluate(const RowEval &ev, const uint64_t *arr, 
   double *ee = reinterpret_cast<double *>(sh.r.tmp);
   const double M = ev.M;
   const int lane = lane_id(), w = tid >> 6;
+  // (two ranks a thread at a time: their exponentials' dependent chains overlap; an index past n reads rank 0 and its
+  // result is dropped)
 #pragma unroll 1
-  for (int i = tid; i < n; i += MT) ee[i] = exp_nonpos((double)fkey_inv(pk_key(arr[i])) - M, sh.etab);
+  for (int i = tid; i < n; i += 2 * MT) {
+    const int i1 = i + MT < n ? i + MT : 0;
+    const double e0 = exp_nonpos((double)fkey_inv(pk_key(arr[i])) - M, sh.etab);
+    const double e1 = exp_nonpos((double)fkey_inv(pk_key(arr[i1])) - M, sh.etab);
+    ee[i] = e0;
+    if (i + MT < n) ee[i + MT] = e1;
+  }
   __syncthreads();
   const int RPW = ((n + NWV - 1) / NWV + WAVE - 1) / WAVE * WAVE;  // ranks per wave (a multiple of 64, 4 RPW >= n)
   double carry = 0.0;
@@ -393,7 +401,10 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
   // and its length is its cost.
   auto batch = [&](const uint64_t(&pk)[GPT], const bool(&ok)[GPT]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int g = 0; g < GPT; ++g) sh.r.tmp[g * MT + tid] = ok[g] ? key_of_raw(pk[g], divide, Rd) : 0ull;
+    for (int g = 0; g < GPT; ++g) {  // (the key for every slot, then a select: no branch that waits for its load)
+      const uint64_t kv = key_of_raw(pk[g], divide, Rd);
+      sh.r.tmp[g * MT + tid] = ok[g] ? kv : 0ull;
+    }
     // the masses of the entries below the certified key, two at a time (independent exponentials overlap), and the
     // head bits of the thread's GPT entries
     uint32_t hb = 0;
@@ -467,7 +478,17 @@ __device__ __forceinline__ void resolve_row(const ScanArgs &a, int row, const gs
       pk[g] = ld_ag(&cl0[(size_t)lo[g] * CAPW + min((uint32_t)SPEC + f - sh.lmax[lo[g]], (uint32_t)CAPW - 1u)]);
     }
   };
-  if (rtot > 0) load_round(0);
+  // (without a second round, as many loads of in-range slots: either way GPT loads follow the speculative batch's, so
+  // that batch waits only for its own; with the round under a condition alone it waited for both)
+  if (rtot > 0) {
+    load_round(0);
+  } else {
+#pragma unroll
+    for (int g = 0; g < GPT; ++g) {
+      okr[g] = false;
+      pk[g] = ld_ag(&cl0[g]);  // (distinct slots: loads of one address would merge)
+    }
+  }
   {
     bool ok[GPT];
 #pragma unroll
