@@ -316,30 +316,50 @@ __device__ __forceinline__ void slice_groups(int s0, Ld ld, F f) {
   auto t0_of = [&](int g) { return s0 + min(g, NG - 1) * 4 * TT + tid; };  // (past the end: the last group again)
   if constexpr (RING == 2) {
     auto b0 = ld(t0_of(0));
+    __builtin_amdgcn_sched_barrier(0);
     auto b1 = ld(t0_of(1));
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll 1
     for (int g = 0; g < NG; g += 2) {
       f(t0_of(g), b0);
+      __builtin_amdgcn_sched_barrier(0);
       b0 = ld(t0_of(g + 2));
+      __builtin_amdgcn_sched_barrier(0);
       f(t0_of(g + 1), b1);
+      __builtin_amdgcn_sched_barrier(0);
       b1 = ld(t0_of(g + 3));
+      __builtin_amdgcn_sched_barrier(0);
     }
     return;
   }
+  // (the groups' loads go out in the loop's order before it too, and no step's code moves across another's loads: a
+  // loop entered with its loads issued in another order waited for all of them in every round)
   auto b0 = ld(t0_of(0));
+  __builtin_amdgcn_sched_barrier(0);
   auto b1 = ld(t0_of(1));
+  __builtin_amdgcn_sched_barrier(0);
   auto b2 = ld(t0_of(2));
+  __builtin_amdgcn_sched_barrier(0);
   auto b3 = ld(t0_of(3));
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll 1
   for (int g = 0; g < NG; g += 4) {
     f(t0_of(g), b0);
+    __builtin_amdgcn_sched_barrier(0);
     b0 = ld(t0_of(g + 4));
+    __builtin_amdgcn_sched_barrier(0);
     f(t0_of(g + 1), b1);
+    __builtin_amdgcn_sched_barrier(0);
     b1 = ld(t0_of(g + 5));
+    __builtin_amdgcn_sched_barrier(0);
     f(t0_of(g + 2), b2);
+    __builtin_amdgcn_sched_barrier(0);
     b2 = ld(t0_of(g + 6));
+    __builtin_amdgcn_sched_barrier(0);
     f(t0_of(g + 3), b3);
+    __builtin_amdgcn_sched_barrier(0);
     b3 = ld(t0_of(g + 7));
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
