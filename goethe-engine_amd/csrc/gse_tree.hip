@@ -1145,33 +1145,90 @@ __global__ __launch_bounds__(TT) __attribute__((amdgpu_waves_per_eu(DTK == GSE_F
 
 // ---- verify: the walk ------------------------------------------------------------------------------------------------
 
+// One node as the walk reads it, every load issued at once with its index in range (a load behind a branch, or one
+// whose address or loop bound is a loaded value, waits for what came before it: a chain of cache latencies per node):
+// the row's flags, the strict decision, the sampled token and the eight rows after u (indexes clamped into rows
+// [u, end); the scans stop on what they read).
+struct WalkNode {
+  uint32_t pf, inf;
+  int stok, skid, samp;
+  int p[8], t[8];
+};
+
+__device__ __forceinline__ void rows8(const TreeArgs &a, int j0, int end, int (&p)[8], int (&t)[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int j = min(j0 + k, end - 1);
+    p[k] = a.parent[j];
+    t[k] = a.token[j];
+  }
+}
+
+__device__ __forceinline__ WalkNode walk_node(const TreeArgs &a, int u, int end) {
+  WalkNode w;
+  w.pf = a.s.params[u].flags;
+  w.inf = a.s.info[u].flags;
+  w.stok = a.st[u].token;
+  w.skid = a.st[u].kid;
+  w.samp = a.sampled[u];
+  rows8(a, u + 1, end, w.p, w.t);
+  return w;
+}
+
+// node_live from the loaded flags
+__device__ __forceinline__ bool walk_live(const WalkNode &w) {
+  return (w.pf & GSE_ROW_MSS) && (w.inf & R_DONE) && !(w.inf & (R_SPECIAL | R_BAD | R_GREEDY));
+}
+
 // More kids than the round was given room for (max_kids, GSE_MAX_KIDS): find_kids dropped the later ones, so a strict
-// node's decision would not be the reference's (spec.py:91 walks every kid). rows (u, end) hold the node's request.
-__device__ __forceinline__ bool kids_over(const TreeArgs &a, int u, int end) {
+// node's decision would not be the reference's (spec.py:91 walks every kid). The kids are the rows after u with parent
+// u, before the first root (parent < 0) or end.
+__device__ __forceinline__ bool kids_over(const TreeArgs &a, int u, int end, WalkNode w) {
   int n = 0;
-  for (int j = u + 1; j < end && a.parent[j] >= 0; ++j) n += a.parent[j] == u ? 1 : 0;
+  bool go = true;
+  for (int j0 = u + 1;;) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      go = go && j0 + k < end && w.p[k] >= 0;
+      n += go && w.p[k] == u ? 1 : 0;
+    }
+    j0 += 8;
+    if (!go || j0 >= end) break;
+    rows8(a, j0, end, w.p, w.t);
+  }
   return n > a.max_kids || n > GSE_MAX_KIDS;
+}
+
+// The first kid of u holding tok among the rows (u, end), or -1; ROOT: a root (parent < 0) also ends the rows.
+template <bool ROOT>
+__device__ __forceinline__ int kid_of(const TreeArgs &a, int u, int end, int tok, WalkNode w) {
+  for (int j0 = u + 1;;) {
+    int kid = -1;
+    bool go = true;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      go = go && j0 + k < end && (!ROOT || w.p[k] >= 0);
+      if (go && kid < 0 && w.p[k] == u && w.t[k] == tok) kid = j0 + k;
+    }
+    j0 += 8;
+    if (kid >= 0 || !go || j0 >= end) return kid;
+    rows8(a, j0, end, w.p, w.t);
+  }
 }
 
 __global__ __launch_bounds__(64) void walk_kernel(TreeArgs a) {
   const int q = blockIdx.x * 64 + threadIdx.x;
   // node_token / node_kid of every node
   for (int u = q; u < a.nodes && (a.out.node_token || a.out.node_kid); u += gridDim.x * 64) {
-    const gse_row &P = a.s.params[u];
+    const WalkNode w = walk_node(a, u, a.nodes);
     int tok, kid;
-    if (P.flags & GSE_ROW_MSS) {
-      const bool live = node_live(a, u, P) && !kids_over(a, u, a.nodes);
-      tok = live ? a.st[u].token : -1;
-      kid = live ? a.st[u].kid : -1;
+    if (w.pf & GSE_ROW_MSS) {
+      const bool live = walk_live(w) && !kids_over(a, u, a.nodes, w);
+      tok = live ? w.stok : -1;
+      kid = live ? w.skid : -1;
     } else {
-      tok = a.sampled[u];
-      kid = -1;
-      if (tok >= 0)
-        for (int j = u + 1; j < a.nodes && a.parent[j] >= 0; ++j)
-          if (a.parent[j] == u && a.token[j] == tok) {
-            kid = j;
-            break;
-          }
+      tok = w.samp;
+      kid = tok >= 0 ? kid_of<true>(a, u, a.nodes, tok, w) : -1;
     }
     if (a.out.node_token) a.out.node_token[u] = tok;
     if (a.out.node_kid) a.out.node_kid[u] = kid;
@@ -1182,25 +1239,20 @@ __global__ __launch_bounds__(64) void walk_kernel(TreeArgs a) {
   int n = 0;
   uint32_t status = GSE_WALK_OK;
   for (int step = 0; step <= end - a.anchor[q] && u >= 0 && u < end; ++step) {
-    const gse_row &P = a.s.params[u];
+    const WalkNode w = walk_node(a, u, end);
     int tok, kid = -1;
-    if (P.flags & GSE_ROW_MSS) {
-      if (kids_over(a, u, end)) {  // (the node's decision is not the reference's: the walk stops before it)
+    if (w.pf & GSE_ROW_MSS) {
+      if (kids_over(a, u, end, w)) {  // (the node's decision is not the reference's: the walk stops before it)
         status = GSE_WALK_KIDS;
         if (n < a.out.emit_ld) a.out.emit_nodes[(int64_t)q * a.out.emit_ld + n] = u;
         break;
       }
-      const bool live = node_live(a, u, P);
-      tok = live ? a.st[u].token : -1;
-      kid = live ? a.st[u].kid : -1;
+      const bool live = walk_live(w);
+      tok = live ? w.stok : -1;
+      kid = live ? w.skid : -1;
     } else {
-      tok = a.sampled[u];
-      if (tok >= 0)
-        for (int j = u + 1; j < end; ++j)
-          if (a.parent[j] == u && a.token[j] == tok) {
-            kid = j;
-            break;
-          }
+      tok = w.samp;
+      if (tok >= 0) kid = kid_of<false>(a, u, end, tok, w);
     }
     if (tok < 0) {  // the path holds the node (engine.py:280-288 appends the kid before its row is decided)
       status = GSE_WALK_ERROR;
