@@ -966,16 +966,19 @@ __global__ __launch_bounds__(TT) void tkid0_kernel(TreeArgs a) {
   __shared__ NodeShared ns;
   const int u = blockIdx.x;
   const gse_row P = a.s.params[u];
-  if (!node_live(a, u, P)) return;
   TreeNode &nd = a.st[u];
-  if ((int)nd.next != 1) return;
+  // the row's flags, its state and its target fields in one round of loads (a load behind a branch waits for the
+  // branch's own): node_live in place
+  const uint32_t inf = a.s.info[u].flags;
+  const int next = (int)nd.next;
+  const Tgt g = tgt_of(a, u, P);
+  if (!(P.flags & GSE_ROW_MSS) || !(inf & R_DONE) || (inf & (R_SPECIAL | R_BAD | R_GREEDY)) || next != 1) return;
   load_etab(sh);
   load_node(a, u, ns);  // (its barrier publishes the table)
   if (ns.k.n == 0) {  // (no kids: pass 1 draws)
     if (threadIdx.x == 0) pass_add(a, 1, u);
     return;
   }
-  const Tgt g = tgt_of(a, u, P);
   const bool acc = test_kid(a, P, g, ns, 0, sh);
   if (threadIdx.x == 0) {
     if (acc) {
