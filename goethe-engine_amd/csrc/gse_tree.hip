@@ -996,10 +996,11 @@ template <int DTK, int QKK>
 __device__ __forceinline__ void tpass_item(const TreeArgs &a, int r, int u, int s, TreeShared &sh, NodeShared &ns) {
   const int tid = threadIdx.x;
   const gse_row P = a.s.params[u];
-  if (!node_live(a, u, P)) return;
   TreeNode &nd = a.st[u];
-  if ((int)nd.next != r) return;
+  const uint32_t inf = a.s.info[u].flags;  // (node_live in place: one round of loads, as in tkid0_kernel)
+  const int next = (int)nd.next;
   const Tgt g = tgt_of(a, u, P);
+  if (!(P.flags & GSE_ROW_MSS) || !(inf & R_DONE) || (inf & (R_SPECIAL | R_BAD | R_GREEDY)) || next != r) return;
   const int V = a.s.V, s0 = s * TS, s1 = min(V, s0 + TS);
   load_etab(sh);
   load_node(a, u, ns);  // (its barrier publishes the table)
