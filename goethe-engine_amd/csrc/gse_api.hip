@@ -193,9 +193,11 @@ gse::ScanArgs make_args(gse_handle *h, const gse_batch &b, int mode) {
   // A call with no histories and no masks keeps no part-sized tables in LDS: its parts may be twice as long (a large
   // batch then streams its rows in half the workgroups, each with one prologue and one first-chunk latency for twice
   // the tokens), and a part's listing target and valve grow with its length, so that a row lists as many candidates.
-  parts(h, b.rows, b.vocab, (!b.hist && !b.mask) ? (uint32_t)gse::PTOK_PLAIN : (uint32_t)gse::PTOK, &a.nparts, &a.plen);
-  a.kt = a.plen > gse::PTOK ? (int)(((int64_t)gse::KT * a.plen + gse::PTOK - 1) / gse::PTOK) : gse::KT;
-  a.vfirst = (int)((int64_t)gse::CAPW / 4 * a.kt / gse::KT) + 1;
+  const bool plain = !b.hist && !b.mask;
+  parts(h, b.rows, b.vocab, plain ? (uint32_t)gse::PTOK_PLAIN : (uint32_t)gse::PTOK, &a.nparts, &a.plen);
+  a.kt = a.plen > gse::PTOK ? (int)(((int64_t)gse::KT * a.plen + gse::PTOK - 1) / gse::PTOK)
+                            : plain ? gse::KT : gse::KT_HM;
+  a.vfirst = (int)((int64_t)gse::CAPW / 4 * a.kt / gse::KT_VALVE) + 1;
   a.mode = mode;
   a.xcd_map = 1;
   a.force_exact = (b.flags & GSE_BATCH_EXACT) ? 1 : 0;

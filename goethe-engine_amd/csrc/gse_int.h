@@ -49,7 +49,10 @@ constexpr int MAXP = 64;    // parts per row
 constexpr int PTOK = 65536; // tokens per part, at most
 constexpr int PTOK_PLAIN = 131072;  // tokens per part, at most, in a call with no histories and no masks (no part-sized
                                     // LDS tables: the parts are twice as long and the listing targets twice as high)
-constexpr int KT = 222;       // tokens of a part of at most PTOK tokens its listing threshold aims to leave above it
+constexpr int KT = 200;       // tokens of a part of at most PTOK tokens its listing threshold aims to leave above it
+constexpr int KT_HM = 150;    // the same in a call with histories or masks: its rows' heads certify with shorter lists,
+                              // which the resolve gathers and sorts faster (much lower and some rows need the exact path)
+constexpr int KT_VALVE = 222; // the listing target at which a part's first-chunk valve is CAPW / 4 (scaled with kt)
 constexpr int PCHUNK = 1024;  // part lengths are multiples of this (one wave chunk)
 constexpr int PMIN = 8192;    // tokens per part, at least, when a small batch is split to fill the device: every part
                               // lists its own candidates, so more parts make a longer row resolve

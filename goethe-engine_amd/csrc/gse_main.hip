@@ -15,9 +15,10 @@
 // wave does not list, from v_exp_f32 with a rigorous error bound (rescaled in fp64 when a lane's maximum rises). The
 // row history's tokens of the part (penalties: counts from an LDS table indexed by rank) take a side pass with the same
 // arithmetic. The part's listing threshold is the kp-th largest of the 256 lane maxima of its waves' first chunks (to
-// 16 key bits; kp aims at a.kt tokens of the part above it (KT, or more in proportion for a part longer than PTOK),
-// scaled by the exact counts of allowed tokens in the sample and in the part); a wave whose list passes a.vfirst
-// (a quarter of its capacity at KT) raises its own to the KV-th largest of its running lane maxima. Every element at or above the threshold in force when it is processed is listed (z bits, id);
+// 16 key bits; kp aims at a.kt tokens of the part above it (KT, KT_HM in a call with histories or masks, or more in
+// proportion for a part longer than PTOK), scaled by the exact counts of allowed tokens in the sample and in the part);
+// a wave whose list passes a.vfirst (a quarter of its capacity at KT_VALVE) raises its own to the KV-th largest of its
+// running lane maxima. Every element at or above the threshold in force when it is processed is listed (z bits, id);
 // thresholds only rise, so a wave's list certifies its top elements down to its final threshold.
 //
 // Row resolve: the union of the waves' lists cut at the largest certified key is the row's certified head: exactly its
@@ -1171,8 +1172,8 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     // The listing threshold: the rank-kp largest of the 256 lane maxima of the waves' first chunks (a 2048-token
     // sample). kp is scaled so that about T tokens of the part lie above it: kp = T * (allowed tokens in the sample) /
     // (allowed tokens in the part), counted exactly, so that a mask whose allowed tokens cluster in runs does not skew
-    // it. T = a.kt (222 for a part of at most PTOK tokens), or 3 top_k + 32 (at most 2 a.kt) for rows that keep at
-    // most top_k elements.
+    // it. T = a.kt (200 for a part of at most PTOK tokens, 150 in a call with histories or masks), or 3 top_k + 32 (at
+    // most 2 a.kt) for rows that keep at most top_k elements.
     uint32_t as = 0;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) as += x0[i] > -INFINITY ? 1u : 0u;
