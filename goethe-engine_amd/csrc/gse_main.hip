@@ -1172,7 +1172,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
     // The listing threshold: the rank-kp largest of the 256 lane maxima of the waves' first chunks (a 2048-token
     // sample). kp is scaled so that about T tokens of the part lie above it: kp = T * (allowed tokens in the sample) /
     // (allowed tokens in the part), counted exactly, so that a mask whose allowed tokens cluster in runs does not skew
-    // it. T = a.kt (200 for a part of at most PTOK tokens, 150 in a call with histories or masks), or 3 top_k + 32 (at
+    // it. T = a.kt (200 for a part of at most PTOK tokens, 150 in a call with histories or masks), or 2 top_k + 32 (at
     // most 2 a.kt) for rows that keep at most top_k elements.
     uint32_t as = 0;
 #pragma unroll
@@ -1194,7 +1194,7 @@ __device__ __forceinline__ bool part_body(const ScanArgs &a, const gse_row &P, c
       Ap += sh.wflags[q];
     }
     const uint32_t kt = (uint32_t)a.kt;
-    const uint32_t T = P.top_k > 0 ? min(2u * kt, (uint32_t)(3 * max(P.top_k, nlp_of(a, P)) + 32)) : kt;
+    const uint32_t T = P.top_k > 0 ? min(2u * kt, (uint32_t)(2 * max(P.top_k, nlp_of(a, P)) + 32)) : kt;
     // (a sample with few allowed tokens estimates nothing: then the lowest lane maximum, and the valve bounds the lists)
     const uint32_t kp = As < 16u ? max(act, 1u) : max(1u, min(act, (T * As + Ap - 1) / max(Ap, 1u)));  // (T As < 2^22)
     uint32_t r = 0;
