@@ -727,8 +727,9 @@ __global__ __launch_bounds__(TT) void tstats_kernel(TreeArgs a) {
   if (y < a.nodes) {
     const int u = y;
     const gse_row P = a.s.params[u];
-    if (!node_live(a, u, P)) return;
+    const uint32_t inf = a.s.info[u].flags;  // (node_live in place: one round of loads, as in tkid0_kernel)
     const Tgt g = tgt_of(a, u, P);
+    if (!(P.flags & GSE_ROW_MSS) || !(inf & R_DONE) || (inf & (R_SPECIAL | R_BAD | R_GREEDY))) return;
     load_etab(sh);
     if (g.c.pen) build_counts(g.c, a.s.hist, s0, sh.cnt);  // (its barriers publish the table)
     else __syncthreads();
